@@ -1,0 +1,153 @@
+/* qmatvec.h -- y = W x for GGUF weight blocks on MI355X (gfx950), the drop-in for the reference's
+ * src/qmatvec.h (aardbeiplantje/PURHIE). Same symbols, argument meaning, buffer layout and error
+ * convention; the kernels are this library's own wave64 HIP code (libpurhie_qmv.so), linked in, so
+ * no code object is loaded by path.
+ *
+ * Weights are HBM-resident: W is a device pointer to N rows of row_bytes = qt_row_size(type, K) bytes
+ * in the unchanged GGUF block layout. All launches are asynchronous on `stream` (0 = the null stream)
+ * with no internal synchronisation. Errors: hipErrorInvalidDeviceFunction (no kernel for this type /
+ * shape), hipErrorInvalidValue (bad shape, alignment, capacity); launch errors pass through.
+ *
+ * Types with int8 kernels: Q8_0 (8), Q4_K (12), Q6_K (14), Q4_0_ROCMFP4 (100), Q4_0_ROCMFP4_FAST (101).
+ */
+#ifndef PURHIE_QMATVEC_H
+#define PURHIE_QMATVEC_H
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* replaces src/qmatvec.h:17-18. The reference loads a code object from co_path; here the kernels are
+ * part of the library and co_path is ignored. Returns 0 (a HIP device is present) or -1. Idempotent. */
+int qmatvec_init(const char *co_path);
+void qmatvec_free(void);
+
+/* replaces src/qmatvec.h:24-26: NVFP4-style output scale registry (the outputs of launches on the
+ * matrix at W are multiplied by s[0], or by s[e] for expert e of n stacked experts). s is read on the
+ * host at launch time. Returns 0 or -1. */
+int qmatvec_set_out_scale(const void *owner, const void *W, size_t bytes, const float *s, int n);
+void qmatvec_drop_out_scales(const void *owner);
+
+/* replaces src/qmatvec.h:29: 1 if a float-activation matvec exists for the type (none here: the
+ * path is the int8 one below) */
+int qmatvec_supported(int type);
+
+/* replaces src/qmatvec.h:49-54 (mode flags). Prefill mode routes every batch size to the GEMM
+ * kernels (so a row's sums do not depend on how the prompt was cut into batches). */
+void qmatvec_set_prefill(int on);
+int qmatvec_prefill(void);
+void qmatvec_set_prefill_fp32(int on);
+
+/* ---------------------------------------------------------------- int8 path
+ * The activation is quantized once (qmatvec_quantize) into both of ggml's CPU formats, Q8_0 (32-value
+ * blocks, ROCmFP4 / Q8_0 weights) and Q8_K (256-value blocks, K-quants), bit-identical to the
+ * reference's src/q8_device.h:54-104. Layout of qmatvec_q8 (src/qmatvec.h:82-93, src/qmatvec.cpp:395-419). */
+typedef struct qmatvec_q8 {
+    int8_t *q0;    /* Q8_0 values [K] */
+    float *d0;     /* Q8_0 scales [K / 32], fp16-rounded */
+    int8_t *qK;    /* Q8_K values [K] */
+    float *dK;     /* Q8_K scales [K / 256] */
+    int32_t *bsK;  /* Q8_K sums of every 16 values [K / 16] */
+    int32_t *s0;   /* per 32 values: fp16(d * sum of the block's q) as float bits */
+    int max_k;
+    uint16_t *xh;  /* optional 16-bit copy (unused by this library's int8 kernels) */
+    int xh_bf16;
+} qmatvec_q8;
+
+typedef struct qmatvec_q8_out {
+    int8_t *q0;
+    float *d0;
+    int8_t *qK;
+    float *dK;
+    int32_t *bsK;
+    int32_t *s0;
+    uint16_t *xh;
+    int xh_bf16;
+} qmatvec_q8_out;
+
+static inline qmatvec_q8_out qmatvec_q8_outputs(const qmatvec_q8 *q) {
+    qmatvec_q8_out o = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (q) {
+        o.q0 = q->q0;
+        o.d0 = q->d0;
+        o.qK = q->qK;
+        o.dK = q->dK;
+        o.bsK = q->bsK;
+        o.s0 = q->s0;
+        o.xh = q->xh;
+        o.xh_bf16 = q->xh_bf16;
+    }
+    return o;
+}
+
+/* replaces src/qmatvec.h:118-119: bytes for vectors of up to max_k values (max_k % 256 == 0), and
+ * binding a qmatvec_q8 to such device memory (16-byte aligned) */
+size_t qmatvec_q8_bytes(int max_k);
+void qmatvec_q8_bind(qmatvec_q8 *q, void *mem, int max_k);
+
+/* replaces src/qmatvec.h:123: 1 if an int8 kernel handles the type at this K (Q8_0 / ROCmFP4: K % 64,
+ * FAST: K % 128, K-quants: K % 256) */
+int qmatvec_q8_supported(int type, int K);
+
+/* replaces src/qmatvec.h:127: x[K] (device) -> q, both formats. K % 32 == 0, K <= q->max_k. */
+hipError_t qmatvec_quantize(const float *x, int K, const qmatvec_q8 *q, hipStream_t stream);
+
+/* replaces src/qmatvec.h:130-131: y = W x with x given by its quantized form */
+hipError_t qmatvec_launch_q8(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N, int K,
+                             hipStream_t stream);
+
+/* replaces src/qmatvec.h:134-135: y = W x (N rows), y2 = W2 x (N2 rows) in one launch */
+hipError_t qmatvec_launch_q8_pair(int type, const void *W, int N, float *y, const void *W2, int N2, float *y2,
+                                  size_t row_bytes, const qmatvec_q8 *q, int K, hipStream_t stream);
+
+/* replaces src/qmatvec.h:144-152: n (1..4) matvecs of one type and K on the same input in one launch;
+ * the _t form takes T (1..4) tokens (input rows t of q, output rows ys[i] + t * Ns[i]), reading the
+ * weights once, each token's result equal to its single-token launch bit for bit */
+int qmatvec_q8_few_supported(int type, int K, int T);
+hipError_t qmatvec_launch_q8_multi_t(int type, int n, const void *const *Ws, const int *Ns, float *const *ys,
+                                     size_t row_bytes, const qmatvec_q8 *q, int K, int T, hipStream_t stream);
+hipError_t qmatvec_launch_q8_multi(int type, int n, const void *const *Ws, const int *Ns, float *const *ys,
+                                   size_t row_bytes, const qmatvec_q8 *q, int K, hipStream_t stream);
+
+/* replaces src/qmatvec.h:157-158: Y[t] = W X[t] for T tokens, q the T rows quantized as one [T * K]
+ * vector, row t of the result at y + t * ldy */
+hipError_t qmatvec_launch_q8_batch(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y,
+                                   long long ldy, int N, int K, int T, hipStream_t stream);
+
+/* replaces src/qmatvec.h:167-179: MoE expert-indexed matvecs. W stacks every expert's N rows. For
+ * token t and slot j < n_used, expert e = ids[t * n_used + j] multiplies input row t (x_per_slot = 0)
+ * or t * n_used + j (x_per_slot = 1) into row t * n_used + j of y; an id of -1 selects Wx (W2x). */
+hipError_t qmatvec_launch_q8_id(int type, const void *W, size_t row_bytes, const int32_t *ids, int n_used,
+                                int x_per_slot, const qmatvec_q8 *q, float *y, int N, int K, int T, hipStream_t stream);
+hipError_t qmatvec_launch_q8_id_pair(int type, const void *W, const void *W2, size_t row_bytes, const int32_t *ids,
+                                     int n_used, int x_per_slot, const qmatvec_q8 *q, float *y, float *y2, int N, int K,
+                                     int T, hipStream_t stream);
+hipError_t qmatvec_launch_q8_id_x(int type, const void *W, const void *W2, const void *Wx, const void *W2x,
+                                  size_t row_bytes, const int32_t *ids, int n_used, int x_per_slot,
+                                  const qmatvec_q8 *q, float *y, float *y2, int N, int K, int T, hipStream_t stream);
+
+/* replaces src/qmatvec.h:189-195: MoE prefill over gpu_moe_group's expert tiles (tile k: expert
+ * tile_e[k], entries tile_start[k] .. + tile_n[k] - 1 of in_rows / out_rows) */
+int qmatvec_id_batch_tile(int type, int N, int K);
+int qmatvec_q8_id_batch_supported(int type, int K);
+hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N,
+                                      int K, int max_tiles, int tile, const int32_t *n_tiles, const int32_t *tile_e,
+                                      const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
+                                      const int32_t *out_rows, hipStream_t stream);
+
+/* No counterpart in the reference: a test hook for the parity tests. The integer dot of every weight
+ * scale group (Q8_0 / FAST / Q4_K: 32 values, ROCmFP4 / Q6_K: 16) of every row against the quantized
+ * activation, computed by the same device decoders as the matvec kernels: out[N][K / group]. Q4_K / Q6_K
+ * dot the raw levels (0..15 / 0..63). */
+hipError_t qmatvec_debug_block_dots(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, int32_t *out,
+                                    int N, int K, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PURHIE_QMATVEC_H */

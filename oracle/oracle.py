@@ -1,0 +1,272 @@
+"""ctypes binding of the C oracle (oracle.c) and of the compiled reference CPU sources (_ref/libref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+leg, as the checker of the HIP product. Nothing in purhie_amd/ imports this module.
+"""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+REF_PATH = os.path.join(_HERE, "_ref", "libref.so")
+
+Q8_0, Q4_K, Q6_K, FP4, FAST, F32, F16, BF16 = 8, 12, 14, 100, 101, 0, 1, 30
+KQ = (Q4_K, Q6_K)
+BLOCK = {Q8_0: 32, Q4_K: 256, Q6_K: 256, FP4: 32, FAST: 32, F32: 1, F16: 1, BF16: 1}
+BYTES = {Q8_0: 34, Q4_K: 144, Q6_K: 210, FP4: 18, FAST: 17, F32: 4, F16: 2, BF16: 2}
+GROUP = {Q8_0: 32, FP4: 16, FAST: 32, Q4_K: 32, Q6_K: 16}
+
+_lib = None
+_ref = None
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        vp, i64, i32, sz = C.c_void_p, C.c_int64, C.c_int, C.c_size_t
+        L.orc_f32_to_f16.restype = C.c_uint16
+        L.orc_f32_to_f16.argtypes = [C.c_float]
+        L.orc_f16_to_f32.restype = C.c_float
+        L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_ue4m3_half.restype = C.c_float
+        L.orc_ue4m3_half.argtypes = [C.c_uint8]
+        L.orc_ue4m3_fp4common.restype = C.c_float
+        L.orc_ue4m3_fp4common.argtypes = [C.c_uint8]
+        L.orc_f32_to_f16_n.argtypes = [vp, vp, i64]
+        L.orc_f16_to_f32_n.argtypes = [vp, vp, i64]
+        L.orc_row_size.restype = sz
+        L.orc_row_size.argtypes = [i32, i64]
+        L.orc_to_float.argtypes = [i32, vp, vp, i64]
+        L.orc_quantize.argtypes = [i32, vp, vp, i64, i64, i32]
+        L.orc_quantize_q8_0.argtypes = [vp, i64, vp, vp, vp]
+        L.orc_quantize_q8_k.argtypes = [vp, i64, vp, vp, vp]
+        L.orc_block_dots.argtypes = [i32, vp, sz, i32, i32, vp, vp]
+        L.orc_matvec.argtypes = [i32, vp, sz, i32, i32, vp, vp, vp, vp, vp, vp, i32]
+        L.orc_cpu_q8_0_quantize.argtypes = [vp, i32, vp, vp]
+        L.orc_cpu_matvec_fp4fast_q8.argtypes = [vp, sz, i32, i32, vp, vp, vp]
+        L.orc_cpu_matvec_q8_q8.argtypes = [vp, sz, i32, i32, vp, vp, vp]
+        L.orc_cpu_expert_ffn.argtypes = [vp, vp, sz, vp, sz, i32, i32, vp, vp, C.c_float, vp]
+        L.orc_moe_router.argtypes = [vp, i32, i32, i32, vp, vp]
+        L.orc_moe_group.restype = i32
+        L.orc_moe_group.argtypes = [vp, i32, i32, i32, i32, vp, vp, vp, vp, vp]
+        L.orc_moe_combine.argtypes = [vp, vp, vp, i32, i32, i32]
+        L.orc_swiglu.argtypes = [vp, vp, vp, i64]
+        L.orc_gemm_act_fp4.argtypes = [vp, vp, vp, vp, i32, i32, i32]
+        _lib = L
+    return _lib
+
+
+def row_size(t, k):
+    return int(lib().orc_row_size(t, k))
+
+
+def f32_to_f16(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    h = np.empty(x.shape, dtype=np.uint16)
+    lib().orc_f32_to_f16_n(_ptr(x), _ptr(h), x.size)
+    return h
+
+
+def f16_to_f32(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    x = np.empty(h.shape, dtype=np.float32)
+    lib().orc_f16_to_f32_n(_ptr(h), _ptr(x), h.size)
+    return x
+
+
+def quantize(t, x, n_threads=0):
+    """rows of fp32 x[nrows][k] -> uint8 [nrows][row_size]"""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    nrows, k = x.shape
+    out = np.zeros((nrows, row_size(t, k)), dtype=np.uint8)
+    assert lib().orc_quantize(t, _ptr(x), _ptr(out), nrows, k, n_threads) == 0
+    return out
+
+
+def to_float(t, w, k):
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    nrows = w.size // row_size(t, k)
+    y = np.empty((nrows, k), dtype=np.float32)
+    for r in range(nrows):
+        assert lib().orc_to_float(t, _ptr(w[r]), _ptr(y[r]), k) == 0
+    return y
+
+
+def quantize_act(x, kq):
+    """one or more rows (flattened) -> dict(q, d, bs, s0) in the reference's Q8_0 or Q8_K form"""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    k = x.size
+    q = np.zeros(k, dtype=np.int8)
+    if kq:
+        d = np.zeros(k // 256, dtype=np.float32)
+        bs = np.zeros(k // 16, dtype=np.int32)
+        lib().orc_quantize_q8_k(_ptr(x), k, _ptr(q), _ptr(d), _ptr(bs))
+        return dict(q=q, d=d, bs=bs)
+    d = np.zeros(k // 32, dtype=np.float32)
+    s0 = np.zeros(k // 32, dtype=np.int32)
+    lib().orc_quantize_q8_0(_ptr(x), k, _ptr(q), _ptr(d), _ptr(s0))
+    return dict(q=q, d=d, s0=s0)
+
+
+def block_dots(t, W, N, K, q):
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    out = np.zeros((N, K // GROUP[t]), dtype=np.int32)
+    assert lib().orc_block_dots(t, _ptr(W), row_size(t, K), N, K, _ptr(q), _ptr(out)) == 0
+    return out
+
+
+def matvec(t, W, N, K, act, want_ref=True, n_threads=0):
+    """y (fp32, reference CPU order), ref (double from dequantized values), mag (sum |w x|)"""
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    y = np.zeros(N, dtype=np.float32)
+    ref = np.zeros(N, dtype=np.float64) if want_ref else None
+    mag = np.zeros(N, dtype=np.float64)
+    bs = act.get("bs")
+    assert lib().orc_matvec(t, _ptr(W), row_size(t, K), N, K, _ptr(act["q"]), _ptr(act["d"]),
+                            _ptr(bs), _ptr(y), _ptr(ref), _ptr(mag), n_threads) == 0
+    return y, ref, mag
+
+
+def moe_router(logits, n_used):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    T, E = logits.shape
+    ids = np.zeros((T, n_used), dtype=np.int32)
+    wts = np.zeros((T, n_used), dtype=np.float32)
+    lib().orc_moe_router(_ptr(logits), T, E, n_used, _ptr(ids), _ptr(wts))
+    return ids, wts
+
+
+def moe_group(ids, n_expert, tile):
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    T, n_used = ids.shape
+    n = T * n_used
+    mt = min(n, n_expert + n // tile)
+    tok = np.zeros(n, dtype=np.int32)
+    pair = np.zeros(n, dtype=np.int32)
+    te = np.zeros(mt, dtype=np.int32)
+    ts = np.zeros(mt, dtype=np.int32)
+    tn = np.zeros(mt, dtype=np.int32)
+    nt = lib().orc_moe_group(_ptr(ids), T, n_used, n_expert, tile, _ptr(tok), _ptr(pair), _ptr(te), _ptr(ts),
+                             _ptr(tn))
+    return dict(tok_rows=tok, pair_rows=pair, n_tiles=nt, tile_e=te[:nt], tile_start=ts[:nt], tile_n=tn[:nt])
+
+
+def moe_combine(down, wts):
+    down = np.ascontiguousarray(down, dtype=np.float32)
+    T, n_used, n = down.shape
+    out = np.zeros((T, n), dtype=np.float32)
+    lib().orc_moe_combine(_ptr(down), _ptr(np.ascontiguousarray(wts, dtype=np.float32)), _ptr(out), n_used, n, T)
+    return out
+
+
+def swiglu(g, u):
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    u = np.ascontiguousarray(u, dtype=np.float32)
+    out = np.empty_like(g)
+    lib().orc_swiglu(_ptr(g), _ptr(u), _ptr(out), g.size)
+    return out
+
+
+def gemm_act_fp4(A16, W, Ws, M, N, K):
+    C_ = np.zeros((M, N), dtype=np.float32)
+    lib().orc_gemm_act_fp4(_ptr(np.ascontiguousarray(A16, np.uint16)), _ptr(np.ascontiguousarray(W, np.uint8)),
+                           _ptr(np.ascontiguousarray(Ws, np.uint8)), _ptr(C_), M, N, K)
+    return C_
+
+
+def cpu_expert_ffn(gate, up, down, FE, E, q, d, limit=0.0):
+    out = np.zeros(E, dtype=np.float32)
+    lib().orc_cpu_expert_ffn(_ptr(gate), _ptr(up), row_size(FAST, E), _ptr(down), row_size(FAST, FE), FE, E,
+                             _ptr(q), _ptr(d), limit, _ptr(out))
+    return out
+
+
+# ---------------------------------------------------------------- the compiled reference (_ref)
+
+def ref_available():
+    return os.path.exists(REF_PATH)
+
+
+def ref():
+    """the reference's own CPU sources built by oracle/ref.mk (quant_types, quantize, expert_cpu)"""
+    global _ref
+    if _ref is None:
+        R = C.CDLL(REF_PATH)
+        vp, i64, i32, sz = C.c_void_p, C.c_int64, C.c_int, C.c_size_t
+        R.qt_row_size.restype = sz
+        R.qt_row_size.argtypes = [i32, i64]
+        R.qt_to_float.argtypes = [i32, vp, vp, i64]
+        R.qt_vec_dot_q8k.argtypes = [i32]
+        R.qt_fp16_to_fp32.restype = C.c_float
+        R.qt_fp16_to_fp32.argtypes = [C.c_uint16]
+        R.qz_fp32_to_fp16.restype = C.c_uint16
+        R.qz_fp32_to_fp16.argtypes = [C.c_float]
+        R.qz_quantize.argtypes = [i32, vp, i32, vp, i64, i64, i32, C.c_char_p, sz]
+        R.qz_supported.argtypes = [i32]
+        getattr(R, "_Z17cpu_q8_0_quantizePKfiPaPf").argtypes = [vp, i32, vp, vp]
+        getattr(R, "_Z21cpu_matvec_fp4fast_q8PKvmiiPKaPKfPf").argtypes = [vp, sz, i32, i32, vp, vp, vp]
+        getattr(R, "_Z16cpu_matvec_q8_q8PKvmiiPKaPKfPf").argtypes = [vp, sz, i32, i32, vp, vp, vp]
+        getattr(R, "_Z14cpu_expert_ffnPKvS0_mS0_miiPKaPKffPfS5_").argtypes = [vp, vp, sz, vp, sz, i32, i32, vp, vp,
+                                                                           C.c_float, vp, vp]
+        _ref = R
+    return _ref
+
+
+def ref_quantize(t, x, n_threads=1):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    nrows, k = x.shape
+    out = np.zeros((nrows, int(ref().qt_row_size(t, k))), dtype=np.uint8)
+    err = C.create_string_buffer(256)
+    rc = ref().qz_quantize(t, _ptr(out), F32, _ptr(x), nrows, k, n_threads, err, 256)
+    assert rc == 0, err.value
+    return out
+
+
+def ref_to_float(t, w, k):
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    rb = int(ref().qt_row_size(t, k))
+    nrows = w.size // rb
+    y = np.empty((nrows, k), dtype=np.float32)
+    for r in range(nrows):
+        assert ref().qt_to_float(t, _ptr(w.reshape(nrows, rb)[r]), _ptr(y[r]), k) == 0
+    return y
+
+
+def ref_cpu_q8_0_quantize(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    q = np.zeros(x.size, dtype=np.int8)
+    d = np.zeros(x.size // 32, dtype=np.float32)
+    getattr(ref(), "_Z17cpu_q8_0_quantizePKfiPaPf")(_ptr(x), x.size, _ptr(q), _ptr(d))
+    return q, d
+
+
+def ref_cpu_matvec(t, W, N, K, q, d):
+    y = np.zeros(N, dtype=np.float32)
+    fn = "_Z21cpu_matvec_fp4fast_q8PKvmiiPKaPKfPf" if t == FAST else "_Z16cpu_matvec_q8_q8PKvmiiPKaPKfPf"
+    getattr(ref(), fn)(_ptr(np.ascontiguousarray(W, np.uint8)), int(ref().qt_row_size(t, K)), N, K, _ptr(q), _ptr(d),
+                       _ptr(y))
+    return y
+
+
+def ref_cpu_expert_ffn(gate, up, down, FE, E, q, d, limit=0.0):
+    out = np.zeros(E, dtype=np.float32)
+    work = np.zeros(3 * FE + FE // 4 + 16, dtype=np.float32)
+    getattr(ref(), "_Z14cpu_expert_ffnPKvS0_mS0_miiPKaPKffPfS5_")(
+        _ptr(gate), _ptr(up), int(ref().qt_row_size(FAST, E)), _ptr(down), int(ref().qt_row_size(FAST, FE)), FE, E,
+        _ptr(q), _ptr(d), limit, _ptr(out), _ptr(work))
+    return out

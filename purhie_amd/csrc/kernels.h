@@ -1,0 +1,64 @@
+// kernels.h -- internal launch interface between the C-ABI host layer (qmatvec.cpp, ...) and the HIP
+// kernels of libpurhie_qmv. Not installed: the public interface is include/*.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pq {
+
+// ggml type ids of the path's weight formats
+constexpr int TY_Q8_0 = 8, TY_Q4_K = 12, TY_Q6_K = 14, TY_FP4 = 100, TY_FAST = 101;
+
+// quantized activation output pointers (the layout of qmatvec_q8)
+struct Q8Ptrs {
+    int8_t *q0;
+    float *d0;
+    int8_t *qK;
+    float *dK;
+    int32_t *bsK;
+    int32_t *s0;
+};
+
+hipError_t launch_quantize_q8(const float *x, int n, const Q8Ptrs &o, hipStream_t stream);
+
+// Decode matvec over up to 4 stacked matrices of one type and K, T (1..4) tokens. Rows [bound[i-1],
+// bound[i]) of the launch come from W[i] and go to y[i] (token t at y[i] + t * ystride[i]).
+struct MvArgs {
+    const uint8_t *W[4];
+    float *y[4];
+    int bound[4];
+    long long ystride[4];
+    float osc[4];
+    long long row_bytes;
+    const int8_t *q;     // token 0's quantized activation (Q8_0 or Q8_K values); token t at q + t * K
+    const float *d;      // its scales; token t at d + t * (K / act block)
+    const int32_t *bs;   // Q8_K group sums (K-quants); token t at bs + t * (K / 16)
+    int Nt, K, L, T;
+};
+hipError_t launch_matvec(int type, const MvArgs &a, hipStream_t stream);
+
+// MoE expert-indexed matvec (decode): grid (row groups, n_used * nmat, T)
+struct MvIdArgs {
+    const uint8_t *W[2];   // stacked experts of the first and second matrix
+    const uint8_t *Wx[2];  // the matrices an id of -1 selects
+    float *y[2];
+    const float *es[2];    // per-expert output scales (null: s[m])
+    float s[2], sx[2];
+    long long row_bytes;
+    const int32_t *ids;
+    const int8_t *q;
+    const float *d;
+    const int32_t *bs;
+    int n_used, x_per_slot, N, K, L, nmat, T;
+};
+hipError_t launch_matvec_id(int type, const MvIdArgs &a, hipStream_t stream);
+
+// per-scale-group integer dots (test hook)
+hipError_t launch_block_dots(int type, const uint8_t *W, long long row_bytes, const int8_t *q, int32_t *out, int N,
+                             int K, hipStream_t stream);
+
+// lanes per row the decode kernels use for a matrix of K columns and `rows` rows in total
+int matvec_lanes(int type, int K, long long rows);
+
+}  // namespace pq

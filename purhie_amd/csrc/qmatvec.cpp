@@ -1,0 +1,322 @@
+// qmatvec.cpp -- the C ABI of include/qmatvec.h over this library's HIP kernels.
+//
+// Host-side dispatch mirrors the reference's src/qmatvec.cpp (argument checks, error codes, buffer
+// layout of qmatvec_q8, the output-scale registry); the launch geometry is this library's own
+// (wave64 kernels, lanes per row chosen per shape, activation staged in LDS).
+#include "../../include/qmatvec.h"
+#include "../../include/quant_types.h"
+#include "kernels.h"
+
+#include <atomic>
+#include <mutex>
+#include <stdlib.h>
+#include <string.h>
+#include <vector>
+
+using namespace pq;
+
+namespace {
+
+bool is_int8_type(int t) { return t == TY_Q8_0 || t == TY_Q4_K || t == TY_Q6_K || t == TY_FP4 || t == TY_FAST; }
+bool reads_q8k(int t) { return t == TY_Q4_K || t == TY_Q6_K; }
+int act_blk(int t) { return reads_q8k(t) ? 256 : 32; }
+
+// required K multiple of each int8 kernel (src/qmatvec.cpp:423-429)
+int k_multiple(int t) {
+    switch (t) {
+    case TY_Q8_0: case TY_FP4: return 64;
+    case TY_FAST: return 128;
+    case TY_Q4_K: case TY_Q6_K: return 256;
+    }
+    return 0;
+}
+
+// weight base alignment the kernels' loads need (Q4_K: 16-byte loads of 16-aligned blocks)
+uintptr_t w_align(int t) { return t == TY_Q4_K ? 16 : 4; }
+
+int g_inited = 0;
+std::atomic<int> g_prefill{0};
+int g_prefill_fp32 = 0;
+
+// ---- output scales (src/qmatvec.cpp:175-253)
+struct OutScale {
+    const void *owner;
+    const char *lo, *hi;
+    const float *s;
+    int n;
+};
+std::vector<OutScale> g_scales;
+std::mutex g_scales_mu;
+std::atomic<int> g_n_scales{0};
+
+bool find_scale(const void *W, OutScale &o) {
+    if (!W || g_n_scales.load(std::memory_order_relaxed) == 0) return false;
+    std::lock_guard<std::mutex> lk(g_scales_mu);
+    for (const OutScale &x : g_scales)
+        if ((const char *)W >= x.lo && (const char *)W < x.hi) {
+            o = x;
+            return true;
+        }
+    return false;
+}
+
+float dense_scale(const void *W) {
+    OutScale o;
+    if (!find_scale(W, o)) return 1.0f;
+    if (o.n == 1) return o.s[0];
+    return o.s[((const char *)W - o.lo) / ((o.hi - o.lo) / o.n)];
+}
+
+void act_ptrs(int type, const qmatvec_q8 *q, const int8_t *&q8, const float *&d8, const int32_t *&bs) {
+    const bool kq = reads_q8k(type);
+    q8 = kq ? q->qK : q->q0;
+    d8 = kq ? q->dK : q->d0;
+    bs = kq ? q->bsK : nullptr;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qmatvec_init(const char *co_path) {
+    (void)co_path;
+    if (g_inited) return 0;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return -1;
+    g_inited = 1;
+    return 0;
+}
+
+void qmatvec_free(void) { g_inited = 0; }
+
+int qmatvec_set_out_scale(const void *owner, const void *W, size_t bytes, const float *s, int n) {
+    if (!W || !s || n < 1 || bytes % (size_t)n != 0) return -1;
+    std::lock_guard<std::mutex> lk(g_scales_mu);
+    g_scales.push_back({owner, (const char *)W, (const char *)W + bytes, s, n});
+    g_n_scales.store((int)g_scales.size());
+    return 0;
+}
+
+void qmatvec_drop_out_scales(const void *owner) {
+    std::lock_guard<std::mutex> lk(g_scales_mu);
+    for (size_t i = g_scales.size(); i-- > 0;)
+        if (g_scales[i].owner == owner) g_scales.erase(g_scales.begin() + (long)i);
+    g_n_scales.store((int)g_scales.size());
+}
+
+int qmatvec_supported(int type) {
+    (void)type;
+    return 0;
+}
+
+void qmatvec_set_prefill(int on) { g_prefill = on && !getenv("QMATVEC_PREFILL_SPLIT_VARIANT"); }
+int qmatvec_prefill(void) { return g_prefill; }
+void qmatvec_set_prefill_fp32(int on) { g_prefill_fp32 = on; }
+
+static size_t align16(size_t n) { return (n + 15) & ~(size_t)15; }
+
+size_t qmatvec_q8_bytes(int max_k) {
+    const size_t k = (size_t)max_k;
+    return 2 * align16(k) + 2 * align16(k / 32 * 4) + align16(k / 256 * 4) + align16(k / 16 * 4);
+}
+
+void qmatvec_q8_bind(qmatvec_q8 *q, void *mem, int max_k) {
+    const size_t k = (size_t)max_k;
+    char *p = (char *)mem;
+    q->q0 = (int8_t *)p;
+    p += align16(k);
+    q->qK = (int8_t *)p;
+    p += align16(k);
+    q->d0 = (float *)p;
+    p += align16(k / 32 * 4);
+    q->dK = (float *)p;
+    p += align16(k / 256 * 4);
+    q->bsK = (int32_t *)p;
+    p += align16(k / 16 * 4);
+    q->s0 = (int32_t *)p;
+    q->max_k = max_k;
+    q->xh = nullptr;
+    q->xh_bf16 = 0;
+}
+
+int qmatvec_q8_supported(int type, int K) {
+    if (!is_int8_type(type) || K <= 0) return 0;
+    return K % k_multiple(type) == 0;
+}
+
+hipError_t qmatvec_quantize(const float *x, int K, const qmatvec_q8 *q, hipStream_t stream) {
+    if (!q || !x) return hipErrorInvalidValue;
+    if (K <= 0 || K % 32 != 0 || K > q->max_k) return hipErrorInvalidValue;
+    Q8Ptrs o{q->q0, q->d0, q->qK, q->dK, q->bsK, q->s0};
+    return launch_quantize_q8(x, K, o, stream);
+}
+
+int qmatvec_q8_few_supported(int type, int K, int T) { return T >= 1 && T <= 4 && qmatvec_q8_supported(type, K); }
+
+hipError_t qmatvec_launch_q8_multi_t(int type, int n, const void *const *Ws, const int *Ns, float *const *ys,
+                                     size_t row_bytes, const qmatvec_q8 *q, int K, int T, hipStream_t stream) {
+    if (!qmatvec_q8_few_supported(type, K, T)) return hipErrorInvalidDeviceFunction;
+    if (!q || n < 1 || n > 4 || row_bytes != qt_row_size(type, K) || (long long)K * T > q->max_k)
+        return hipErrorInvalidValue;
+    MvArgs a{};
+    int Nt = 0;
+    for (int i = 0; i < 4; ++i) {
+        const int j = i < n ? i : n - 1;  // unused slots repeat the last matrix, with no rows
+        if (((uintptr_t)Ws[j] & (w_align(type) - 1)) != 0 || Ns[j] < 0) return hipErrorInvalidValue;
+        a.W[i] = (const uint8_t *)Ws[j];
+        a.y[i] = ys[j];
+        if (i < n) Nt += Ns[i];
+        a.bound[i] = Nt;
+        a.ystride[i] = Ns[j];
+        a.osc[i] = dense_scale(Ws[j]);
+    }
+    if (Nt == 0) return hipSuccess;
+    a.row_bytes = (long long)row_bytes;
+    act_ptrs(type, q, a.q, a.d, a.bs);
+    a.Nt = Nt;
+    a.K = K;
+    a.T = T;
+    a.L = matvec_lanes(type, K, Nt);
+    return launch_matvec(type, a, stream);
+}
+
+hipError_t qmatvec_launch_q8_multi(int type, int n, const void *const *Ws, const int *Ns, float *const *ys,
+                                   size_t row_bytes, const qmatvec_q8 *q, int K, hipStream_t stream) {
+    return qmatvec_launch_q8_multi_t(type, n, Ws, Ns, ys, row_bytes, q, K, 1, stream);
+}
+
+hipError_t qmatvec_launch_q8_pair(int type, const void *W, int N, float *y, const void *W2, int N2, float *y2,
+                                  size_t row_bytes, const qmatvec_q8 *q, int K, hipStream_t stream) {
+    const void *Ws[] = {W, W2};
+    const int Ns[] = {N, N2};
+    float *ys[] = {y, y2};
+    return qmatvec_launch_q8_multi(type, 2, Ws, Ns, ys, row_bytes, q, K, stream);
+}
+
+hipError_t qmatvec_launch_q8(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N, int K,
+                             hipStream_t stream) {
+    const void *Ws[] = {W};
+    const int Ns[] = {N};
+    float *ys[] = {y};
+    return qmatvec_launch_q8_multi(type, 1, Ws, Ns, ys, row_bytes, q, K, stream);
+}
+
+hipError_t qmatvec_launch_q8_id_x(int type, const void *W, const void *W2, const void *Wx, const void *W2x,
+                                  size_t row_bytes, const int32_t *ids, int n_used, int x_per_slot,
+                                  const qmatvec_q8 *q, float *y, float *y2, int N, int K, int T, hipStream_t stream) {
+    if (!qmatvec_q8_supported(type, K)) return hipErrorInvalidDeviceFunction;
+    if (!q) return hipErrorInvalidValue;
+    const long long in_rows = (long long)T * (x_per_slot ? n_used : 1);
+    const uintptr_t am = w_align(type) - 1;
+    if (T <= 0 || n_used <= 0 || N <= 0 || row_bytes != qt_row_size(type, K) || ((uintptr_t)W & am) != 0 ||
+        in_rows * K > q->max_k)
+        return hipErrorInvalidValue;
+    if ((((uintptr_t)W2 | (uintptr_t)Wx | (uintptr_t)W2x) & am) != 0) return hipErrorInvalidValue;
+    MvIdArgs a{};
+    a.W[0] = (const uint8_t *)W;
+    a.W[1] = (const uint8_t *)W2;
+    a.Wx[0] = (const uint8_t *)Wx;
+    a.Wx[1] = (const uint8_t *)W2x;
+    a.y[0] = y;
+    a.y[1] = y2;
+    const void *ws[2] = {W, W2}, *wx[2] = {Wx, W2x};
+    for (int m = 0; m < 2; ++m) {
+        a.es[m] = nullptr;
+        a.s[m] = a.sx[m] = 1.0f;
+        OutScale o;
+        if (find_scale(ws[m], o)) {
+            if (o.n > 1) a.es[m] = o.s;  // per-expert factors: read by the kernel (device-visible)
+            else a.s[m] = o.s[0];
+        }
+        if (wx[m]) a.sx[m] = dense_scale(wx[m]);
+    }
+    a.row_bytes = (long long)row_bytes;
+    a.ids = ids;
+    act_ptrs(type, q, a.q, a.d, a.bs);
+    a.n_used = n_used;
+    a.x_per_slot = x_per_slot;
+    a.N = N;
+    a.K = K;
+    a.T = T;
+    a.nmat = W2 ? 2 : 1;
+    a.L = matvec_lanes(type, K, (long long)N * n_used * a.nmat * T);
+    return launch_matvec_id(type, a, stream);
+}
+
+hipError_t qmatvec_launch_q8_id(int type, const void *W, size_t row_bytes, const int32_t *ids, int n_used,
+                                int x_per_slot, const qmatvec_q8 *q, float *y, int N, int K, int T, hipStream_t stream) {
+    return qmatvec_launch_q8_id_x(type, W, nullptr, nullptr, nullptr, row_bytes, ids, n_used, x_per_slot, q, y,
+                                  nullptr, N, K, T, stream);
+}
+
+hipError_t qmatvec_launch_q8_id_pair(int type, const void *W, const void *W2, size_t row_bytes, const int32_t *ids,
+                                     int n_used, int x_per_slot, const qmatvec_q8 *q, float *y, float *y2, int N, int K,
+                                     int T, hipStream_t stream) {
+    return qmatvec_launch_q8_id_x(type, W, W2, nullptr, nullptr, row_bytes, ids, n_used, x_per_slot, q, y, y2, N, K,
+                                  T, stream);
+}
+
+hipError_t qmatvec_launch_q8_batch(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y,
+                                   long long ldy, int N, int K, int T, hipStream_t stream) {
+    if (!qmatvec_q8_supported(type, K)) return hipErrorInvalidDeviceFunction;
+    if (!q || T <= 0 || N <= 0 || row_bytes != qt_row_size(type, K) || ((uintptr_t)W & (w_align(type) - 1)) != 0 ||
+        (long long)T * K > q->max_k || ldy < N)
+        return hipErrorInvalidValue;
+    // tokens in groups of up to 4 through the decode kernel (weights read once per group)
+    MvArgs a{};
+    a.W[0] = a.W[1] = a.W[2] = a.W[3] = (const uint8_t *)W;
+    a.bound[0] = a.bound[1] = a.bound[2] = a.bound[3] = N;
+    a.ystride[0] = a.ystride[1] = a.ystride[2] = a.ystride[3] = ldy;
+    a.osc[0] = a.osc[1] = a.osc[2] = a.osc[3] = dense_scale(W);
+    a.row_bytes = (long long)row_bytes;
+    a.Nt = N;
+    a.K = K;
+    a.L = matvec_lanes(type, K, N);
+    const int8_t *q8;
+    const float *d8;
+    const int32_t *bs;
+    act_ptrs(type, q, q8, d8, bs);
+    const int kb = K / act_blk(type);
+    for (int t0 = 0; t0 < T; t0 += 4) {
+        a.T = T - t0 < 4 ? T - t0 : 4;
+        a.y[0] = a.y[1] = a.y[2] = a.y[3] = y + (long long)t0 * ldy;
+        a.q = q8 + (long long)t0 * K;
+        a.d = d8 + (long long)t0 * kb;
+        a.bs = bs ? bs + (long long)t0 * (K / 16) : nullptr;
+        const hipError_t e = launch_matvec(type, a, stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+int qmatvec_id_batch_tile(int type, int N, int K) {
+    (void)type;
+    (void)N;
+    (void)K;
+    return 16;
+}
+
+int qmatvec_q8_id_batch_supported(int type, int K) {
+    (void)type;
+    (void)K;
+    return 0;
+}
+
+hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N,
+                                      int K, int max_tiles, int tile, const int32_t *n_tiles, const int32_t *tile_e,
+                                      const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
+                                      const int32_t *out_rows, hipStream_t stream) {
+    (void)type; (void)W; (void)row_bytes; (void)q; (void)y; (void)N; (void)K; (void)max_tiles; (void)tile;
+    (void)n_tiles; (void)tile_e; (void)tile_start; (void)tile_n; (void)in_rows; (void)out_rows; (void)stream;
+    return hipErrorInvalidDeviceFunction;
+}
+
+hipError_t qmatvec_debug_block_dots(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, int32_t *out,
+                                    int N, int K, hipStream_t stream) {
+    if (!qmatvec_q8_supported(type, K)) return hipErrorInvalidDeviceFunction;
+    if (!q || !out || N <= 0 || row_bytes != qt_row_size(type, K) || K > q->max_k) return hipErrorInvalidValue;
+    return launch_block_dots(type, (const uint8_t *)W, (long long)row_bytes, reads_q8k(type) ? q->qK : q->q0, out, N, K,
+                             stream);
+}
+
+}  // extern "C"
