@@ -98,8 +98,9 @@ def quantize(t, x, n_threads=0):
 
 
 def to_float(t, w, k):
-    w = np.ascontiguousarray(w, dtype=np.uint8)
-    nrows = w.size // row_size(t, k)
+    rb = row_size(t, k)
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1, rb)
+    nrows = w.shape[0]
     y = np.empty((nrows, k), dtype=np.float32)
     for r in range(nrows):
         assert lib().orc_to_float(t, _ptr(w[r]), _ptr(y[r]), k) == 0

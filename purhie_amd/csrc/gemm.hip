@@ -1,0 +1,403 @@
+// gemm.hip -- the prefill GEMM Y[t][n] = sum_k W[n][k] X[t][k] for GGUF weights on gfx950 MFMA, and its
+// MoE form over moe_group's expert tiles. Replaces the reference's matmul_wmma_<type> / matmul_q8_<type> /
+// matmul_wmma_id_<type> (src/matvec_q.hip:2174-3348), whose per-32-block int32 tile sums are followed by a
+// float epilogue per block.
+//
+// MI355X-first design (fp16 MFMA on exactly decoded operands):
+//   * int8 MFMA would need a float fix-up per 16 / 32 K-values of every output (ROCmFP4 has a UE4M3 scale
+//     per 16 weights, Q8_0 activations one per 32): at 32 multiply-adds per output per block the matrix
+//     core outruns the vector ALU by 2-6x. Instead the ROCmFP4 weight value CB[nibble] * ue4m3(e) is exact
+//     in fp16 (|CB * (8 + m)| <= 150 fits 11 bits), so the weight scale rides inside the MFMA operand and
+//     v_mfma_f32_16x16x32_f16 over one 32-value block yields the reference's block term
+//     c0 * e0 + c1 * e1 with exact products; one FMA per output per block applies the activation scale:
+//     acc += d_x * C_block (the reference's d_x * (c0 e0 + c1 e1)).
+//   * the token operand is the Q8_0 int8 activation, exact in fp16, converted once per call by a pre-pass
+//     (k_act_f16) into the GEMM's K order; the weights are decoded in-kernel into LDS once per tile
+//     through a 256-entry half2 table (a byte's two nibbles -> two fp16 codebook values) and a packed
+//     fp16 multiply by the two half-block scales. Within a 32-block the K order is permuted so that a
+//     byte's low / high nibble (values j, j + 16) land side by side; the pre-pass permutes the token
+//     operand identically, so every MFMA sums the same pairs.
+//   * workgroup tile 128 weight rows x 128 tokens, 4 waves of 64 x 64 (4 x 4 MFMA tiles), K stages of 128
+//     (4 blocks) with the next stage's global loads in flight (registers) while the current one runs.
+#include "device.h"
+#include "kernels.h"
+
+namespace pq {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int GB_N = 128;           // weight rows per workgroup
+constexpr int GB_T = 128;           // tokens per workgroup
+constexpr int GB_K = 128;           // K per stage
+constexpr int G_THREADS = 256;
+constexpr int LDS_ROW = GB_K + 8;   // halves per LDS row (16 bytes of padding: conflict-free b128 reads)
+
+// ---------------------------------------------------------------- token pre-pass
+// One thread per 32-value block of one token row: int8 q -> fp16 (exact), in the weight type's K order
+// (perm: position 2j <- value j, 2j + 1 <- value j + 16), plus the block scales; rows >= T (up to Tpad,
+// plus one extra all-zero row used by MoE tiles) are zero.
+__global__ void k_act_f16(const int8_t *__restrict__ q, const float *__restrict__ d, int T, int K, int Tpad,
+                          int perm, _Float16 *__restrict__ xh, float *__restrict__ dxp) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int nb = K / 32;
+    if (i >= (long long)(Tpad + 1) * nb) return;
+    const int t = (int)(i / nb), b = (int)(i % nb);
+    _Float16 *o = xh + (long long)t * K + 32 * b;
+    if (t >= T) {
+        for (int j = 0; j < 32; ++j) o[j] = (_Float16)0.0f;
+        dxp[i] = 0.0f;
+        return;
+    }
+    const int8_t *s = q + (long long)t * K + 32 * b;
+    for (int j = 0; j < 16; ++j) {
+        const _Float16 lo = (_Float16)(float)s[j], hi = (_Float16)(float)s[j + 16];
+        if (perm) {
+            o[2 * j] = lo;
+            o[2 * j + 1] = hi;
+        } else {
+            o[j] = lo;
+            o[j + 16] = hi;
+        }
+    }
+    dxp[i] = d[(long long)t * nb + b];
+}
+
+// ---------------------------------------------------------------- weight stage decoders
+// Each fills rows of the LDS weight tile [GB_N][LDS_ROW] (fp16, the type's K order) for K values
+// k0 .. k0 + 127, and for Q8_0 the per-row block scales sdw[4][GB_N].
+
+// 256-entry table: byte -> half2(CB[low nibble], CB[high nibble])
+__device__ __forceinline__ void init_fp4_lut(uint32_t *lut) {
+    const int b = threadIdx.x;  // blockDim == 256
+    const int lo = (int)(int8_t)(fp4x4(b & 15) & 0xffu), hi = (int)(int8_t)(fp4x4(b >> 4) & 0xffu);
+    h2 v;
+    v.x = (_Float16)(float)lo;
+    v.y = (_Float16)(float)hi;
+    lut[b] = __builtin_bit_cast(uint32_t, v);
+}
+
+// one 32-value FP4 block: 16 value bytes (4 dwords) and the two half-block scales -> 16 half2 in LDS
+__device__ __forceinline__ void fp4_block_to_lds(const uint32_t qs[4], float e0, float e1, const uint32_t *lut,
+                                                 _Float16 *dst) {
+    h2 sc;
+    sc.x = (_Float16)e0;  // exact: a UE4M3 half-scale value is an fp16 value
+    sc.y = (_Float16)e1;
+    uint32_t o[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const h2 c = __builtin_bit_cast(h2, lut[(qs[k] >> (8 * j)) & 0xffu]);
+            o[4 * k + j] = __builtin_bit_cast(uint32_t, c * sc);  // v_pk_mul_f16: exact products
+        }
+    uint4 *d4 = (uint4 *)dst;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) d4[m] = make_uint4(o[4 * m], o[4 * m + 1], o[4 * m + 2], o[4 * m + 3]);
+}
+
+// int8 -> fp16 for 4 bytes: (b ^ 0x80) placed as the low byte of 0x64xx is 1024 + 128 + b, minus 1152
+__device__ __forceinline__ void i8x4_to_h4(uint32_t w, uint32_t &h01, uint32_t &h23) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t a = __builtin_amdgcn_perm(0u, u, 0x0c010c00u) | 0x64006400u;
+    const uint32_t b = __builtin_amdgcn_perm(0u, u, 0x0c030c02u) | 0x64006400u;
+    h2 bias;
+    bias.x = (_Float16)1152.0f;
+    bias.y = (_Float16)1152.0f;
+    h01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a) - bias);
+    h23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, b) - bias);
+}
+
+template <int TYPE>
+struct GStage;
+
+// ROCmFP4: thread t decodes row t / 2, blocks 2 (t & 1) and 2 (t & 1) + 1 of the stage (36 bytes, 4-aligned)
+template <>
+struct GStage<TY_FP4> {
+    static constexpr bool PERM = true, ROW_SCALE = false;
+    struct Raw {
+        uint32_t w[9];
+    };
+    __device__ static void load(const uint8_t *W, long long rb, int N, int n0, int k0, Raw &r) {
+        const int row = n0 + (threadIdx.x >> 1), p = threadIdx.x & 1;
+        if (row >= N) {
+#pragma unroll
+            for (int k = 0; k < 9; ++k) r.w[k] = 0;
+            return;
+        }
+        const uint8_t *b = W + (long long)row * rb + (long long)(k0 / 32 + 2 * p) * 18;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) r.w[k] = ld32(b + 4 * k);
+    }
+    __device__ static void store(const Raw &r, const uint32_t *lut, _Float16 *sW, float *) {
+        const int row = threadIdx.x >> 1, p = threadIdx.x & 1;
+        _Float16 *dst = sW + row * LDS_ROW + 64 * p;
+        const uint32_t qa[4] = {r.w[0], r.w[1], r.w[2], r.w[3]};
+        uint32_t qb[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) qb[k] = align_bytes(r.w[5 + k], r.w[4 + k], 2);
+        fp4_block_to_lds(qa, ue4m3_half(r.w[4]), ue4m3_half(r.w[4] >> 8), lut, dst);
+        fp4_block_to_lds(qb, ue4m3_half(r.w[8] >> 16), ue4m3_half(r.w[8] >> 24), lut, dst + 32);
+    }
+};
+
+// ROCmFP4_FAST: thread t decodes row t / 2, blocks 2 (t & 1), 2 (t & 1) + 1 (34 bytes at a 2-aligned offset,
+// realigned by v_alignbyte)
+template <>
+struct GStage<TY_FAST> {
+    static constexpr bool PERM = true, ROW_SCALE = false;
+    // The pair starts 0 or 2 bytes past a dword boundary (row bytes are a multiple of 4): nine aligned dwords
+    // from the boundary below cover its 34 bytes. A pair at offset 0 is never a row's last (that one starts
+    // at row_bytes - 34, 2 past a boundary), so the two spare bytes it reads are still inside the row.
+    struct Raw {
+        uint32_t w[9];
+        uint32_t off;
+    };
+    __device__ static void load(const uint8_t *W, long long rb, int N, int n0, int k0, Raw &r) {
+        const int row = n0 + (threadIdx.x >> 1), p = threadIdx.x & 1;
+        if (row >= N) {
+#pragma unroll
+            for (int k = 0; k < 9; ++k) r.w[k] = 0;
+            r.off = 0;
+            return;
+        }
+        const uint8_t *b = W + (long long)row * rb + (long long)(k0 / 32 + 2 * p) * 17;
+        r.off = (uint32_t)((uintptr_t)b & 3u);
+        const uint8_t *a = b - r.off;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) r.w[k] = ld32(a + 4 * k);
+    }
+    __device__ static void store(const Raw &r, const uint32_t *lut, _Float16 *sW, float *) {
+        const int row = threadIdx.x >> 1, p = threadIdx.x & 1;
+        _Float16 *dst = sW + row * LDS_ROW + 64 * p;
+        uint32_t w[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) w[k] = align_bytes(k < 8 ? r.w[k + 1] : 0u, r.w[k], r.off);
+        // block 0: bytes 0..15 values, 16 scale; block 1: bytes 17..32 values, 33 scale
+        const uint32_t qa[4] = {w[0], w[1], w[2], w[3]};
+        uint32_t qb[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) qb[k] = align_bytes(w[5 + k], w[4 + k], 1);
+        const float ea = ue4m3_half(w[4]), eb = ue4m3_half(w[8] >> 8);
+        fp4_block_to_lds(qa, ea, ea, lut, dst);
+        fp4_block_to_lds(qb, eb, eb, lut, dst + 32);
+    }
+};
+
+// Q8_0: thread t decodes row t / 2, blocks 2 (t & 1), 2 (t & 1) + 1 (68 bytes, 4-aligned): the int8 values
+// (exact in fp16) in natural order, and the two fp16 block scales into sdw[block][row]
+template <>
+struct GStage<TY_Q8_0> {
+    static constexpr bool PERM = false, ROW_SCALE = true;
+    struct Raw {
+        uint32_t w[17];
+    };
+    __device__ static void load(const uint8_t *W, long long rb, int N, int n0, int k0, Raw &r) {
+        const int row = n0 + (threadIdx.x >> 1), p = threadIdx.x & 1;
+        if (row >= N) {
+#pragma unroll
+            for (int k = 0; k < 17; ++k) r.w[k] = 0;
+            return;
+        }
+        const uint8_t *b = W + (long long)row * rb + (long long)(k0 / 32 + 2 * p) * 34;
+#pragma unroll
+        for (int k = 0; k < 17; ++k) r.w[k] = ld32(b + 4 * k);
+    }
+    __device__ static void store(const Raw &r, const uint32_t *, _Float16 *sW, float *sdw) {
+        const int row = threadIdx.x >> 1, p = threadIdx.x & 1;
+        uint4 *d4 = (uint4 *)(sW + row * LDS_ROW + 64 * p);
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+            uint32_t v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = blk == 0 ? align_bytes(r.w[k + 1], r.w[k], 2) : r.w[9 + k];
+            uint32_t h[16];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) i8x4_to_h4(v[k], h[2 * k], h[2 * k + 1]);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) d4[4 * blk + m] = make_uint4(h[4 * m], h[4 * m + 1], h[4 * m + 2], h[4 * m + 3]);
+        }
+        sdw[(2 * p) * GB_N + row] = h2f(r.w[0] & 0xffffu);
+        sdw[(2 * p + 1) * GB_N + row] = h2f(r.w[8] >> 16);
+    }
+};
+
+// ---------------------------------------------------------------- token rows of a tile
+struct TokMap {
+    const int32_t *rows;  // MoE: in_rows + tile_start (null: dense)
+    int base, n, zero_row;
+    __device__ int row(int j) const { return rows ? (j < n ? rows[j] : zero_row) : base + j; }
+};
+
+
+template <int TYPE>
+__global__ void __launch_bounds__(G_THREADS, 2) k_gemm(GemmArgs a) {
+    using S = GStage<TYPE>;
+    __shared__ __attribute__((aligned(16))) _Float16 sW[GB_N * LDS_ROW];
+    __shared__ __attribute__((aligned(16))) _Float16 sX[GB_T * LDS_ROW];
+    __shared__ float sdx[4 * GB_T];   // [block][token]
+    __shared__ float sdw[4 * GB_N];   // [block][row] (Q8_0 weights)
+    __shared__ uint32_t lut[256];
+
+    // tile coordinates
+    int n0, e = 0;
+    TokMap tm;
+    const int32_t *orow = nullptr;
+    if (a.n_tiles) {  // MoE: grid (row tiles, tiles)
+        const int k = blockIdx.y;
+        if (k >= *a.n_tiles) return;
+        e = a.tile_e[k];
+        const int st = a.tile_start[k];
+        tm = {a.in_rows + st, 0, a.tile_n[k], a.zero_row};
+        orow = a.out_rows + st;
+        n0 = blockIdx.x * GB_N;
+    } else {          // dense: grid (token tiles, row tiles); a row tile's token tiles are adjacent
+        tm = {nullptr, (int)blockIdx.x * GB_T, GB_T, a.zero_row};
+        n0 = blockIdx.y * GB_N;
+    }
+    const uint8_t *W = a.W + (long long)e * a.N * a.row_bytes;
+    if (!S::ROW_SCALE) init_fp4_lut(lut);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wn = (wave & 1) * 64, wt = (wave >> 1) * 64;  // the wave's 64 x 64 sub-tile
+    const int nb = a.K / 32;
+
+    // token operand staging: thread t copies 64 halves (128 bytes) of token row t / 2
+    const int xr = tid >> 1, xp = tid & 1;
+    const _Float16 *xsrc = a.xh + (long long)tm.row(xr) * a.K + 64 * xp;
+    const float *dsrc = a.dx + (long long)tm.row(tid & 127) * nb;
+
+    typename S::Raw raw;
+    uint4 xv0, xv1, xv2, xv3, xv4, xv5, xv6, xv7;
+    float2 dv;
+    // global loads of stage k0: the weight bytes, 64 token halves, and the scales of blocks k0/32 + 2 (tid >> 7)
+    // and + 1 for token tid & 127
+#define GEMM_ISSUE(k0)                                                  \
+    do {                                                                \
+        S::load(W, a.row_bytes, a.N, n0, (k0), raw);                    \
+        const uint4 *s4 = (const uint4 *)(xsrc + (k0));                 \
+        xv0 = s4[0];                                                    \
+        xv1 = s4[1];                                                    \
+        xv2 = s4[2];                                                    \
+        xv3 = s4[3];                                                    \
+        xv4 = s4[4];                                                    \
+        xv5 = s4[5];                                                    \
+        xv6 = s4[6];                                                    \
+        xv7 = s4[7];                                                    \
+        dv = *(const float2 *)(dsrc + (k0) / 32 + 2 * (tid >> 7));      \
+    } while (0)
+
+    f4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    GEMM_ISSUE(0);
+    for (int k0 = 0; k0 < a.K; k0 += GB_K) {
+        __syncthreads();  // the previous stage's LDS reads are done (and the table is written)
+        S::store(raw, lut, sW, sdw);
+        uint4 *xd = (uint4 *)(sX + xr * LDS_ROW + 64 * xp);
+        xd[0] = xv0;
+        xd[1] = xv1;
+        xd[2] = xv2;
+        xd[3] = xv3;
+        xd[4] = xv4;
+        xd[5] = xv5;
+        xd[6] = xv6;
+        xd[7] = xv7;
+        sdx[(2 * (tid >> 7)) * GB_T + (tid & 127)] = dv.x;
+        sdx[(2 * (tid >> 7) + 1) * GB_T + (tid & 127)] = dv.y;
+        __syncthreads();
+        if (k0 + GB_K < a.K) GEMM_ISSUE(k0 + GB_K);  // next stage's global loads in flight during the MFMAs
+
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int kk = b * 32 + 8 * (lane >> 4);
+            h8 fa[4], fb[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) fa[i] = *(const h8 *)(sW + (wn + 16 * i + (lane & 15)) * LDS_ROW + kk);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fb[j] = *(const h8 *)(sX + (wt + 16 * j + (lane & 15)) * LDS_ROW + kk);
+            float dxj[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dxj[j] = sdx[b * GB_T + wt + 16 * j + (lane & 15)];
+            float dwi[4][4];
+            if (S::ROW_SCALE) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float4 v = *(const float4 *)(sdw + b * GB_N + wn + 16 * i + 4 * (lane >> 4));
+                    dwi[i][0] = v.x;
+                    dwi[i][1] = v.y;
+                    dwi[i][2] = v.z;
+                    dwi[i][3] = v.w;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[j], f4{0.0f, 0.0f, 0.0f, 0.0f}, 0,
+                                                                         0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float s = S::ROW_SCALE ? dwi[i][r] * dxj[j] : dxj[j];
+                        acc[i][j][r] = __builtin_fmaf(s, c[r], acc[i][j][r]);
+                    }
+                }
+        }
+    }
+
+    // store: lane holds rows 4 (lane / 16) .. + 3 of each 16 x 16 tile, token column lane % 16
+    const float sc = a.es ? a.es[e] : a.osc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int tt = wt + 16 * j + (lane & 15);
+        long long yrow;
+        if (orow) {
+            if (tt >= tm.n) continue;
+            yrow = (long long)orow[tt] * a.N;
+        } else {
+            const int t = tm.base + tt;
+            if (t >= a.T) continue;
+            yrow = (long long)t * a.ldy;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int n = n0 + wn + 16 * i + 4 * (lane >> 4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (n + r < a.N) a.y[yrow + n + r] = acc[i][j][r] * sc;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- host launchers
+
+int gemm_supported(int type) { return type == TY_FP4 || type == TY_FAST || type == TY_Q8_0; }
+
+int gemm_k_multiple() { return GB_K; }
+
+int gemm_token_tile() { return GB_T; }
+
+hipError_t launch_act_f16(int type, const int8_t *q, const float *d, int T, int K, int Tpad, _Float16 *xh, float *dxp,
+                          hipStream_t stream) {
+    const long long n = (long long)(Tpad + 1) * (K / 32);
+    const int perm = GStage<TY_FP4>::PERM && (type == TY_FP4 || type == TY_FAST);
+    hipLaunchKernelGGL(k_act_f16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, q, d, T, K, Tpad, perm, xh,
+                       dxp);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm(int type, const GemmArgs &a, dim3 grid, hipStream_t stream) {
+    switch (type) {
+    case TY_FP4: hipLaunchKernelGGL(k_gemm<TY_FP4>, grid, dim3(G_THREADS), 0, stream, a); break;
+    case TY_FAST: hipLaunchKernelGGL(k_gemm<TY_FAST>, grid, dim3(G_THREADS), 0, stream, a); break;
+    case TY_Q8_0: hipLaunchKernelGGL(k_gemm<TY_Q8_0>, grid, dim3(G_THREADS), 0, stream, a); break;
+    default: return hipErrorInvalidDeviceFunction;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace pq

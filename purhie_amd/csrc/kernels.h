@@ -58,6 +58,29 @@ hipError_t launch_matvec_id(int type, const MvIdArgs &a, hipStream_t stream);
 hipError_t launch_block_dots(int type, const uint8_t *W, long long row_bytes, const int8_t *q, int32_t *out, int N,
                              int K, hipStream_t stream);
 
+// Prefill GEMM (fp16 MFMA on exactly decoded operands). Token operand: xh [rows][K] fp16 and dx
+// [rows][K / 32] from launch_act_f16 (row zero_row all zero); dense tiles (n_tiles null) or MoE tiles.
+struct GemmArgs {
+    const uint8_t *W;       // dense: the matrix; MoE: stacked experts
+    long long row_bytes;
+    const _Float16 *xh;     // token operand [rows][K] (pre-pass)
+    const float *dx;        // block scales [rows][K / 32]
+    float *y;
+    long long ldy;
+    int N, K, T, zero_row;
+    float osc;
+    // MoE tiles (n_tiles null: dense)
+    const int32_t *n_tiles, *tile_e, *tile_start, *tile_n, *in_rows, *out_rows;
+    const float *es;        // per-expert output scales (null: osc)
+};
+
+int gemm_supported(int type);
+int gemm_k_multiple();
+int gemm_token_tile();
+hipError_t launch_act_f16(int type, const int8_t *q, const float *d, int T, int K, int Tpad, _Float16 *xh, float *dxp,
+                          hipStream_t stream);
+hipError_t launch_gemm(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);
+
 // lanes per row the decode kernels use for a matrix of K columns and `rows` rows in total
 int matvec_lanes(int type, int K, long long rows);
 

@@ -74,6 +74,60 @@ void act_ptrs(int type, const qmatvec_q8 *q, const int8_t *&q8, const float *&d8
     bs = kq ? q->bsK : nullptr;
 }
 
+// batches of at least this many tokens take the GEMM outside prefill mode (QMATVEC_WMMA_MIN_T, as the
+// reference's src/qmatvec.cpp:150)
+int gemm_min_t() {
+    static const int v = getenv("QMATVEC_WMMA_MIN_T") ? atoi(getenv("QMATVEC_WMMA_MIN_T")) : 32;
+    return v;
+}
+
+size_t align16z(size_t n) { return (n + 15) & ~(size_t)15; }
+
+// The GEMM's token operand: rows of q as fp16 in the weight type's K order plus the block scales, in a
+// stream-ordered allocation (freed on the same stream after the GEMM).
+struct TokWs {
+    void *mem = nullptr;
+    _Float16 *xh = nullptr;
+    float *dx = nullptr;
+};
+
+hipError_t tokens_to_f16(int type, const qmatvec_q8 *q, int rows, int K, int Tpad, TokWs &w, hipStream_t stream) {
+    const size_t xb = align16z((size_t)(Tpad + 1) * K * 2), db = (size_t)(Tpad + 1) * (K / 32) * 4;
+    hipError_t e = hipMallocAsync(&w.mem, xb + db, stream);
+    if (e != hipSuccess) return e;
+    w.xh = (_Float16 *)w.mem;
+    w.dx = (float *)((char *)w.mem + xb);
+    return launch_act_f16(type, q->q0, q->d0, rows, K, Tpad, w.xh, w.dx, stream);
+}
+
+hipError_t gemm_dense(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, long long ldy, int N,
+                      int K, int T, hipStream_t stream) {
+    const int BT = gemm_token_tile();
+    const int Tpad = (T + BT - 1) / BT * BT;
+    TokWs w;
+    hipError_t e = tokens_to_f16(type, q, T, K, Tpad, w, stream);
+    if (e == hipSuccess) {
+        GemmArgs a{};
+        a.W = (const uint8_t *)W;
+        a.row_bytes = (long long)row_bytes;
+        a.xh = w.xh;
+        a.dx = w.dx;
+        a.y = y;
+        a.ldy = ldy;
+        a.N = N;
+        a.K = K;
+        a.T = T;
+        a.zero_row = Tpad;
+        a.osc = dense_scale(W);
+        e = launch_gemm(type, a, dim3((unsigned)(Tpad / BT), (unsigned)((N + 127) / 128)), stream);
+    }
+    if (w.mem) {
+        const hipError_t f = hipFreeAsync(w.mem, stream);
+        if (e == hipSuccess) e = f;
+    }
+    return e;
+}
+
 }  // namespace
 
 extern "C" {
@@ -262,6 +316,9 @@ hipError_t qmatvec_launch_q8_batch(int type, const void *W, size_t row_bytes, co
     if (!q || T <= 0 || N <= 0 || row_bytes != qt_row_size(type, K) || ((uintptr_t)W & (w_align(type) - 1)) != 0 ||
         (long long)T * K > q->max_k || ldy < N)
         return hipErrorInvalidValue;
+    // prefill mode or a batch of 32+ tokens: the MFMA GEMM (the reference's WMMA threshold, src/qmatvec.cpp:553)
+    if (gemm_supported(type) && K % gemm_k_multiple() == 0 && (g_prefill || T >= gemm_min_t()) && N >= 64)
+        return gemm_dense(type, W, row_bytes, q, y, ldy, N, K, T, stream);
     // tokens in groups of up to 4 through the decode kernel (weights read once per group)
     MvArgs a{};
     a.W[0] = a.W[1] = a.W[2] = a.W[3] = (const uint8_t *)W;
@@ -289,26 +346,57 @@ hipError_t qmatvec_launch_q8_batch(int type, const void *W, size_t row_bytes, co
     return hipSuccess;
 }
 
-int qmatvec_id_batch_tile(int type, int N, int K) {
-    (void)type;
-    (void)N;
-    (void)K;
-    return 16;
+int qmatvec_q8_id_batch_supported(int type, int K) {
+    return qmatvec_q8_supported(type, K) && gemm_supported(type) && K % gemm_k_multiple() == 0;
 }
 
-int qmatvec_q8_id_batch_supported(int type, int K) {
-    (void)type;
-    (void)K;
-    return 0;
+// the largest tile the expert-tiled GEMM takes: each expert's weights are read once per this many entries
+int qmatvec_id_batch_tile(int type, int N, int K) {
+    (void)N;
+    return qmatvec_q8_id_batch_supported(type, K) ? gemm_token_tile() : 16;
 }
 
 hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N,
                                       int K, int max_tiles, int tile, const int32_t *n_tiles, const int32_t *tile_e,
                                       const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
                                       const int32_t *out_rows, hipStream_t stream) {
-    (void)type; (void)W; (void)row_bytes; (void)q; (void)y; (void)N; (void)K; (void)max_tiles; (void)tile;
-    (void)n_tiles; (void)tile_e; (void)tile_start; (void)tile_n; (void)in_rows; (void)out_rows; (void)stream;
-    return hipErrorInvalidDeviceFunction;
+    if (!qmatvec_q8_id_batch_supported(type, K)) return hipErrorInvalidDeviceFunction;
+    if (!q || max_tiles <= 0 || tile <= 0 || tile > qmatvec_id_batch_tile(type, N, K) || N <= 0 ||
+        row_bytes != qt_row_size(type, K) || ((uintptr_t)W & (w_align(type) - 1)) != 0)
+        return hipErrorInvalidValue;
+    // every input row the buffer can hold (in_rows index them) goes through the pre-pass; row `rows` is zero
+    const int rows = q->max_k / K;
+    TokWs w;
+    hipError_t e = tokens_to_f16(type, q, rows, K, rows, w, stream);
+    if (e == hipSuccess) {
+        GemmArgs a{};
+        a.W = (const uint8_t *)W;
+        a.row_bytes = (long long)row_bytes;
+        a.xh = w.xh;
+        a.dx = w.dx;
+        a.y = y;
+        a.N = N;
+        a.K = K;
+        a.zero_row = rows;
+        a.n_tiles = n_tiles;
+        a.tile_e = tile_e;
+        a.tile_start = tile_start;
+        a.tile_n = tile_n;
+        a.in_rows = in_rows;
+        a.out_rows = out_rows;
+        OutScale o;
+        a.osc = 1.0f;
+        if (find_scale(W, o)) {
+            if (o.n > 1) a.es = o.s;
+            else a.osc = o.s[0];
+        }
+        e = launch_gemm(type, a, dim3((unsigned)((N + 127) / 128), (unsigned)max_tiles), stream);
+    }
+    if (w.mem) {
+        const hipError_t f = hipFreeAsync(w.mem, stream);
+        if (e == hipSuccess) e = f;
+    }
+    return e;
 }
 
 hipError_t qmatvec_debug_block_dots(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, int32_t *out,

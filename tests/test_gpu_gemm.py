@@ -1,0 +1,118 @@
+"""GPU parity of the prefill GEMM (qmatvec_launch_q8_batch on the MFMA path) and of the MoE expert-tiled
+GEMM (qmatvec_launch_q8_id_batch): every output within 1e-5 of sum |w x| of the oracle's per-token matvec
+(the reference's tolerance for its WMMA path, tests/matvec_verify.cpp:230,272), and a token's result
+independent of the batch it is computed in (split invariance, the reference's prefill-mode contract)."""
+import numpy as np
+import pytest
+
+from purhie_amd import synth
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+GEMM_TYPES = (100, 101, 8)
+
+
+@pytest.fixture(scope="module")
+def Q():
+    from purhie_amd import qmatvec
+    qmatvec.lib()
+    yield qmatvec
+    qmatvec.lib().qmatvec_set_prefill(0)
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def acts(seed, T, K, outliers=True):
+    x = synth.gaussian(seed, T * K)
+    if outliers:  # config 3's 0.1% outliers x20
+        x = synth.with_outliers(x, seed + 1, 0.001, 20.0)
+    return x.reshape(T, K)
+
+
+def run_batch(Q, t, Wd, x, N, K, ldy=None):
+    import torch
+    T = x.shape[0]
+    ldy = ldy or N
+    q = Q.Q8(((T * K + 255) // 256) * 256)
+    Q.quantize(dev(x.reshape(-1)), T * K, q)
+    y = torch.full((T, ldy), float("nan"), dtype=torch.float32, device="cuda")
+    Q.launch_q8_batch(t, Wd, q, y, ldy, N, K, T)
+    return host(y)[:, :N]
+
+
+def check_tokens(oracle, t, W, N, K, x, got):
+    for i in range(x.shape[0]):
+        a = oracle.quantize_act(x[i], t in (12, 14))
+        want, ref, mag = oracle.matvec(t, W, N, K, a)
+        err = np.abs(got[i] - want) / (mag + 1e-30)
+        assert err.max() <= TOL, f"token {i}: max rel err {err.max():.3g}"
+        assert np.all(np.abs(got[i] - ref) <= TOL * mag)
+
+
+@pytest.mark.parametrize("t", GEMM_TYPES)
+@pytest.mark.parametrize("N,K,T", [(256, 1024, 70), (200, 2048, 130), (128, 5120, 33), (1024, 2048, 256)])
+def test_gemm_parity(Q, oracle, t, N, K, T):
+    W = oracle.quantize(t, synth.gaussian(N * 7 + K, N * K, 0, 0.02).reshape(N, K))
+    x = acts(T + K, T, K)
+    got = run_batch(Q, t, dev(W), x, N, K)
+    check_tokens(oracle, t, W, N, K, x, got)
+
+
+@pytest.mark.parametrize("t", GEMM_TYPES)
+def test_gemm_ldy_and_split_invariance(Q, oracle, t):
+    """prefill mode: every batch size takes the GEMM (one row included) and a token's sums do not depend on
+    how the prompt was cut (the reference's qmatvec_set_prefill contract, src/qmatvec.h:43-49)"""
+    N, K = 320, 1024
+    W = oracle.quantize(t, synth.gaussian(5, N * K, 0, 0.02).reshape(N, K))
+    Wd = dev(W)
+    x = acts(6, 150, K)
+    Q.lib().qmatvec_set_prefill(1)
+    try:
+        full = run_batch(Q, t, Wd, x, N, K, ldy=N + 13)
+        parts = np.concatenate([run_batch(Q, t, Wd, x[s:e], N, K) for s, e in ((0, 1), (1, 70), (70, 150))])
+    finally:
+        Q.lib().qmatvec_set_prefill(0)
+    assert np.array_equal(full.view(np.uint32), parts.view(np.uint32))
+    check_tokens(oracle, t, W, N, K, x[:3], full[:3])
+
+
+@pytest.mark.parametrize("t,N,K", [(100, 768, 2048), (100, 2048, 768), (8, 512, 1024), (101, 256, 1024)])
+def test_moe_tiled_gemm(Q, oracle, t, N, K):
+    """expert tiles from the grouping (config 4 shapes): entry i of tile k multiplies input row in_rows[i] by
+    expert tile_e[k] into output row out_rows[i]"""
+    import torch
+    E, n_used, T = 16, 4, 48
+    W = oracle.quantize(t, synth.gaussian(9, E * N * K, 0, 0.02).reshape(E * N, K))
+    ids = (synth.splitmix64(10, T * n_used) % np.uint64(E)).astype(np.int32).reshape(T, n_used)
+    tile = Q.lib().qmatvec_id_batch_tile(t, N, K)
+    assert tile >= 64
+    g = oracle.moe_group(ids, E, min(tile, 16))  # small tiles: several tiles per expert
+    x = acts(11, T, K)
+    q = Q.Q8(((T * K + 255) // 256) * 256)
+    Q.quantize(dev(x.reshape(-1)), T * K, q)
+    y = torch.full((T * n_used, N), float("nan"), dtype=torch.float32, device="cuda")
+    nt = np.array([g["n_tiles"]], np.int32)
+    L = Q.lib()
+    import ctypes as C
+    p = lambda a: C.c_void_p(a.data_ptr())
+    bufs = [dev(nt), dev(g["tile_e"]), dev(g["tile_start"]), dev(g["tile_n"]), dev(g["tok_rows"]),
+            dev(g["pair_rows"])]
+    rc = L.qmatvec_launch_q8_id_batch(t, p(dev(W)), Q.row_size(t, K), q.ref, p(y), N, K, g["n_tiles"] + 3,
+                                      min(tile, 16), *[p(b) for b in bufs], None)
+    assert rc == 0
+    got = host(y)
+    rb = W.shape[1]
+    for tt in range(T):
+        a = oracle.quantize_act(x[tt], t in (12, 14))
+        for j in range(n_used):
+            want, _, mag = oracle.matvec(t, W.reshape(E, N, rb)[ids[tt, j]], N, K, a)
+            assert np.all(np.abs(got[tt * n_used + j] - want) <= TOL * mag)
