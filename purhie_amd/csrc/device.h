@@ -63,11 +63,19 @@ __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32
 // 4-byte aligned global loads (the compiler merges consecutive ones into dwordx2/x4)
 __device__ __forceinline__ uint32_t ld32(const uint8_t *p) { return *(const uint32_t *)p; }
 
+// the same, non-temporal: weights stream past the caches once (the activation stays cached)
+__device__ __forceinline__ uint32_t ld32_nt(const uint8_t *p) { return __builtin_nontemporal_load((const uint32_t *)p); }
+
 struct u32x4 {
     uint32_t x, y, z, w;
 };
 __device__ __forceinline__ u32x4 ld128(const uint8_t *p) {  // 16-byte aligned
     const uint4 v = *(const uint4 *)p;
+    return {v.x, v.y, v.z, v.w};
+}
+typedef uint32_t u32v4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 ld128_nt(const uint8_t *p) {  // 16-byte aligned, non-temporal
+    const u32v4 v = __builtin_nontemporal_load((const u32v4 *)p);
     return {v.x, v.y, v.z, v.w};
 }
 

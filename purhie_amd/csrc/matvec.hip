@@ -20,7 +20,7 @@
 namespace pq {
 
 constexpr int MV_THREADS = 256;
-constexpr int MV_U = 4;  // tasks a lane keeps in flight
+constexpr int MV_U = 8;  // tasks a lane keeps in flight
 
 // ---------------------------------------------------------------- activation view (LDS)
 template <int NT>
@@ -49,7 +49,7 @@ struct Mv<TY_Q8_0> {
     __device__ static void load(const uint8_t *wr, int task, Raw &r) {
         const uint8_t *p = wr + (long long)task * 68;
 #pragma unroll
-        for (int k = 0; k < 17; ++k) r.w[k] = ld32(p + 4 * k);
+        for (int k = 0; k < 17; ++k) r.w[k] = ld32_nt(p + 4 * k);
     }
     template <int NT>
     __device__ static void compute(const Raw &r, int task, int, const Act<NT> &x, float acc[NT]) {
@@ -114,7 +114,7 @@ struct Mv<TY_FP4> {
     __device__ static void load(const uint8_t *wr, int task, Raw &r) {
         const uint8_t *p = wr + (long long)task * 36;
 #pragma unroll
-        for (int k = 0; k < 9; ++k) r.w[k] = ld32(p + 4 * k);
+        for (int k = 0; k < 9; ++k) r.w[k] = ld32_nt(p + 4 * k);
     }
     template <int NT>
     __device__ static void compute(const Raw &r, int task, int, const Act<NT> &x, float acc[NT]) {
@@ -153,7 +153,7 @@ struct Mv<TY_FAST> {
     __device__ static void load(const uint8_t *wr, int task, Raw &r) {
         const uint8_t *p = wr + (long long)task * 68;
 #pragma unroll
-        for (int k = 0; k < 17; ++k) r.w[k] = ld32(p + 4 * k);
+        for (int k = 0; k < 17; ++k) r.w[k] = ld32_nt(p + 4 * k);
     }
     __device__ static __forceinline__ uint32_t dw(const uint32_t *w, int off) {  // off compile-time
         return (off & 3) == 0 ? w[off >> 2] : align_bytes(w[(off >> 2) + 1], w[off >> 2], off & 3);
@@ -196,8 +196,8 @@ struct Mv<TY_Q4_K> {
     };
     __device__ static void load(const uint8_t *wr, int task, Raw &r) {
         const uint8_t *p = wr + (long long)(task >> 3) * 144;
-        r.h = ld128(p);
-        r.qs = ld128(p + 16 + 16 * (task & 7));
+        r.h = ld128_nt(p);
+        r.qs = ld128_nt(p + 16 + 16 * (task & 7));
     }
     // 6-bit scales of sub-blocks 2c, 2c + 1 and the min of sub-block s from the scale dwords y, z, w
     // (bytes 4..15 of the block), gathered with v_perm_b32 using lane-constant selectors.
@@ -288,8 +288,8 @@ struct Mv<TY_Q6_K> {
         const uint8_t *a1 = b + 64 * h + rr - off, *a2 = b + 128 + 32 * h + l - off;
 #pragma unroll
         for (int k = 0; k < 5; ++k) {
-            r.ql[k] = ld32(a1 + 4 * k);
-            r.qh[k] = ld32(a2 + 4 * k);
+            r.ql[k] = ld32_nt(a1 + 4 * k);
+            r.qh[k] = ld32_nt(a2 + 4 * k);
         }
         r.off = off;
         const int g_lo = 8 * h + (l >> 4) + (second ? 2 : 0);
@@ -355,7 +355,7 @@ __device__ __forceinline__ void stage_act(const StageCtx &c) {
 
 // ---------------------------------------------------------------- the row loop shared by the kernels
 
-template <int TYPE, int NT>
+template <int TYPE, int NT, bool STAGE>
 __device__ __forceinline__ void row_sum(const uint8_t *wr, int K, int gl, int L, const Act<NT> &x, float acc[NT],
                                         bool valid, const StageCtx &stage) {
     using P = Mv<TYPE>;
@@ -365,11 +365,11 @@ __device__ __forceinline__ void row_sum(const uint8_t *wr, int K, int gl, int L,
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
     typename P::Raw raw[MV_U];
     int task = gl;
-    // first batch in flight before the activation is staged
+    // first batch in flight before the activation is staged (STAGE) or read through the caches
 #pragma unroll
     for (int u = 0; u < MV_U; ++u)
         if (valid && task + u * L < ntask) P::load(wr, task + u * L, raw[u]);
-    stage_act(stage);
+    if (STAGE) stage_act(stage);
     if (!valid) return;
     for (;;) {
 #pragma unroll
@@ -418,11 +418,25 @@ __device__ __forceinline__ void setup_lds(uint8_t *smem, const int8_t *q, const 
 // ---------------------------------------------------------------- dense decode kernel
 
 template <int TYPE, int NT>
+__device__ __forceinline__ void global_act(const int8_t *q, const float *d, const int32_t *bs, int K, Act<NT> &x) {
+    const int nblk = K / act_blk<TYPE>();
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        x.q[t] = q + t * K;
+        x.d[t] = d + t * nblk;
+        x.bs[t] = bs + t * (K / 16);
+    }
+}
+
+// STAGE: the activation staged in LDS once per workgroup behind a barrier; otherwise read through the
+// L1 / L2 caches (the weights stream past them with non-temporal loads), every wave independent.
+template <int TYPE, int NT, bool STAGE>
 __global__ void __launch_bounds__(MV_THREADS) k_matvec(MvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     StageCtx c;
     Act<NT> x;
-    setup_lds<TYPE, NT>(smem, a.q, a.d, a.bs, a.K, c, x);
+    if (STAGE) setup_lds<TYPE, NT>(smem, a.q, a.d, a.bs, a.K, c, x);
+    else global_act<TYPE, NT>(a.q, a.d, a.bs, a.K, x);
     const int L = a.L;
     const int lane = threadIdx.x & 63, gl = lane & (L - 1);
     const int row = (blockIdx.x * (MV_THREADS / 64) + (threadIdx.x >> 6)) * (64 / L) + lane / L;
@@ -431,7 +445,7 @@ __global__ void __launch_bounds__(MV_THREADS) k_matvec(MvArgs a) {
     const int base = mat == 0 ? 0 : a.bound[mat - 1];
     const uint8_t *wr = a.W[mat] + (long long)(row - base) * a.row_bytes;
     float acc[NT];
-    row_sum<TYPE, NT>(wr, a.K, gl, L, x, acc, valid, c);
+    row_sum<TYPE, NT, STAGE>(wr, a.K, gl, L, x, acc, valid, c);
     if (!valid) return;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -442,7 +456,7 @@ __global__ void __launch_bounds__(MV_THREADS) k_matvec(MvArgs a) {
 
 // ---------------------------------------------------------------- MoE expert-indexed kernel
 
-template <int TYPE>
+template <int TYPE, bool STAGE>
 __global__ void __launch_bounds__(MV_THREADS) k_matvec_id(MvIdArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int m = (int)blockIdx.y >= a.n_used ? 1 : 0;
@@ -453,14 +467,16 @@ __global__ void __launch_bounds__(MV_THREADS) k_matvec_id(MvIdArgs a) {
     const int kb = K / act_blk<TYPE>();
     StageCtx c;
     Act<1> x;
-    setup_lds<TYPE, 1>(smem, a.q + in_row * K, a.d + in_row * kb, a.bs ? a.bs + in_row * (K / 16) : nullptr, K, c, x);
+    const int32_t *bsr = a.bs ? a.bs + in_row * (K / 16) : nullptr;
+    if (STAGE) setup_lds<TYPE, 1>(smem, a.q + in_row * K, a.d + in_row * kb, bsr, K, c, x);
+    else global_act<TYPE, 1>(a.q + in_row * K, a.d + in_row * kb, bsr, K, x);
     const int L = a.L;
     const int lane = threadIdx.x & 63, gl = lane & (L - 1);
     const int row = (blockIdx.x * (MV_THREADS / 64) + (threadIdx.x >> 6)) * (64 / L) + lane / L;
     const bool valid = row < a.N;
     const uint8_t *wr = e >= 0 ? a.W[m] + ((long long)e * a.N + row) * a.row_bytes : a.Wx[m] + (long long)row * a.row_bytes;
     float acc[1];
-    row_sum<TYPE, 1>(wr, K, gl, L, x, acc, valid, c);
+    row_sum<TYPE, 1, STAGE>(wr, K, gl, L, x, acc, valid, c);
     if (!valid) return;
     const float v = group_sum(acc[0], L);
     const float sc = e < 0 ? a.sx[m] : a.es[m] ? a.es[m][e] : a.s[m];
@@ -515,6 +531,12 @@ __global__ void k_block_dots(const uint8_t *W, long long rb, const int8_t *q, in
 
 // ---------------------------------------------------------------- host launchers
 
+// PURHIE_MV_STAGE=1: stage the activation in LDS (the A/B alternative of the cached reads)
+static bool stage_activations() {
+    static const bool v = getenv("PURHIE_MV_STAGE") && atoi(getenv("PURHIE_MV_STAGE")) != 0;
+    return v;
+}
+
 static int pow2_at_least(int v) {
     int p = 1;
     while (p < v) p <<= 1;
@@ -536,12 +558,13 @@ int matvec_lanes(int type, int K, long long rows) {
     case TY_Q6_K: nt = tasks_of<TY_Q6_K>(K); break;
     default: return 0;
     }
-    // about 4 tasks per lane, and at least 8 lanes (the K-quants' 8 quarters of a super-block)
-    int L = pow2_at_least((nt + 3) / 4);
+    // about 6 tasks per lane (all of a lane's loads in flight at once, MV_U = 8), at least 8 lanes (the
+    // K-quants' 8 quarters of a super-block)
+    int L = pow2_at_least((nt + 5) / 6);
     if (L < 8) L = 8;
     if (L > 64) L = 64;
     // few rows in the launch: more lanes per row, to keep enough waves in flight
-    while (L < 64 && rows * L / 64 < 4096 && nt > L) L <<= 1;
+    while (L < 64 && rows * L / 64 < 2048 && nt > L) L <<= 1;
     if (const char *e = getenv("PURHIE_MV_LANES")) {
         const int v = atoi(e);
         if (v >= 8 && v <= 64 && (v & (v - 1)) == 0) L = v;
@@ -554,8 +577,10 @@ static hipError_t launch_t(const MvArgs &a, hipStream_t stream) {
     const int rows_per_wg = (MV_THREADS / 64) * (64 / a.L);
     const unsigned grid = (unsigned)((a.Nt + rows_per_wg - 1) / rows_per_wg);
     const size_t lds = (size_t)lds_bytes<TYPE>(a.K, NT);
-    if (lds > 65536) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k_matvec<TYPE, NT>), dim3(grid), dim3(MV_THREADS), lds, stream, a);
+    if (stage_activations() && lds <= 65536)
+        hipLaunchKernelGGL((k_matvec<TYPE, NT, true>), dim3(grid), dim3(MV_THREADS), lds, stream, a);
+    else
+        hipLaunchKernelGGL((k_matvec<TYPE, NT, false>), dim3(grid), dim3(MV_THREADS), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -586,8 +611,10 @@ static hipError_t launch_id_t(const MvIdArgs &a, hipStream_t stream) {
     const int rows_per_wg = (MV_THREADS / 64) * (64 / a.L);
     const dim3 grid((unsigned)((a.N + rows_per_wg - 1) / rows_per_wg), (unsigned)(a.n_used * a.nmat), (unsigned)a.T);
     const size_t lds = (size_t)lds_bytes<TYPE>(a.K, 1);
-    if (lds > 65536) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k_matvec_id<TYPE>), grid, dim3(MV_THREADS), lds, stream, a);
+    if (stage_activations() && lds <= 65536)
+        hipLaunchKernelGGL((k_matvec_id<TYPE, true>), grid, dim3(MV_THREADS), lds, stream, a);
+    else
+        hipLaunchKernelGGL((k_matvec_id<TYPE, false>), grid, dim3(MV_THREADS), 0, stream, a);
     return hipGetLastError();
 }
 
