@@ -31,29 +31,27 @@ __device__ __forceinline__ float ue4m3_half(uint32_t e) {
 // signed int8 dot of 4 bytes, accumulated: v_dot4_i32_i8
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
-// Four 4-bit ROCmFP4 codes (one per byte, 0..15, sign in bit 3) -> four int8 codebook values
-// {0, 1, 2, 3, 4, 6, 8, 10} with the sign: two byte lookups (v_perm_b32: positive and negative tables of
-// 8) and a byte select by the sign mask. The sign mask is built with v_perm's sign-replicating selectors
-// (selector 8..11 = bit 7 of bytes 1, 3, 5, 7 of {S0:S1}) after moving each code's bit 3 to bit 7.
-__device__ __forceinline__ int fp4x4(uint32_t n) {
-    const uint32_t sel = n & 0x07070707u;
+// Four 4-bit ROCmFP4 codes -> four int8 codebook values {0, 1, 2, 3, 4, 6, 8, 10} with the sign in bit 3:
+// two byte lookups by the 3-bit magnitude index (v_perm_b32 on a positive and a negative table of 8), then
+// a third v_perm picks, per byte, the positive (selector i) or the negative (selector 4 + i) result, the
+// selector built from the sign bit. sel: the magnitude indices (bytes 0..7); sgn4: 4 in the bytes whose
+// code is negative, 0 elsewhere.
+__device__ __forceinline__ int fp4_pick(uint32_t sel, uint32_t sgn4) {
     const uint32_t pos = __builtin_amdgcn_perm(0x0a080604u, 0x03020100u, sel);
     const uint32_t neg = __builtin_amdgcn_perm(0xf6f8fafcu, 0xfdfeff00u, sel);
-    const uint32_t s = n << 4;  // bit 3 of byte i -> bit 7 of byte i
-    const uint32_t m = __builtin_amdgcn_perm(s, s << 8, 0x0b090a08u);
-    return (int)((pos & ~m) | (neg & m));
+    return (int)__builtin_amdgcn_perm(neg, pos, 0x03020100u | sgn4);
 }
 
-// Four 4-bit codes taken from the high nibbles of the bytes of w
+// the codes in the low nibbles of the bytes of w
+__device__ __forceinline__ int fp4x4_lo(uint32_t w) { return fp4_pick(w & 0x07070707u, (w & 0x08080808u) >> 1); }
+
+// the codes in the high nibbles of the bytes of w
 __device__ __forceinline__ int fp4x4_hi(uint32_t w) {
-    const uint32_t sel = (w >> 4) & 0x07070707u;
-    const uint32_t pos = __builtin_amdgcn_perm(0x0a080604u, 0x03020100u, sel);
-    const uint32_t neg = __builtin_amdgcn_perm(0xf6f8fafcu, 0xfdfeff00u, sel);
-    const uint32_t m = __builtin_amdgcn_perm(w, w << 8, 0x0b090a08u);  // bit 7 of each byte
-    return (int)((pos & ~m) | (neg & m));
+    return fp4_pick((w >> 4) & 0x07070707u, (w & 0x80808080u) >> 5);
 }
 
-__device__ __forceinline__ int fp4x4_lo(uint32_t w) { return fp4x4(w & 0x0f0f0f0fu); }
+// four codes, one per byte (0..15)
+__device__ __forceinline__ int fp4x4(uint32_t n) { return fp4x4_lo(n); }
 
 // the dword starting `off` bytes (0..3, run-time) into the 8 bytes {hi:lo}
 __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t off) {
@@ -98,5 +96,38 @@ __device__ __forceinline__ float group_sum(float v, int L) {
     for (int off = L >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
     return v;
 }
+
+// Row r of a dense launch: its weights and output (token t at out + t * ystride), and the output scale.
+// The argument arrays are read with constant indices and selected: a run-time index into a kernel-argument
+// array is a memory load, and its wait would also wait for every weight load issued before it.
+struct DenseRows {
+    const MvArgs &a;
+    template <class T>
+    __device__ static T pick(int m, T v0, T v1, T v2, T v3) {
+        return m == 0 ? v0 : m == 1 ? v1 : m == 2 ? v2 : v3;
+    }
+    __device__ int mat(int row) const { return (row >= a.bound[0]) + (row >= a.bound[1]) + (row >= a.bound[2]); }
+    __device__ int base(int m) const { return pick(m, 0, a.bound[0], a.bound[1], a.bound[2]); }
+    __device__ const uint8_t *w(int row) const {
+        const int m = mat(row);
+        return pick(m, a.W[0], a.W[1], a.W[2], a.W[3]) + (long long)(row - base(m)) * a.row_bytes;
+    }
+    __device__ void store(int row, int t, float v) const {
+        const int m = mat(row);
+        float *y = pick(m, a.y[0], a.y[1], a.y[2], a.y[3]);
+        const long long ys = pick(m, a.ystride[0], a.ystride[1], a.ystride[2], a.ystride[3]);
+        y[(long long)t * ys + (row - base(m))] = v * pick(m, a.osc[0], a.osc[1], a.osc[2], a.osc[3]);
+    }
+};
+
+// Rows of one (matrix, slot, token) of an expert-indexed launch
+struct IdRows {
+    const uint8_t *W;
+    long long rb;
+    float *y;
+    float sc;
+    __device__ const uint8_t *w(int row) const { return W + (long long)row * rb; }
+    __device__ void store(int row, int, float v) const { y[row] = v * sc; }
+};
 
 }  // namespace pq

@@ -54,6 +54,11 @@ struct MvIdArgs {
 };
 hipError_t launch_matvec_id(int type, const MvIdArgs &a, hipStream_t stream);
 
+// the one-unit-per-lane tile kernels (mv_tile.hip); hipErrorNotSupported for a shape or alignment they do
+// not take (launch_matvec / launch_matvec_id then use the per-wave kernels)
+hipError_t launch_matvec_tile(int type, const MvArgs &a, hipStream_t stream);
+hipError_t launch_matvec_id_tile(int type, const MvIdArgs &a, hipStream_t stream);
+
 // per-scale-group integer dots (test hook)
 hipError_t launch_block_dots(int type, const uint8_t *W, long long row_bytes, const int8_t *q, int32_t *out, int N,
                              int K, hipStream_t stream);

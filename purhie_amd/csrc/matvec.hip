@@ -2,15 +2,16 @@
 //
 // Replaces the reference's matvec_q8_<type> / matvec_q8t_<type> / matvec_q8_id_<type>
 // (src/matvec_q.hip:1403-1965). Structure, MI355X-first:
-//   * a workgroup of 4 waves; L lanes (8..64, a power of two) per row, 64 / L rows per wave;
-//   * each lane streams a fixed number of "tasks" (a pair of Q8_0 / ROCmFP4 blocks, a quad of FAST
-//     blocks, or one 16-byte quarter-chunk of a K-quant super-block) with wide global loads, U tasks in
-//     flight before any arithmetic;
-//   * the quantized activation (Q8_0 or Q8_K form, up to 4 tokens) is staged once per workgroup in LDS
-//     while the first weight loads are in flight, and read back with 128-bit LDS reads;
-//   * integer dots with v_dot4_i32_i8 on codes decoded by v_perm_b32 byte tables;
-//   * per task a float term in the reference's per-block form (scale_w * scale_x) * int_sum, summed
-//     per lane in task order, then a butterfly over the row's L lanes.
+//   * a workgroup of 4 waves; L lanes (8..64, a power of two, a compile-time constant) per row, 64 / L
+//     rows per wave; L is picked per shape so that a lane has about 6 "tasks" (a pair of Q8_0 / ROCmFP4
+//     blocks, a quad of FAST blocks, or one 16-byte quarter of a K-quant super-block);
+//   * every lane issues all its tasks' weight loads (wide, non-temporal: the weights stream past the
+//     caches once) before any arithmetic, from one base pointer with compile-time offsets;
+//   * the quantized activation (Q8_0 or Q8_K form, up to 4 tokens) is read through the L1 / L2 caches,
+//     where it stays for every row of the launch; no barrier, every wave independent;
+//   * integer dots with v_dot4_i32_i8 on codes decoded by v_perm_b32 byte tables, 24-bit integer
+//     scale products, and per task a float term in the reference's per-block form
+//     (scale_w * scale_x) * int_sum, summed per lane in task order, then a butterfly over the row's lanes.
 // Per-block integer sums are exact, and the same as the reference's; the float order differs from the
 // reference CPU path's sequential sum (checked to 1e-5 of sum |w x| by the parity tests). A token's
 // result does not depend on how many tokens share the launch (the same code per token).
@@ -22,7 +23,7 @@ namespace pq {
 constexpr int MV_THREADS = 256;
 constexpr int MV_U = 8;  // tasks a lane keeps in flight
 
-// ---------------------------------------------------------------- activation view (LDS)
+// quantized activation of NT tokens, already offset to the lane's first task
 template <int NT>
 struct Act {
     const int8_t *q[NT];
@@ -30,7 +31,12 @@ struct Act {
     const int32_t *bs[NT];
 };
 
+__device__ __forceinline__ int mul24(int a, int b) { return __mul24(a, b); }
+
 // ---------------------------------------------------------------- per-type task policies
+// For a lane with index gl among its row's L lanes: wbase / xoff / doff / boff locate its first task in the
+// row's weights and in the activation (values, scales, group sums); consecutive tasks of the lane are
+// W_STEP / X_STEP / D_STEP / B_STEP further on (compile-time, given L).
 
 template <int TYPE>
 struct Mv;
@@ -43,16 +49,25 @@ struct Mv<TY_Q8_0> {
     static constexpr int ACT_BLK = 32;
     static constexpr bool KQ = false;
     __host__ __device__ static int tasks(int K) { return K / 64; }
+    static constexpr int LDIV = 1, W_UNIT = 68, X_UNIT = 64, D_UNIT = 2, B_UNIT = 0;
+    static constexpr int U = 3;  // tasks in flight per buffer (17 dwords each)
+    struct Lane {
+        __device__ Lane(int) {}
+    };
+    __device__ static long long wbase(int gl) { return 68LL * gl; }
+    __device__ static int xoff(int gl) { return 64 * gl; }
+    __device__ static int doff(int gl) { return 2 * gl; }
+    __device__ static int boff(int) { return 0; }
     struct Raw {
         uint32_t w[17];
     };
-    __device__ static void load(const uint8_t *wr, int task, Raw &r) {
-        const uint8_t *p = wr + (long long)task * 68;
+    __device__ static void load(const uint8_t *p, Raw &r) {
 #pragma unroll
         for (int k = 0; k < 17; ++k) r.w[k] = ld32_nt(p + 4 * k);
     }
     template <int NT>
-    __device__ static void compute(const Raw &r, int task, int, const Act<NT> &x, float acc[NT]) {
+    __device__ static void compute(const Raw &r, const Lane &, const Act<NT> &x, int xo, int dof, int, float acc[NT],
+                                   bool v) {
         uint32_t qa[8], qb[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -62,7 +77,7 @@ struct Mv<TY_Q8_0> {
         const float e0 = h2f(r.w[0] & 0xffffu), e1 = h2f(r.w[8] >> 16);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const int4 *xv = (const int4 *)(x.q[t] + task * 64);
+            const int4 *xv = (const int4 *)(x.q[t] + xo);
             const int4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
             int s0 = dot4((int)qa[0], x0.x, 0);
             s0 = dot4((int)qa[1], x0.y, s0);
@@ -80,9 +95,9 @@ struct Mv<TY_Q8_0> {
             s1 = dot4((int)qb[5], x3.y, s1);
             s1 = dot4((int)qb[6], x3.z, s1);
             s1 = dot4((int)qb[7], x3.w, s1);
-            const float2 dx = *(const float2 *)(x.d[t] + 2 * task);
-            acc[t] = __builtin_fmaf(e0 * dx.x, (float)s0, acc[t]);
-            acc[t] = __builtin_fmaf(e1 * dx.y, (float)s1, acc[t]);
+            const float2 dx = *(const float2 *)(x.d[t] + dof);
+            acc[t] = __builtin_fmaf(v ? e0 * dx.x : 0.0f, (float)s0, acc[t]);
+            acc[t] = __builtin_fmaf(v ? e1 * dx.y : 0.0f, (float)s1, acc[t]);
         }
     }
 };
@@ -108,16 +123,25 @@ struct Mv<TY_FP4> {
     static constexpr int ACT_BLK = 32;
     static constexpr bool KQ = false;
     __host__ __device__ static int tasks(int K) { return K / 64; }
+    static constexpr int LDIV = 1, W_UNIT = 36, X_UNIT = 64, D_UNIT = 2, B_UNIT = 0;
+    static constexpr int U = 5;  // 9 dwords each
+    struct Lane {
+        __device__ Lane(int) {}
+    };
+    __device__ static long long wbase(int gl) { return 36LL * gl; }
+    __device__ static int xoff(int gl) { return 64 * gl; }
+    __device__ static int doff(int gl) { return 2 * gl; }
+    __device__ static int boff(int) { return 0; }
     struct Raw {
         uint32_t w[9];
     };
-    __device__ static void load(const uint8_t *wr, int task, Raw &r) {
-        const uint8_t *p = wr + (long long)task * 36;
+    __device__ static void load(const uint8_t *p, Raw &r) {
 #pragma unroll
         for (int k = 0; k < 9; ++k) r.w[k] = ld32_nt(p + 4 * k);
     }
     template <int NT>
-    __device__ static void compute(const Raw &r, int task, int, const Act<NT> &x, float acc[NT]) {
+    __device__ static void compute(const Raw &r, const Lane &, const Act<NT> &x, int xo, int dof, int, float acc[NT],
+                                   bool v) {
         const uint32_t qa[4] = {r.w[0], r.w[1], r.w[2], r.w[3]};
         uint32_t qb[4];
 #pragma unroll
@@ -126,11 +150,12 @@ struct Mv<TY_FP4> {
         const float eb0 = ue4m3_half(r.w[8] >> 16), eb1 = ue4m3_half(r.w[8] >> 24);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const int4 *xv = (const int4 *)(x.q[t] + task * 64);
+            const int4 *xv = (const int4 *)(x.q[t] + xo);
             int a0, a1, b0, b1;
             fp4_block_dots(qa, xv[0], xv[1], a0, a1);
             fp4_block_dots(qb, xv[2], xv[3], b0, b1);
-            const float2 dx = *(const float2 *)(x.d[t] + 2 * task);
+            const float2 dl = *(const float2 *)(x.d[t] + dof);
+            const float2 dx = v ? dl : make_float2(0.0f, 0.0f);  // (UE4M3 scales are finite: 0 x e = 0)
             const float ta = __builtin_fmaf(ea1 * dx.x, (float)a1, ea0 * dx.x * (float)a0);
             const float tb = __builtin_fmaf(eb1 * dx.y, (float)b1, eb0 * dx.y * (float)b0);
             acc[t] += ta;
@@ -147,11 +172,19 @@ struct Mv<TY_FAST> {
     static constexpr int ACT_BLK = 32;
     static constexpr bool KQ = false;
     __host__ __device__ static int tasks(int K) { return K / 128; }
+    static constexpr int LDIV = 1, W_UNIT = 68, X_UNIT = 128, D_UNIT = 4, B_UNIT = 0;
+    static constexpr int U = 3;  // 17 dwords each
+    struct Lane {
+        __device__ Lane(int) {}
+    };
+    __device__ static long long wbase(int gl) { return 68LL * gl; }
+    __device__ static int xoff(int gl) { return 128 * gl; }
+    __device__ static int doff(int gl) { return 4 * gl; }
+    __device__ static int boff(int) { return 0; }
     struct Raw {
         uint32_t w[17];
     };
-    __device__ static void load(const uint8_t *wr, int task, Raw &r) {
-        const uint8_t *p = wr + (long long)task * 68;
+    __device__ static void load(const uint8_t *p, Raw &r) {
 #pragma unroll
         for (int k = 0; k < 17; ++k) r.w[k] = ld32_nt(p + 4 * k);
     }
@@ -159,7 +192,8 @@ struct Mv<TY_FAST> {
         return (off & 3) == 0 ? w[off >> 2] : align_bytes(w[(off >> 2) + 1], w[off >> 2], off & 3);
     }
     template <int NT>
-    __device__ static void compute(const Raw &r, int task, int, const Act<NT> &x, float acc[NT]) {
+    __device__ static void compute(const Raw &r, const Lane &, const Act<NT> &x, int xo, int dof, int, float acc[NT],
+                                   bool v) {
         uint32_t w[18];
 #pragma unroll
         for (int k = 0; k < 17; ++k) w[k] = r.w[k];
@@ -172,10 +206,10 @@ struct Mv<TY_FAST> {
             const float e = ue4m3_half(dw(w, 17 * j + 16));
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const int4 *xv = (const int4 *)(x.q[t] + task * 128 + 32 * j);
+                const int4 *xv = (const int4 *)(x.q[t] + xo + 32 * j);
                 int s0, s1;
                 fp4_block_dots(qs, xv[0], xv[1], s0, s1);
-                acc[t] = __builtin_fmaf(e * x.d[t][4 * task + j], (float)(s0 + s1), acc[t]);
+                acc[t] = __builtin_fmaf(v ? e * x.d[t][dof + j] : 0.0f, (float)(s0 + s1), acc[t]);
             }
         }
     }
@@ -185,56 +219,64 @@ struct Mv<TY_FAST> {
 // qs bytes 16 s .. 16 s + 15, i.e. chunk c = s / 2, values 64 c + l + 0..15 (low nibbles, sub-block 2c)
 // and 64 c + 32 + l + 0..15 (high nibbles, sub-block 2c + 1), l = 16 (s & 1); plus the block header
 // (d, dmin, the 12 scale bytes). The lane with quarter s also applies sub-block s's min through the Q8_K
-// group sums 2 s, 2 s + 1 (reference src/matvec_q.hip:1752-1789).
+// group sums 2 s, 2 s + 1 (reference src/matvec_q.hip:1752-1789). A lane's quarter s is fixed (L % 8 == 0).
 template <>
 struct Mv<TY_Q4_K> {
     static constexpr int ACT_BLK = 256;
     static constexpr bool KQ = true;
     __host__ __device__ static int tasks(int K) { return K / 256 * 8; }
+    static constexpr int LDIV = 8, W_UNIT = 144, X_UNIT = 256, D_UNIT = 1, B_UNIT = 16;
+    static constexpr int U = 6;  // 8 dwords each
+    // 6-bit scales of sub-blocks 2c, 2c + 1 and the min of sub-block s from the scale dwords y, z, w
+    // (bytes 4..15 of the block), gathered with v_perm_b32 using the lane's selectors:
+    //   scales: (perm(w, y, p) & pmask) | ((perm(w, y, q) >> 6) & 0x0303) << 4
+    //   min:    ((perm(w, z, m) >> msh) & mmask) | ((perm(w, z, n) >> 6) & 3) << 4
+    struct Lane {
+        uint32_t p, pmask, q, m, msh, mmask, n;
+        __device__ Lane(int gl) {
+            const int s = gl & 7, c = s >> 1;
+            if (c < 2) {  // sub-blocks 2c, 2c + 1 < 4: scale = byte j & 63 (y)
+                p = (uint32_t)(2 * c) | (uint32_t)(2 * c + 1) << 8 | 0x0c0c0000u;
+                pmask = 0x3f3fu;
+                q = 0x0c0c0c0cu;
+            } else {  // j = 4 + i: scale = (w byte i & 15) | (y byte i >> 6) << 4
+                const int i = 2 * c - 4;
+                p = (uint32_t)(4 + i) | (uint32_t)(5 + i) << 8 | 0x0c0c0000u;
+                pmask = 0x0f0fu;
+                q = (uint32_t)i | (uint32_t)(i + 1) << 8 | 0x0c0c0000u;
+            }
+            if (s < 4) {  // min = z byte s & 63
+                m = (uint32_t)s | 0x0c0c0c00u;
+                msh = 0;
+                mmask = 63;
+                n = 0x0c0c0c0cu;
+            } else {  // min = (w byte i >> 4) | (z byte i >> 6) << 4
+                const int i = s - 4;
+                m = (uint32_t)(4 + i) | 0x0c0c0c00u;
+                msh = 4;
+                mmask = 15;
+                n = (uint32_t)i | 0x0c0c0c00u;
+            }
+        }
+    };
+    __device__ static long long wbase(int gl) { return 144LL * (gl >> 3); }
+    __device__ static int xoff(int gl) {
+        const int s = gl & 7;
+        return 256 * (gl >> 3) + 64 * (s >> 1) + 16 * (s & 1);
+    }
+    __device__ static int doff(int gl) { return gl >> 3; }
+    __device__ static int boff(int gl) { return 16 * (gl >> 3) + 2 * (gl & 7); }
     struct Raw {
         u32x4 h, qs;
     };
-    __device__ static void load(const uint8_t *wr, int task, Raw &r) {
-        const uint8_t *p = wr + (long long)(task >> 3) * 144;
+    // the task's block header and its quarter s of qs; p = the block header of the lane's current task
+    __device__ static void load(const uint8_t *p, Raw &r, int s) {
         r.h = ld128_nt(p);
-        r.qs = ld128_nt(p + 16 + 16 * (task & 7));
-    }
-    // 6-bit scales of sub-blocks 2c, 2c + 1 and the min of sub-block s from the scale dwords y, z, w
-    // (bytes 4..15 of the block), gathered with v_perm_b32 using lane-constant selectors.
-    struct Sel {
-        uint32_t p, pmask, q;   // scales: (perm(w, y, p) & pmask) | ((perm(w, y, q) >> 6) & 0x0303) << 4
-        uint32_t m, msh, mmask, n;  // min: ((perm(w, z, m) >> msh) & mmask) | ((perm(w, z, n) >> 6) & 3) << 4
-    };
-    __device__ static Sel selectors(int s) {
-        const int c = s >> 1;
-        Sel o;
-        if (c < 2) {  // sub-blocks 2c, 2c + 1 < 4: scale = byte j & 63 (y)
-            o.p = (uint32_t)(2 * c) | (uint32_t)(2 * c + 1) << 8 | 0x0c0c0000u;
-            o.pmask = 0x3f3fu;
-            o.q = 0x0c0c0c0cu;
-        } else {  // j = 4 + i: scale = (w byte i & 15) | (y byte i >> 6) << 4
-            const int i = 2 * c - 4;
-            o.p = (uint32_t)(4 + i) | (uint32_t)(5 + i) << 8 | 0x0c0c0000u;
-            o.pmask = 0x0f0fu;
-            o.q = (uint32_t)i | (uint32_t)(i + 1) << 8 | 0x0c0c0000u;
-        }
-        if (s < 4) {  // min = z byte s & 63
-            o.m = (uint32_t)s | 0x0c0c0c00u;
-            o.msh = 0;
-            o.mmask = 63;
-            o.n = 0x0c0c0c0cu;
-        } else {  // min = (w byte i >> 4) | (z byte i >> 6) << 4
-            const int i = s - 4;
-            o.m = (uint32_t)(4 + i) | 0x0c0c0c00u;
-            o.msh = 4;
-            o.mmask = 15;
-            o.n = (uint32_t)i | 0x0c0c0c00u;
-        }
-        return o;
+        r.qs = ld128_nt(p + 16 + 16 * s);
     }
     template <int NT>
-    __device__ static void compute(const Raw &r, int task, int s, const Act<NT> &x, float acc[NT]) {
-        const Sel o = selectors(s);
+    __device__ static void compute(const Raw &r, const Lane &o, const Act<NT> &x, int xo, int dof, int bo,
+                                   float acc[NT], bool v) {
         const uint32_t sc2 = (__builtin_amdgcn_perm(r.h.w, r.h.y, o.p) & o.pmask) |
                              (((__builtin_amdgcn_perm(r.h.w, r.h.y, o.q) >> 6) & 0x0303u) << 4);
         const int sc_lo = (int)(sc2 & 0xffu), sc_hi = (int)(sc2 >> 8);
@@ -242,25 +284,30 @@ struct Mv<TY_Q4_K> {
                              (((__builtin_amdgcn_perm(r.h.w, r.h.z, o.n) >> 6) & 3u) << 4));
         const float dw = h2f(r.h.x & 0xffffu), dm = h2f(r.h.x >> 16);
         const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
-        const int sb = task >> 3, c = s >> 1, l = (s & 1) * 16;
+        int lo[4], hi[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            lo[k] = (int)(q[k] & 0x0f0f0f0fu);
+            hi[k] = (int)((q[k] >> 4) & 0x0f0f0f0fu);
+        }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const int8_t *xb = x.q[t] + sb * 256 + 64 * c + l;
+            const int8_t *xb = x.q[t] + xo;
             const int4 xl = *(const int4 *)xb, xh = *(const int4 *)(xb + 32);
-            int slo = dot4((int)(q[0] & 0x0f0f0f0fu), xl.x, 0);
-            slo = dot4((int)(q[1] & 0x0f0f0f0fu), xl.y, slo);
-            slo = dot4((int)(q[2] & 0x0f0f0f0fu), xl.z, slo);
-            slo = dot4((int)(q[3] & 0x0f0f0f0fu), xl.w, slo);
-            int shi = dot4((int)((q[0] >> 4) & 0x0f0f0f0fu), xh.x, 0);
-            shi = dot4((int)((q[1] >> 4) & 0x0f0f0f0fu), xh.y, shi);
-            shi = dot4((int)((q[2] >> 4) & 0x0f0f0f0fu), xh.z, shi);
-            shi = dot4((int)((q[3] >> 4) & 0x0f0f0f0fu), xh.w, shi);
-            const int2 b2 = *(const int2 *)(x.bs[t] + sb * 16 + 2 * s);
-            const int isum = sc_lo * slo + sc_hi * shi;
-            const int msum = mn * (b2.x + b2.y);
-            const float dx = x.d[t][sb];
-            acc[t] = __builtin_fmaf(dw * dx, (float)isum, acc[t]);
-            acc[t] = __builtin_fmaf(-(dm * dx), (float)msum, acc[t]);
+            int slo = dot4(lo[0], xl.x, 0);
+            slo = dot4(lo[1], xl.y, slo);
+            slo = dot4(lo[2], xl.z, slo);
+            slo = dot4(lo[3], xl.w, slo);
+            int shi = dot4(hi[0], xh.x, 0);
+            shi = dot4(hi[1], xh.y, shi);
+            shi = dot4(hi[2], xh.z, shi);
+            shi = dot4(hi[3], xh.w, shi);
+            const int2 b2 = *(const int2 *)(x.bs[t] + bo);
+            const int isum = mul24(sc_lo, slo) + mul24(sc_hi, shi);
+            const int msum = mul24(mn, b2.x + b2.y);
+            const float dx = x.d[t][dof];
+            acc[t] = __builtin_fmaf(v ? dw * dx : 0.0f, (float)isum, acc[t]);
+            acc[t] = __builtin_fmaf(v ? -(dm * dx) : 0.0f, (float)msum, acc[t]);
         }
     }
 };
@@ -275,111 +322,115 @@ struct Mv<TY_Q6_K> {
     static constexpr int ACT_BLK = 256;
     static constexpr bool KQ = true;
     __host__ __device__ static int tasks(int K) { return K / 256 * 8; }
+    static constexpr int LDIV = 8, W_UNIT = 210, X_UNIT = 256, D_UNIT = 1, B_UNIT = 16;
+    static constexpr int U = 4;  // 14 dwords each
+    struct Lane {
+        int s, qlo, qho, sh, g_lo;
+        __device__ Lane(int gl) {
+            s = gl & 7;
+            const int h = s >> 2, rr = (s & 3) * 16, l = rr & 31, second = rr >= 32;
+            qlo = 64 * h + rr;
+            qho = 128 + 32 * h + l;
+            sh = second ? 2 : 0;
+            g_lo = 8 * h + (l >> 4) + (second ? 2 : 0);
+        }
+    };
+    __device__ static long long wbase(int gl) { return 210LL * (gl >> 3); }
+    __device__ static int xoff(int gl) {
+        const int s = gl & 7, h = s >> 2, rr = (s & 3) * 16;
+        return 256 * (gl >> 3) + 128 * h + (rr >= 32 ? 32 : 0) + (rr & 31);
+    }
+    __device__ static int doff(int gl) { return gl >> 3; }
+    __device__ static int boff(int gl) { return 16 * (gl >> 3) + 2 * (gl & 7); }
     struct Raw {
         uint32_t ql[5], qh[5];
         uint32_t off;
         int sc_lo, sc_hi;
         uint32_t scp, d;
     };
-    __device__ static void load(const uint8_t *wr, int task, Raw &r) {
-        const int s = task & 7, h = s >> 2, rr = (s & 3) * 16, l = rr & 31, second = rr >= 32;
-        const uint8_t *b = wr + (long long)(task >> 3) * 210;
+    __device__ static void load(const uint8_t *b, Raw &r, const Lane &o) {
         const uint32_t off = (uint32_t)((uintptr_t)b & 3u);
-        const uint8_t *a1 = b + 64 * h + rr - off, *a2 = b + 128 + 32 * h + l - off;
+        const uint8_t *a1 = b + o.qlo - off, *a2 = b + o.qho - off;
 #pragma unroll
         for (int k = 0; k < 5; ++k) {
             r.ql[k] = ld32_nt(a1 + 4 * k);
             r.qh[k] = ld32_nt(a2 + 4 * k);
         }
         r.off = off;
-        const int g_lo = 8 * h + (l >> 4) + (second ? 2 : 0);
-        r.sc_lo = (int)((const int8_t *)b)[192 + g_lo];
-        r.sc_hi = (int)((const int8_t *)b)[192 + g_lo + 4];
-        r.scp = *(const uint16_t *)(b + 192 + 2 * s);
+        r.sc_lo = (int)((const int8_t *)b)[192 + o.g_lo];
+        r.sc_hi = (int)((const int8_t *)b)[192 + o.g_lo + 4];
+        r.scp = *(const uint16_t *)(b + 192 + 2 * o.s);
         r.d = *(const uint16_t *)(b + 208);
     }
     template <int NT>
-    __device__ static void compute(const Raw &r, int task, int s, const Act<NT> &x, float acc[NT]) {
-        const int h = s >> 2, rr = (s & 3) * 16, l = rr & 31, second = rr >= 32;
-        const int sh = second ? 2 : 0;
-        const int v_lo = 128 * h + (second ? 32 : 0) + l;
-        uint32_t vlo[4], vhi[4];
+    __device__ static void compute(const Raw &r, const Lane &o, const Act<NT> &x, int xo, int dof, int bo,
+                                   float acc[NT], bool v) {
+        int vlo[4], vhi[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const uint32_t ql = align_bytes(r.ql[k + 1], r.ql[k], r.off);
             const uint32_t qh = align_bytes(r.qh[k + 1], r.qh[k], r.off);
-            vlo[k] = (ql & 0x0f0f0f0fu) | (((qh >> sh) & 0x03030303u) << 4);
-            vhi[k] = ((ql >> 4) & 0x0f0f0f0fu) | (((qh >> (sh + 4)) & 0x03030303u) << 4);
+            vlo[k] = (int)((ql & 0x0f0f0f0fu) | (((qh >> o.sh) & 0x03030303u) << 4));
+            vhi[k] = (int)(((ql >> 4) & 0x0f0f0f0fu) | (((qh >> (o.sh + 4)) & 0x03030303u) << 4));
         }
         const int sca = (int)(int8_t)(r.scp & 0xffu), scb = (int)(int8_t)(r.scp >> 8);
         const float dw = h2f(r.d);
-        const int sb = task >> 3;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const int8_t *xb = x.q[t] + sb * 256 + v_lo;
+            const int8_t *xb = x.q[t] + xo;
             const int4 xl = *(const int4 *)xb, xh = *(const int4 *)(xb + 64);
-            int slo = dot4((int)vlo[0], xl.x, 0);
-            slo = dot4((int)vlo[1], xl.y, slo);
-            slo = dot4((int)vlo[2], xl.z, slo);
-            slo = dot4((int)vlo[3], xl.w, slo);
-            int shi = dot4((int)vhi[0], xh.x, 0);
-            shi = dot4((int)vhi[1], xh.y, shi);
-            shi = dot4((int)vhi[2], xh.z, shi);
-            shi = dot4((int)vhi[3], xh.w, shi);
-            const int2 b2 = *(const int2 *)(x.bs[t] + sb * 16 + 2 * s);
-            int isum = r.sc_lo * slo + r.sc_hi * shi;
-            isum -= 32 * (sca * b2.x + scb * b2.y);
-            acc[t] = __builtin_fmaf(dw * x.d[t][sb], (float)isum, acc[t]);
+            int slo = dot4(vlo[0], xl.x, 0);
+            slo = dot4(vlo[1], xl.y, slo);
+            slo = dot4(vlo[2], xl.z, slo);
+            slo = dot4(vlo[3], xl.w, slo);
+            int shi = dot4(vhi[0], xh.x, 0);
+            shi = dot4(vhi[1], xh.y, shi);
+            shi = dot4(vhi[2], xh.z, shi);
+            shi = dot4(vhi[3], xh.w, shi);
+            const int2 b2 = *(const int2 *)(x.bs[t] + bo);
+            int isum = mul24(r.sc_lo, slo) + mul24(r.sc_hi, shi);
+            isum -= 32 * (mul24(sca, b2.x) + mul24(scb, b2.y));
+            acc[t] = __builtin_fmaf(v ? dw * x.d[t][dof] : 0.0f, (float)isum, acc[t]);
         }
     }
 };
 
-// Staging of NT tokens' activations into LDS: values (NT K bytes), scales (NT K / blk floats), group
-// sums (K-quants, NT K / 16 ints); the sources are contiguous (token t at + t K, ...).
-struct StageCtx {
-    const int8_t *q;
-    const float *d;
-    const int32_t *bs;
-    int8_t *sq;
-    float *sd;
-    int32_t *sbs;
-    int nq, nd, nbs;  // bytes, floats, ints
-};
+// ---------------------------------------------------------------- the lane loop shared by the kernels
 
-__device__ __forceinline__ void stage_act(const StageCtx &c) {
-    for (int i = threadIdx.x * 16; i < c.nq; i += MV_THREADS * 16) *(int4 *)(c.sq + i) = *(const int4 *)(c.q + i);
-    for (int i = threadIdx.x; i < c.nd; i += MV_THREADS) c.sd[i] = c.d[i];
-    for (int i = threadIdx.x; i < c.nbs; i += MV_THREADS) c.sbs[i] = c.bs[i];
-    __syncthreads();
+template <int TYPE>
+__device__ __forceinline__ void load_task(const uint8_t *p, typename Mv<TYPE>::Raw &r, const typename Mv<TYPE>::Lane &o,
+                                          int gl) {
+    if constexpr (TYPE == TY_Q4_K) Mv<TYPE>::load(p, r, gl & 7);
+    else if constexpr (TYPE == TY_Q6_K) Mv<TYPE>::load(p, r, o);
+    else Mv<TYPE>::load(p, r);
 }
 
-// ---------------------------------------------------------------- the row loop shared by the kernels
-
-template <int TYPE, int NT, bool STAGE>
-__device__ __forceinline__ void row_sum(const uint8_t *wr, int K, int gl, int L, const Act<NT> &x, float acc[NT],
-                                        bool valid, const StageCtx &stage) {
+// the row's partial sum of this lane: tasks gl, gl + L, ... of the row at wr, MV_U at a time, every load of
+// a batch issued before its arithmetic
+template <int TYPE, int NT, int L>
+__device__ __forceinline__ void row_sum(const uint8_t *wr, int K, int gl, const Act<NT> &x0, float acc[NT]) {
     using P = Mv<TYPE>;
+    constexpr int SL = L / P::LDIV;  // units of the lane's task stride
+    constexpr int WS = P::W_UNIT * SL, XS = P::X_UNIT * SL, DS = P::D_UNIT * SL, BS = P::B_UNIT * SL;
     const int ntask = P::tasks(K);
-    const int s = gl & 7;
+    const int nu = (ntask - gl + L - 1) / L;  // tasks of this lane
+    const typename P::Lane o(gl);
+    const uint8_t *wp = wr + P::wbase(gl);
+    int xo = P::xoff(gl), dof = P::doff(gl), bo = P::boff(gl);
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
-    typename P::Raw raw[MV_U];
-    int task = gl;
-    // first batch in flight before the activation is staged (STAGE) or read through the caches
-#pragma unroll
-    for (int u = 0; u < MV_U; ++u)
-        if (valid && task + u * L < ntask) P::load(wr, task + u * L, raw[u]);
-    if (STAGE) stage_act(stage);
-    if (!valid) return;
-    for (;;) {
+    for (int u0 = 0; u0 < nu; u0 += MV_U) {
+        typename P::Raw raw[MV_U];
 #pragma unroll
         for (int u = 0; u < MV_U; ++u)
-            if (task + u * L < ntask) P::template compute<NT>(raw[u], task + u * L, s, x, acc);
-        task += MV_U * L;
-        if (task >= ntask) break;
+            if (u0 + u < nu) load_task<TYPE>(wp + u * WS, raw[u], o, gl);
 #pragma unroll
         for (int u = 0; u < MV_U; ++u)
-            if (task + u * L < ntask) P::load(wr, task + u * L, raw[u]);
+            if (u0 + u < nu) P::template compute<NT>(raw[u], o, x0, xo + u * XS, dof + u * DS, bo + u * BS, acc, true);
+        wp += MV_U * WS;
+        xo += MV_U * XS;
+        dof += MV_U * DS;
+        bo += MV_U * BS;
     }
 }
 
@@ -388,37 +439,8 @@ __host__ __device__ constexpr int act_blk() {
     return Mv<TYPE>::ACT_BLK;
 }
 
-// LDS bytes for NT tokens of K values
-template <int TYPE>
-__host__ __device__ inline int lds_bytes(int K, int NT) {
-    return NT * K + NT * (K / act_blk<TYPE>()) * 4 + (Mv<TYPE>::KQ ? NT * (K / 16) * 4 : 0);
-}
-
 template <int TYPE, int NT>
-__device__ __forceinline__ void setup_lds(uint8_t *smem, const int8_t *q, const float *d, const int32_t *bs, int K,
-                                          StageCtx &c, Act<NT> &x) {
-    const int nblk = K / act_blk<TYPE>();
-    c.q = q;
-    c.d = d;
-    c.bs = bs;
-    c.sq = (int8_t *)smem;
-    c.sd = (float *)(smem + NT * K);
-    c.sbs = (int32_t *)(c.sd + NT * nblk);
-    c.nq = NT * K;
-    c.nd = NT * nblk;
-    c.nbs = Mv<TYPE>::KQ ? NT * (K / 16) : 0;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        x.q[t] = c.sq + t * K;
-        x.d[t] = c.sd + t * nblk;
-        x.bs[t] = c.sbs + t * (K / 16);
-    }
-}
-
-// ---------------------------------------------------------------- dense decode kernel
-
-template <int TYPE, int NT>
-__device__ __forceinline__ void global_act(const int8_t *q, const float *d, const int32_t *bs, int K, Act<NT> &x) {
+__device__ __forceinline__ void act_view(const int8_t *q, const float *d, const int32_t *bs, int K, Act<NT> &x) {
     const int nblk = K / act_blk<TYPE>();
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -428,25 +450,21 @@ __device__ __forceinline__ void global_act(const int8_t *q, const float *d, cons
     }
 }
 
-// STAGE: the activation staged in LDS once per workgroup behind a barrier; otherwise read through the
-// L1 / L2 caches (the weights stream past them with non-temporal loads), every wave independent.
-template <int TYPE, int NT, bool STAGE>
+// ---------------------------------------------------------------- long rows (more than MV_U tasks a lane)
+// one row group per wave, the activation read through the caches
+
+template <int TYPE, int NT, int L>
 __global__ void __launch_bounds__(MV_THREADS) k_matvec(MvArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    StageCtx c;
-    Act<NT> x;
-    if (STAGE) setup_lds<TYPE, NT>(smem, a.q, a.d, a.bs, a.K, c, x);
-    else global_act<TYPE, NT>(a.q, a.d, a.bs, a.K, x);
-    const int L = a.L;
     const int lane = threadIdx.x & 63, gl = lane & (L - 1);
     const int row = (blockIdx.x * (MV_THREADS / 64) + (threadIdx.x >> 6)) * (64 / L) + lane / L;
-    const bool valid = row < a.Nt;
-    const int mat = valid ? (row >= a.bound[0]) + (row >= a.bound[1]) + (row >= a.bound[2]) : 0;
+    if (row >= a.Nt) return;  // (a whole lane group: rows of 64 / L lanes)
+    const int mat = (row >= a.bound[0]) + (row >= a.bound[1]) + (row >= a.bound[2]);
     const int base = mat == 0 ? 0 : a.bound[mat - 1];
     const uint8_t *wr = a.W[mat] + (long long)(row - base) * a.row_bytes;
+    Act<NT> x;
+    act_view<TYPE, NT>(a.q, a.d, a.bs, a.K, x);
     float acc[NT];
-    row_sum<TYPE, NT, STAGE>(wr, a.K, gl, L, x, acc, valid, c);
-    if (!valid) return;
+    row_sum<TYPE, NT, L>(wr, a.K, gl, x, acc);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const float v = group_sum(acc[t], L);
@@ -455,36 +473,31 @@ __global__ void __launch_bounds__(MV_THREADS) k_matvec(MvArgs a) {
 }
 
 // ---------------------------------------------------------------- MoE expert-indexed kernel
+// grid (row groups, n_used * nmat, T): slot j of token t uses expert ids[t * n_used + j] (-1: Wx)
 
-template <int TYPE, bool STAGE>
+template <int TYPE, int L>
 __global__ void __launch_bounds__(MV_THREADS) k_matvec_id(MvIdArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = threadIdx.x & 63, gl = lane & (L - 1);
+    const int row = (blockIdx.x * (MV_THREADS / 64) + (threadIdx.x >> 6)) * (64 / L) + lane / L;
+    if (row >= a.N) return;
     const int m = (int)blockIdx.y >= a.n_used ? 1 : 0;
     const int slot = (int)blockIdx.y - m * a.n_used, t = blockIdx.z;
     const int e = a.ids[t * a.n_used + slot];
     const long long in_row = a.x_per_slot ? (long long)t * a.n_used + slot : t;
     const int K = a.K;
     const int kb = K / act_blk<TYPE>();
-    StageCtx c;
-    Act<1> x;
-    const int32_t *bsr = a.bs ? a.bs + in_row * (K / 16) : nullptr;
-    if (STAGE) setup_lds<TYPE, 1>(smem, a.q + in_row * K, a.d + in_row * kb, bsr, K, c, x);
-    else global_act<TYPE, 1>(a.q + in_row * K, a.d + in_row * kb, bsr, K, x);
-    const int L = a.L;
-    const int lane = threadIdx.x & 63, gl = lane & (L - 1);
-    const int row = (blockIdx.x * (MV_THREADS / 64) + (threadIdx.x >> 6)) * (64 / L) + lane / L;
-    const bool valid = row < a.N;
     const uint8_t *wr = e >= 0 ? a.W[m] + ((long long)e * a.N + row) * a.row_bytes : a.Wx[m] + (long long)row * a.row_bytes;
+    Act<1> x;
+    act_view<TYPE, 1>(a.q + in_row * K, a.d + in_row * kb, a.bs ? a.bs + in_row * (K / 16) : nullptr, K, x);
     float acc[1];
-    row_sum<TYPE, 1, STAGE>(wr, K, gl, L, x, acc, valid, c);
-    if (!valid) return;
+    row_sum<TYPE, 1, L>(wr, K, gl, x, acc);
     const float v = group_sum(acc[0], L);
     const float sc = e < 0 ? a.sx[m] : a.es[m] ? a.es[m][e] : a.s[m];
     if (gl == 0) a.y[m][((long long)t * a.n_used + slot) * a.N + row] = v * sc;
 }
 
 // ---------------------------------------------------------------- per-group integer dots (test hook)
-// One thread per (row, group); the same code decoders as the kernels above.
+// One thread per (row, group); the same code decoder (fp4x4) as the kernels above.
 
 __device__ __forceinline__ int cb_value(uint32_t nib) { return (int)(int8_t)(fp4x4(nib) & 0xffu); }
 
@@ -531,40 +544,21 @@ __global__ void k_block_dots(const uint8_t *W, long long rb, const int8_t *q, in
 
 // ---------------------------------------------------------------- host launchers
 
-// PURHIE_MV_STAGE=1: stage the activation in LDS (the A/B alternative of the cached reads)
-static bool stage_activations() {
-    static const bool v = getenv("PURHIE_MV_STAGE") && atoi(getenv("PURHIE_MV_STAGE")) != 0;
-    return v;
-}
-
-static int pow2_at_least(int v) {
-    int p = 1;
-    while (p < v) p <<= 1;
-    return p;
-}
-
-template <int TYPE>
-static int tasks_of(int K) {
-    return Mv<TYPE>::tasks(K);
-}
-
 int matvec_lanes(int type, int K, long long rows) {
-    int nt = 0;
+    int nt = 0, U = 1;
     switch (type) {
-    case TY_Q8_0: nt = tasks_of<TY_Q8_0>(K); break;
-    case TY_FP4: nt = tasks_of<TY_FP4>(K); break;
-    case TY_FAST: nt = tasks_of<TY_FAST>(K); break;
-    case TY_Q4_K: nt = tasks_of<TY_Q4_K>(K); break;
-    case TY_Q6_K: nt = tasks_of<TY_Q6_K>(K); break;
+    case TY_Q8_0: nt = Mv<TY_Q8_0>::tasks(K); U = Mv<TY_Q8_0>::U; break;
+    case TY_FP4: nt = Mv<TY_FP4>::tasks(K); U = Mv<TY_FP4>::U; break;
+    case TY_FAST: nt = Mv<TY_FAST>::tasks(K); U = Mv<TY_FAST>::U; break;
+    case TY_Q4_K: nt = Mv<TY_Q4_K>::tasks(K); U = Mv<TY_Q4_K>::U; break;
+    case TY_Q6_K: nt = Mv<TY_Q6_K>::tasks(K); U = Mv<TY_Q6_K>::U; break;
     default: return 0;
     }
-    // about 6 tasks per lane (all of a lane's loads in flight at once, MV_U = 8), at least 8 lanes (the
-    // K-quants' 8 quarters of a super-block)
-    int L = pow2_at_least((nt + 5) / 6);
-    if (L < 8) L = 8;
-    if (L > 64) L = 64;
-    // few rows in the launch: more lanes per row, to keep enough waves in flight
-    while (L < 64 && rows * L / 64 < 2048 && nt > L) L <<= 1;
+    // the fewest lanes (>= 8: the K-quants' 8 quarters of a super-block) that keep a lane's tasks of a row
+    // within the type's U, so the streaming kernels hold a whole row group in registers
+    int L = 8;
+    while (L < 64 && (nt + L - 1) / L > U) L <<= 1;
+    (void)rows;
     if (const char *e = getenv("PURHIE_MV_LANES")) {
         const int v = atoi(e);
         if (v >= 8 && v <= 64 && (v & (v - 1)) == 0) L = v;
@@ -572,16 +566,29 @@ int matvec_lanes(int type, int K, long long rows) {
     return L;
 }
 
+// PURHIE_MV_TILE=0 sends every shape to the per-wave kernels (a tuning and test knob, read per launch)
+static bool tile_enabled() {
+    const char *e = getenv("PURHIE_MV_TILE");
+    return !(e && e[0] == '0');
+}
+
+template <int TYPE, int NT, int L>
+static hipError_t launch_tl(const MvArgs &a, hipStream_t stream) {
+    const int rows_per_wg = (MV_THREADS / 64) * (64 / L);
+    const unsigned grid = (unsigned)((a.Nt + rows_per_wg - 1) / rows_per_wg);
+    hipLaunchKernelGGL((k_matvec<TYPE, NT, L>), dim3(grid), dim3(MV_THREADS), 0, stream, a);
+    return hipGetLastError();
+}
+
 template <int TYPE, int NT>
 static hipError_t launch_t(const MvArgs &a, hipStream_t stream) {
-    const int rows_per_wg = (MV_THREADS / 64) * (64 / a.L);
-    const unsigned grid = (unsigned)((a.Nt + rows_per_wg - 1) / rows_per_wg);
-    const size_t lds = (size_t)lds_bytes<TYPE>(a.K, NT);
-    if (stage_activations() && lds <= 65536)
-        hipLaunchKernelGGL((k_matvec<TYPE, NT, true>), dim3(grid), dim3(MV_THREADS), lds, stream, a);
-    else
-        hipLaunchKernelGGL((k_matvec<TYPE, NT, false>), dim3(grid), dim3(MV_THREADS), 0, stream, a);
-    return hipGetLastError();
+    switch (a.L) {
+    case 8: return launch_tl<TYPE, NT, 8>(a, stream);
+    case 16: return launch_tl<TYPE, NT, 16>(a, stream);
+    case 32: return launch_tl<TYPE, NT, 32>(a, stream);
+    case 64: return launch_tl<TYPE, NT, 64>(a, stream);
+    }
+    return hipErrorInvalidValue;
 }
 
 template <int TYPE>
@@ -596,6 +603,10 @@ static hipError_t launch_nt(const MvArgs &a, hipStream_t stream) {
 }
 
 hipError_t launch_matvec(int type, const MvArgs &a, hipStream_t stream) {
+    if (tile_enabled()) {
+        const hipError_t e = launch_matvec_tile(type, a, stream);
+        if (e != hipErrorNotSupported) return e;
+    }
     switch (type) {
     case TY_Q8_0: return launch_nt<TY_Q8_0>(a, stream);
     case TY_FP4: return launch_nt<TY_FP4>(a, stream);
@@ -606,19 +617,30 @@ hipError_t launch_matvec(int type, const MvArgs &a, hipStream_t stream) {
     return hipErrorInvalidDeviceFunction;
 }
 
-template <int TYPE>
-static hipError_t launch_id_t(const MvIdArgs &a, hipStream_t stream) {
-    const int rows_per_wg = (MV_THREADS / 64) * (64 / a.L);
+template <int TYPE, int L>
+static hipError_t launch_id_tl(const MvIdArgs &a, hipStream_t stream) {
+    const int rows_per_wg = (MV_THREADS / 64) * (64 / L);
     const dim3 grid((unsigned)((a.N + rows_per_wg - 1) / rows_per_wg), (unsigned)(a.n_used * a.nmat), (unsigned)a.T);
-    const size_t lds = (size_t)lds_bytes<TYPE>(a.K, 1);
-    if (stage_activations() && lds <= 65536)
-        hipLaunchKernelGGL((k_matvec_id<TYPE, true>), grid, dim3(MV_THREADS), lds, stream, a);
-    else
-        hipLaunchKernelGGL((k_matvec_id<TYPE, false>), grid, dim3(MV_THREADS), 0, stream, a);
+    hipLaunchKernelGGL((k_matvec_id<TYPE, L>), grid, dim3(MV_THREADS), 0, stream, a);
     return hipGetLastError();
 }
 
+template <int TYPE>
+static hipError_t launch_id_t(const MvIdArgs &a, hipStream_t stream) {
+    switch (a.L) {
+    case 8: return launch_id_tl<TYPE, 8>(a, stream);
+    case 16: return launch_id_tl<TYPE, 16>(a, stream);
+    case 32: return launch_id_tl<TYPE, 32>(a, stream);
+    case 64: return launch_id_tl<TYPE, 64>(a, stream);
+    }
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_matvec_id(int type, const MvIdArgs &a, hipStream_t stream) {
+    if (tile_enabled()) {
+        const hipError_t e = launch_matvec_id_tile(type, a, stream);
+        if (e != hipErrorNotSupported) return e;
+    }
     switch (type) {
     case TY_Q8_0: return launch_id_t<TY_Q8_0>(a, stream);
     case TY_FP4: return launch_id_t<TY_FP4>(a, stream);

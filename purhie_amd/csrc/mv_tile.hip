@@ -1,0 +1,615 @@
+// mv_tile.hip -- the decode matvec y = W x_q with one whole quantization unit per lane (gfx950, wave64).
+//
+// Replaces the reference's matvec_q8_<type> / matvec_q8t_<type> / matvec_q8_id_<type> (src/matvec_q.hip:
+// 1403-1965) for the shapes it covers (K a whole number of units, at most 256 units a row); the per-wave
+// kernels of matvec.hip take the rest. The unit a lane owns (values of one row):
+//   Q4_K: one 144-byte super-block (256)    Q6_K: one 210-byte super-block (256)
+//   ROCmFP4: eight 18-byte blocks (256)     ROCmFP4_FAST: eight 17-byte blocks (256)
+//   Q8_0: four 34-byte blocks (128)
+// so a scale decode serves a whole block and the integer work per byte is small.
+//
+// A workgroup (4 waves) owns a tile of whole rows of one matrix: its units, row-major, are one contiguous
+// byte range, and wave w owns units 64 w .. 64 w + 63 -- again contiguous. Per workgroup:
+//   1. the activation of the NT tokens (Q8_0 or Q8_K values, scales, group sums) is loaded first: the
+//      vector-memory counter retires in issue order, so waiting for it does not wait for the weights;
+//   2. each wave loads its byte range with consecutive lanes on consecutive 16-byte chunks (non-temporal;
+//      a wave instruction covers 1 KiB of 8 cache lines, where one unit per lane would touch 64);
+//   3. the activation goes to LDS (values padded by 16 bytes per 256, so that the unit columns sit in
+//      different banks); barrier; each wave writes its chunks to its own LDS region and every lane reads
+//      its unit back (LDS is in order within a wave: no barrier);
+//   4. each lane forms its unit's exact per-block integer dots (v_dot4_i32_i8 on codes decoded by masks or
+//      v_perm_b32 tables) and one float partial per token in the reference's per-block form;
+//   5. partials go to LDS; barrier; thread r adds row r's partials over its units in order.
+// The grid holds every tile of the launch (no persistent loop): all weight loads of a launch are in flight
+// from the start and each wave computes as its data arrives. A row's result is a fixed-order sum of
+// per-unit partials: it does not depend on the tile size, the other matrices of the launch, or how many
+// tokens share it.
+#include "device.h"
+#include "kernels.h"
+
+namespace pq {
+
+constexpr int TL_THREADS = 256;
+constexpr int TL_PAD = 272;  // LDS bytes per 256 activation values
+
+// the dword at byte offset off (compile-time after unrolling) of the unit's dwords
+template <int N>
+__device__ __forceinline__ uint32_t dwb(const uint32_t (&w)[N], int off) {
+    const int i = off >> 2, s = off & 3;
+    if (s == 0) return w[i];
+    return align_bytes(i + 1 < N ? w[i + 1] : 0u, w[i], (uint32_t)s);
+}
+
+// byte at offset off of the unit
+template <int N>
+__device__ __forceinline__ uint32_t byteb(const uint32_t (&w)[N], int off) {
+    return (w[off >> 2] >> (8 * (off & 3))) & 0xffu;
+}
+
+// the activation as staged in LDS, at the lane's unit (token t: values x + t * xt, scales d + t * nd,
+// group sums s + t * ns)
+struct Lx {
+    const int8_t *x;
+    const float *d;
+    const int32_t *s;
+    const float *lut;  // UE4M3 byte -> half scale
+    int xt, nd, ns;
+};
+
+__device__ __forceinline__ int dot8(const int *v, const int4 a, const int4 b) {
+    int s = dot4(v[0], a.x, 0);
+    s = dot4(v[1], a.y, s);
+    s = dot4(v[2], a.z, s);
+    s = dot4(v[3], a.w, s);
+    s = dot4(v[4], b.x, s);
+    s = dot4(v[5], b.y, s);
+    s = dot4(v[6], b.z, s);
+    return dot4(v[7], b.w, s);
+}
+
+__device__ __forceinline__ int dot4x(const int *v, const int4 a) {
+    int s = dot4(v[0], a.x, 0);
+    s = dot4(v[1], a.y, s);
+    s = dot4(v[2], a.z, s);
+    return dot4(v[3], a.w, s);
+}
+
+// a unit's dwords from LDS: 16-byte aligned (b128 reads) or 8-byte aligned (b64 reads)
+template <int N>
+__device__ __forceinline__ void read16(const uint8_t *p, uint32_t (&w)[N], uint32_t &aux) {
+    static_assert(N % 4 == 0, "whole 16-byte reads");
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+        const uint4 v = ((const uint4 *)p)[i];
+        w[4 * i] = v.x;
+        w[4 * i + 1] = v.y;
+        w[4 * i + 2] = v.z;
+        w[4 * i + 3] = v.w;
+    }
+    aux = 0;
+}
+template <int N>
+__device__ __forceinline__ void read8(const uint8_t *p, uint32_t (&w)[N], uint32_t &aux) {
+    static_assert(N % 2 == 0, "whole 8-byte reads");
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+        const uint2 v = ((const uint2 *)p)[i];
+        w[2 * i] = v.x;
+        w[2 * i + 1] = v.y;
+    }
+    aux = 0;
+}
+
+template <int TYPE>
+struct Tu;
+
+// Q4_K super-block: d, dmin (dword 0), 12 scale bytes (dwords 1..3), qs (dwords 4..35). Chunk c of qs
+// (32 bytes) holds values 64 c + 0..31 in its low nibbles (sub-block 2 c) and 64 c + 32..63 in its high
+// nibbles (sub-block 2 c + 1). The 6-bit scales and mins of the 8 sub-blocks are unpacked four at a time
+// (reference src/quant_types.cpp:193-201): scale j < 4 = y byte j & 63, j >= 4 = (w byte & 15) | (y byte
+// >> 6) << 4; min j < 4 = z byte j & 63, j >= 4 = (w byte >> 4) | (z byte >> 6) << 4 (y, z, w = dwords
+// 1..3). Per super-block: d dx isum - dmin dx msum, isum = sum_j sc_j dot_j, msum = sum_j m_j sum32_j
+// (reference src/matvec_q.hip:1752-1789).
+template <>
+struct Tu<TY_Q4_K> {
+    static constexpr int VALS = 256, BYTES = 144, NDW = 36, ACT = 256, SUMS = 32, LEAD = 0;
+    static constexpr bool LUT = false;
+    __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read16(p, w, aux); }
+    template <int NT>
+    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT]) {
+        const uint32_t y = w[1], z = w[2], v = w[3];
+        const uint32_t sc[2] = {y & 0x3f3f3f3fu, (v & 0x0f0f0f0fu) | ((y >> 2) & 0x30303030u)};
+        const uint32_t mn[2] = {z & 0x3f3f3f3fu, ((v >> 4) & 0x0f0f0f0fu) | ((z >> 2) & 0x30303030u)};
+        int isum[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) isum[t] = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            int lo[8], hi[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t q = w[4 + 8 * c + k];
+                lo[k] = (int)(q & 0x0f0f0f0fu);
+                hi[k] = (int)((q >> 4) & 0x0f0f0f0fu);
+            }
+            const int sa = (int)((sc[c >> 1] >> (16 * (c & 1))) & 0xffu);
+            const int sb = (int)((sc[c >> 1] >> (16 * (c & 1) + 8)) & 0xffu);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const int4 *xv = (const int4 *)(x.x + t * x.xt + 64 * c);
+                const int slo = dot8(lo, xv[0], xv[1]);
+                const int shi = dot8(hi, xv[2], xv[3]);
+                isum[t] += __mul24(sa, slo) + __mul24(sb, shi);
+            }
+        }
+        const float dw = h2f(w[0] & 0xffffu), dm = h2f(w[0] >> 16);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int4 s0 = *(const int4 *)(x.s + t * x.ns), s1 = *(const int4 *)(x.s + t * x.ns + 4);
+            int msum = __mul24((int)(mn[0] & 0xffu), s0.x);
+            msum += __mul24((int)((mn[0] >> 8) & 0xffu), s0.y);
+            msum += __mul24((int)((mn[0] >> 16) & 0xffu), s0.z);
+            msum += __mul24((int)(mn[0] >> 24), s0.w);
+            msum += __mul24((int)(mn[1] & 0xffu), s1.x);
+            msum += __mul24((int)((mn[1] >> 8) & 0xffu), s1.y);
+            msum += __mul24((int)((mn[1] >> 16) & 0xffu), s1.z);
+            msum += __mul24((int)(mn[1] >> 24), s1.w);
+            const float dx = x.d[t * x.nd];
+            acc[t] = __builtin_fmaf(dw * dx, (float)isum[t], -(dm * dx) * (float)msum);
+        }
+    }
+};
+
+// Q6_K super-block (210 bytes, 2-aligned): ql (bytes 0..127), qh (128..191), 16 int8 scales (192..207),
+// d (208..209). Read as 53 dwords from the 4-aligned address at or below it and realigned. For half h,
+// l in 0..31: values 128 h + l + {0, 32, 64, 96} are ql[64 h + l] & 15, ql[64 h + 32 + l] & 15,
+// ql[64 h + l] >> 4, ql[64 h + 32 + l] >> 4, each with 2 bits of qh[32 h + l] (bits 0-1, 2-3, 4-5, 6-7) as
+// bits 4-5; the 16-value group g has scale sc[g]. The -32 offset goes through the Q8_K 16-value sums:
+// isum = sum_g sc_g (dot_g - 32 sum16_g) (reference src/matvec_q.hip:1716-1750).
+template <>
+struct Tu<TY_Q6_K> {
+    static constexpr int VALS = 256, BYTES = 210, NDW = 53, ACT = 256, SUMS = 16, LEAD = 15;
+    static constexpr bool LUT = false;
+    __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) {
+        const uint32_t *a = (const uint32_t *)((uintptr_t)p & ~(uintptr_t)3);
+#pragma unroll
+        for (int i = 0; i < NDW; ++i) w[i] = a[i];
+        aux = (uint32_t)((uintptr_t)p & 3u);
+    }
+    template <int NT>
+    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t off, const Lx &x, float (&acc)[NT]) {
+        uint32_t v[NDW];
+#pragma unroll
+        for (int i = 0; i < NDW; ++i) v[i] = align_bytes(i + 1 < NDW ? w[i + 1] : 0u, w[i], off);
+        int isum[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) isum[t] = 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int lc = 0; lc < 2; ++lc) {
+                int q[4][4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t A = v[16 * h + 4 * lc + i], B = v[16 * h + 8 + 4 * lc + i];
+                    const uint32_t H = v[32 + 8 * h + 4 * lc + i];
+                    q[0][i] = (int)((A & 0x0f0f0f0fu) | ((H << 4) & 0x30303030u));
+                    q[1][i] = (int)((B & 0x0f0f0f0fu) | ((H << 2) & 0x30303030u));
+                    q[2][i] = (int)(((A >> 4) & 0x0f0f0f0fu) | (H & 0x30303030u));
+                    q[3][i] = (int)(((B >> 4) & 0x0f0f0f0fu) | ((H >> 2) & 0x30303030u));
+                }
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const int g = 8 * h + 2 * m + lc;
+                    const int sc = (int)(int8_t)((v[48 + (g >> 2)] >> (8 * (g & 3))) & 0xffu);
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        const int4 xa = *(const int4 *)(x.x + t * x.xt + 128 * h + 32 * m + 16 * lc);
+                        const int dg = dot4x(q[m], xa);
+                        isum[t] += __mul24(sc, dg - 32 * x.s[t * x.ns + g]);
+                    }
+                }
+            }
+        }
+        const float dw = h2f(v[52] & 0xffffu);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = (dw * x.d[t * x.nd]) * (float)isum[t];
+    }
+};
+
+// Q8_0: four 34-byte blocks (fp16 scale, 32 int8 values); per block (e dx) sum
+// (reference src/matvec_q.hip:1566-1573 q8_0_q8_block, 1576 mv_q8_0).
+template <>
+struct Tu<TY_Q8_0> {
+    static constexpr int VALS = 128, BYTES = 136, NDW = 34, ACT = 32, SUMS = 0, LEAD = 8;
+    static constexpr bool LUT = false;
+    __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read8(p, w, aux); }
+    template <int NT>
+    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT]) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int off = 34 * b;
+            int qs[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) qs[k] = (int)dwb(w, off + 2 + 4 * k);
+            const float e = h2f((off & 3) ? (w[off >> 2] >> 16) : (w[off >> 2] & 0xffffu));
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const int4 *xv = (const int4 *)(x.x + t * x.xt + 32 * b);
+                const int s = dot8(qs, xv[0], xv[1]);
+                acc[t] = __builtin_fmaf(e * x.d[t * x.nd + b], (float)s, acc[t]);
+            }
+        }
+    }
+};
+
+// ROCmFP4 (type 100): eight 18-byte blocks (16 value bytes: value j in the low nibble of byte j, j + 16 in
+// the high nibble; UE4M3 half-block scales at bytes 16, 17). Per block (e0 dx) s0 + (e1 dx) s1
+// (reference src/matvec_q.hip:1310-1327 P4ROCmFP4::block, 1428 mv_p4).
+template <>
+struct Tu<TY_FP4> {
+    static constexpr int VALS = 256, BYTES = 144, NDW = 36, ACT = 32, SUMS = 0, LEAD = 0;
+    static constexpr bool LUT = true;
+    __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read16(p, w, aux); }
+    template <int NT>
+    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT]) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const int off = 18 * b;
+            int lo[4], hi[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t q = dwb(w, off + 4 * k);
+                lo[k] = fp4x4_lo(q);
+                hi[k] = fp4x4_hi(q);
+            }
+            const float e0 = x.lut[byteb(w, off + 16)], e1 = x.lut[byteb(w, off + 17)];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const int4 *xv = (const int4 *)(x.x + t * x.xt + 32 * b);
+                const int s0 = dot4x(lo, xv[0]), s1 = dot4x(hi, xv[1]);
+                const float dx = x.d[t * x.nd + b];
+                acc[t] += __builtin_fmaf(e1 * dx, (float)s1, e0 * dx * (float)s0);
+            }
+        }
+    }
+};
+
+// ROCmFP4_FAST (type 101): eight 17-byte blocks (16 value bytes, one UE4M3 scale at byte 16); per block
+// (e dx) (s0 + s1) (reference src/matvec_q.hip:1492-1502, 1505 mv_fast).
+template <>
+struct Tu<TY_FAST> {
+    static constexpr int VALS = 256, BYTES = 136, NDW = 34, ACT = 32, SUMS = 0, LEAD = 8;
+    static constexpr bool LUT = true;
+    __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read8(p, w, aux); }
+    template <int NT>
+    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT]) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int off = 17 * j;
+            int lo[4], hi[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t q = dwb(w, off + 4 * k);
+                lo[k] = fp4x4_lo(q);
+                hi[k] = fp4x4_hi(q);
+            }
+            const float e = x.lut[byteb(w, off + 16)];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const int4 *xv = (const int4 *)(x.x + t * x.xt + 32 * j);
+                const int s = dot4x(lo, xv[0]) + dot4x(hi, xv[1]);
+                acc[t] = __builtin_fmaf(e * x.d[t * x.nd + j], (float)s, acc[t]);
+            }
+        }
+    }
+};
+
+// ---------------------------------------------------------------- LDS layout of a tile
+
+template <int TYPE>
+struct TileLds {
+    static constexpr int REGION = (64 * Tu<TYPE>::BYTES + Tu<TYPE>::LEAD + 15) & ~15;  // a wave's weight bytes
+    static constexpr int CH = (REGION / 16 + 63) / 64;                                  // its 16-byte chunks a lane
+    int xt, nd, ns;                                                                     // per token
+    int off_d, off_s, off_lut, off_p, off_w, bytes;
+    __host__ __device__ TileLds(int K, int NT) {
+        using P = Tu<TYPE>;
+        xt = (K + 255) / 256 * TL_PAD;
+        nd = K / P::ACT;
+        ns = P::SUMS ? K / P::SUMS : 0;
+        off_d = NT * xt;
+        off_s = off_d + ((NT * nd * 4 + 15) & ~15);
+        off_lut = off_s + ((NT * ns * 4 + 15) & ~15);
+        off_p = off_lut + (P::LUT ? 1024 : 0);
+        off_w = off_p + NT * TL_THREADS * 4;
+        bytes = off_w + (TL_THREADS / 64) * REGION;
+    }
+};
+
+// ---------------------------------------------------------------- the tile kernel body
+
+constexpr int TL_QN = 4, TL_DN = 2, TL_SN = 4;  // activation loads a thread holds across the weight issue
+
+// Stage the activation of NT tokens (global: values q + t K, scales d + t nd, Q8_K 16-value sums
+// bs + t K / 16) into LDS. Each thread's first TL_QN value chunks, TL_DN scales and TL_SN group sums are
+// loaded by issue() (before the weights), anything beyond by commit(). Q4_K's 32-value sums are the two
+// 16-value sums added when written (nothing in issue() waits for a load).
+template <int TYPE, int NT>
+struct Stager {
+    static constexpr bool PAIR = Tu<TYPE>::SUMS == 32;
+    int4 qv[TL_QN];
+    float dv[TL_DN];
+    int2 sv[TL_SN];
+    int nq, ndt, nst;
+
+    __device__ __forceinline__ void issue(const TileLds<TYPE> &L, const int8_t *q, const float *d, const int32_t *bs, int K) {
+        nq = NT * K / 16;
+        ndt = NT * L.nd;
+        nst = NT * L.ns;
+        const int tid = threadIdx.x;
+        // (unconditional loads, clamped to the last element: with a load skipped on some path the compiler
+        // can no longer count the loads in flight and waits for all of them, the weights included)
+#pragma unroll
+        for (int i = 0; i < TL_QN; ++i) {
+            const int c = tid + i * TL_THREADS;
+            qv[i] = *(const int4 *)(q + 16 * (long long)(c < nq ? c : nq - 1));
+        }
+#pragma unroll
+        for (int i = 0; i < TL_DN; ++i) {
+            const int e = tid + i * TL_THREADS;
+            dv[i] = d[e < ndt ? e : ndt - 1];
+        }
+        if (Tu<TYPE>::SUMS) {
+#pragma unroll
+            for (int i = 0; i < TL_SN; ++i) {
+                const int e = tid + i * TL_THREADS;
+                sv[i] = load_s(bs, e < nst ? e : nst - 1);
+            }
+        }
+    }
+    __device__ static __forceinline__ int2 load_s(const int32_t *bs, int e) {
+        if (PAIR) return *(const int2 *)(bs + 2 * (long long)e);
+        return make_int2(bs[e], 0);
+    }
+    __device__ static __forceinline__ void put_q(const TileLds<TYPE> &L, uint8_t *smem, int K, int c, int4 v) {
+        const int per = K / 16, t = c / per, cc = c - t * per;
+        *(int4 *)(smem + t * L.xt + (cc >> 4) * TL_PAD + (cc & 15) * 16) = v;
+    }
+    __device__ static __forceinline__ void put_s(const TileLds<TYPE> &L, uint8_t *smem, int e, int2 v) {
+        ((int32_t *)(smem + L.off_s))[e] = PAIR ? v.x + v.y : v.x;
+    }
+    __device__ __forceinline__ void commit(const TileLds<TYPE> &L, uint8_t *smem, const int8_t *q, const float *d,
+                                           const int32_t *bs, int K) {
+        const int tid = threadIdx.x;
+        float *ld = (float *)(smem + L.off_d);
+#pragma unroll
+        for (int i = 0; i < TL_QN; ++i) {
+            const int c = tid + i * TL_THREADS;
+            if (c < nq) put_q(L, smem, K, c, qv[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < TL_DN; ++i) {
+            const int e = tid + i * TL_THREADS;
+            if (e < ndt) ld[e] = dv[i];
+        }
+        if (Tu<TYPE>::SUMS) {
+#pragma unroll
+            for (int i = 0; i < TL_SN; ++i) {
+                const int e = tid + i * TL_THREADS;
+                if (e < nst) put_s(L, smem, e, sv[i]);
+            }
+        }
+        for (int c = tid + TL_QN * TL_THREADS; c < nq; c += TL_THREADS) put_q(L, smem, K, c, *(const int4 *)(q + 16 * (long long)c));
+        for (int e = tid + TL_DN * TL_THREADS; e < ndt; e += TL_THREADS) ld[e] = d[e];
+        if (Tu<TYPE>::SUMS)
+            for (int e = tid + TL_SN * TL_THREADS; e < nst; e += TL_THREADS) put_s(L, smem, e, load_s(bs, e));
+        if (Tu<TYPE>::LUT) ((float *)(smem + L.off_lut))[tid] = ue4m3_half((uint32_t)tid);
+    }
+};
+
+// One tile: rows [row0, row0 + nr) of one matrix (contiguous, nb units each, nr * nb <= 256).
+template <int TYPE, int NT, class Rows>
+__device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int row0, int nr, int K, int nb,
+                                          const int8_t *q, const float *d, const int32_t *bs) {
+    using P = Tu<TYPE>;
+    using TL = TileLds<TYPE>;
+    const TL L(K, NT);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    Stager<TYPE, NT> st;
+    st.issue(L, q, d, bs, K);
+
+    // this wave's units [64 wave, 64 wave + wu) of the tile: bytes [g, g + wu BYTES), loaded as the 16-byte
+    // chunks from the aligned address a at or below g (each chunk holds at least one byte of the range)
+    // (a wave past the tile's units loads the tile's first chunk; loads past a wave's last chunk repeat it)
+    const int nu = nr * nb, u0 = 64 * wave;
+    const int wu = nu - u0 < 0 ? 0 : nu - u0 > 64 ? 64 : nu - u0;
+    const uint8_t *g = rows.w(row0) + (long long)(wu ? u0 : 0) * P::BYTES;
+    const int lead = (int)((uintptr_t)g & 15u);
+    const uint8_t *ga = g - lead;  // (pointer arithmetic keeps the global address space: no flat loads)
+    const int nch = wu ? (lead + wu * P::BYTES + 15) >> 4 : 1;
+    u32x4 c[TL::CH];
+#pragma unroll
+    for (int i = 0; i < TL::CH; ++i) {
+        const int ci = lane + 64 * i;
+        c[i] = ld128_nt(ga + 16 * (ci < nch ? ci : nch - 1));
+    }
+
+    st.commit(L, smem, q, d, bs, K);
+    __syncthreads();
+    uint8_t *region = smem + L.off_w + wave * TL::REGION;
+#pragma unroll
+    for (int i = 0; i < TL::CH; ++i) {
+        const int ci = lane + 64 * i;
+        if (ci < nch) *(u32x4 *)(region + 16 * ci) = c[i];
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+
+    // this lane's unit (an idle lane reads unit 0 of its wave region and its partial is never used)
+    const int u = tid < nu ? tid : u0;
+    const int k = u % nb;
+    uint32_t w[P::NDW], aux;
+    P::read(region + lead + (u - u0) * P::BYTES, w, aux);
+    const int v0 = k * P::VALS;
+    Lx x;
+    x.x = (const int8_t *)smem + (v0 >> 8) * TL_PAD + (v0 & 255);
+    x.d = (const float *)(smem + L.off_d) + v0 / P::ACT;
+    x.s = (const int32_t *)(smem + L.off_s) + (P::SUMS ? v0 / P::SUMS : 0);
+    x.lut = (const float *)(smem + L.off_lut);
+    x.xt = L.xt;
+    x.nd = L.nd;
+    x.ns = L.ns;
+    float acc[NT];
+    P::template compute<NT>(w, aux, x, acc);
+
+    float *part = (float *)(smem + L.off_p);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) part[t * TL_THREADS + tid] = acc[t];
+    __syncthreads();
+    if (tid < nr) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float *pr = part + t * TL_THREADS + tid * nb;
+            float s = 0.0f;
+            for (int kk = 0; kk < nb; ++kk) s += pr[kk];
+            rows.store(row0 + tid, t, s);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- kernels
+
+// tiles of R rows, per matrix: matrix m owns tiles [tp[m - 1], tp[m]) of the grid
+struct TileArgs {
+    int R, nb, tp[4];
+};
+
+template <int TYPE, int NT>
+__global__ void __launch_bounds__(TL_THREADS) k_mv_tile(MvArgs a, TileArgs ta) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const DenseRows rows{a};
+    const int bx = (int)blockIdx.x;
+    const int m = (bx >= ta.tp[0]) + (bx >= ta.tp[1]) + (bx >= ta.tp[2]);
+    const int first = DenseRows::pick(m, 0, ta.tp[0], ta.tp[1], ta.tp[2]);
+    const int row0 = rows.base(m) + (bx - first) * ta.R;
+    const int end = DenseRows::pick(m, a.bound[0], a.bound[1], a.bound[2], a.bound[3]);
+    const int nr = end - row0 < ta.R ? end - row0 : ta.R;
+    tile_body<TYPE, NT>(smem, rows, row0, nr, a.K, ta.nb, a.q, a.d, a.bs);
+}
+
+// MoE: grid (tiles, n_used * nmat, T); slot j of token t uses expert ids[t * n_used + j] (-1: Wx)
+template <int TYPE>
+__global__ void __launch_bounds__(TL_THREADS) k_mv_tile_id(MvIdArgs a, TileArgs ta) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int m = (int)blockIdx.y >= a.n_used ? 1 : 0;
+    const int slot = (int)blockIdx.y - m * a.n_used, t = blockIdx.z;
+    const int e = a.ids[t * a.n_used + slot];
+    const long long in_row = a.x_per_slot ? (long long)t * a.n_used + slot : t;
+    const int K = a.K;
+    const IdRows rows{e >= 0 ? a.W[m] + (long long)e * a.N * a.row_bytes : a.Wx[m], a.row_bytes,
+                      a.y[m] + ((long long)t * a.n_used + slot) * a.N,
+                      e < 0 ? a.sx[m] : a.es[m] ? a.es[m][e] : a.s[m]};
+    const int row0 = (int)blockIdx.x * ta.R;
+    const int nr = a.N - row0 < ta.R ? a.N - row0 : ta.R;
+    tile_body<TYPE, 1>(smem, rows, row0, nr, K, ta.nb, a.q + in_row * K, a.d + in_row * (K / Tu<TYPE>::ACT),
+                       a.bs ? a.bs + in_row * (K / 16) : nullptr);
+}
+
+// ---------------------------------------------------------------- host side
+
+static bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+// The tile kernels take a shape when K is a whole number of units (at most 256 a row), the tile's LDS fits
+// in 64 KiB, and the operands are aligned for the wide reads: weight matrices 16 bytes with rows a multiple
+// of 16 (Q4_K, ROCmFP4) or 8 (Q8_0, ROCmFP4_FAST) bytes (Q6_K: any even row), activation values 16 bytes,
+// scales 4, Q4_K's paired group sums 8.
+template <int TYPE>
+static bool tile_takes(int K, int NT, const uint8_t *const *W, int nW, long long row_bytes, const void *q,
+                       const void *d, const void *bs) {
+    using P = Tu<TYPE>;
+    if (K <= 0 || K % P::VALS || K / P::VALS > TL_THREADS) return false;
+    if (TileLds<TYPE>(K, NT).bytes > 65536) return false;
+    for (int i = 0; i < nW; ++i)
+        if (!aligned(W[i], 16)) return false;
+    if (row_bytes % (P::LEAD == 0 ? 16 : P::LEAD == 8 ? 8 : 2)) return false;
+    if (!aligned(q, 16) || !aligned(d, 4)) return false;
+    if (P::SUMS && (!bs || !aligned(bs, P::SUMS == 32 ? 8 : 4))) return false;
+    return true;
+}
+
+template <int TYPE, int NT>
+static hipError_t tile_dense(const MvArgs &a, hipStream_t stream) {
+    int nW = 1;
+    while (nW < 4 && a.bound[nW - 1] < a.Nt) ++nW;
+    if (!tile_takes<TYPE>(a.K, NT, a.W, nW, a.row_bytes, a.q, a.d, a.bs)) return hipErrorNotSupported;
+    TileArgs ta;
+    ta.nb = a.K / Tu<TYPE>::VALS;
+    ta.R = TL_THREADS / ta.nb;
+    int tiles = 0, lo = 0;
+    for (int i = 0; i < 4; ++i) {
+        const int n = a.bound[i] - lo;
+        tiles += n > 0 ? (n + ta.R - 1) / ta.R : 0;
+        ta.tp[i] = tiles;
+        lo = a.bound[i] > lo ? a.bound[i] : lo;
+    }
+    const size_t lds = (size_t)TileLds<TYPE>(a.K, NT).bytes;
+    hipLaunchKernelGGL((k_mv_tile<TYPE, NT>), dim3((unsigned)tiles), dim3(TL_THREADS), lds, stream, a, ta);
+    return hipGetLastError();
+}
+
+template <int TYPE>
+static hipError_t tile_dense_t(const MvArgs &a, hipStream_t stream) {
+    switch (a.T) {
+    case 1: return tile_dense<TYPE, 1>(a, stream);
+    case 2: return tile_dense<TYPE, 2>(a, stream);
+    case 3: return tile_dense<TYPE, 3>(a, stream);
+    case 4: return tile_dense<TYPE, 4>(a, stream);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_matvec_tile(int type, const MvArgs &a, hipStream_t stream) {
+    switch (type) {
+    case TY_Q8_0: return tile_dense_t<TY_Q8_0>(a, stream);
+    case TY_FP4: return tile_dense_t<TY_FP4>(a, stream);
+    case TY_FAST: return tile_dense_t<TY_FAST>(a, stream);
+    case TY_Q4_K: return tile_dense_t<TY_Q4_K>(a, stream);
+    case TY_Q6_K: return tile_dense_t<TY_Q6_K>(a, stream);
+    }
+    return hipErrorNotSupported;
+}
+
+template <int TYPE>
+static hipError_t tile_id(const MvIdArgs &a, hipStream_t stream) {
+    // (null Wx entries pass the alignment check; a row of activation is K values, K / ACT scales and K / 16
+    // sums on from the previous one, which keeps every row as aligned as the first when K % VALS == 0)
+    const uint8_t *W[4] = {a.W[0], a.Wx[0], a.nmat > 1 ? a.W[1] : nullptr, a.nmat > 1 ? a.Wx[1] : nullptr};
+    if (!tile_takes<TYPE>(a.K, 1, W, 4, a.row_bytes, a.q, a.d, a.bs)) return hipErrorNotSupported;
+    TileArgs ta = {};
+    ta.nb = a.K / Tu<TYPE>::VALS;
+    ta.R = TL_THREADS / ta.nb;
+    const dim3 grid((unsigned)((a.N + ta.R - 1) / ta.R), (unsigned)(a.n_used * a.nmat), (unsigned)a.T);
+    const size_t lds = (size_t)TileLds<TYPE>(a.K, 1).bytes;
+    hipLaunchKernelGGL((k_mv_tile_id<TYPE>), grid, dim3(TL_THREADS), lds, stream, a, ta);
+    return hipGetLastError();
+}
+
+hipError_t launch_matvec_id_tile(int type, const MvIdArgs &a, hipStream_t stream) {
+    switch (type) {
+    case TY_Q8_0: return tile_id<TY_Q8_0>(a, stream);
+    case TY_FP4: return tile_id<TY_FP4>(a, stream);
+    case TY_FAST: return tile_id<TY_FAST>(a, stream);
+    case TY_Q4_K: return tile_id<TY_Q4_K>(a, stream);
+    case TY_Q6_K: return tile_id<TY_Q6_K>(a, stream);
+    }
+    return hipErrorNotSupported;
+}
+
+}  // namespace pq
