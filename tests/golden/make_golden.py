@@ -1,0 +1,73 @@
+"""Write the golden vectors of tests/golden/ from the reference's own CPU code.
+
+Runs in the build container, where oracle/ref.mk has compiled the reference's quant_types.cpp, quantize.cpp
+(+ quantize_iq.cpp) and expert_cpu.cpp into oracle/_ref/libref.so. Each fixture holds seeded inputs and the
+reference's outputs for them (no reference source or code travels):
+  enc_<type>.npz    rows x (fp32) -> reference encoder bytes (qz_quantize) and decoder floats (qt_to_float)
+  act_q8_0.npz      x -> reference cpu_q8_0_quantize values and scales
+  matvec_<type>.npz Q8_0 / ROCmFP4_FAST matrix (reference-encoded), Q8_0 activation, reference CPU matvec y
+  expert_ffn.npz    a FAST expert FFN (gate, up, down) and activation, reference cpu_expert_ffn output
+
+Usage: python tests/golden/make_golden.py   (rewrites the .npz files beside this script)
+"""
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+from oracle import oracle as O  # noqa: E402
+from purhie_amd import synth  # noqa: E402
+
+TYPES = (8, 12, 14, 100, 101)
+
+
+def enc_rows(seed, K):
+    """6 rows: N(0, 0.02), N(0, 1) with outliers x20, all zero, one constant, tiny values, a sparse row"""
+    g = synth.gaussian(seed, K, 0, 0.02)
+    o = synth.with_outliers(synth.gaussian(seed + 1, K), seed + 2, 0.01, 20.0)
+    z = np.zeros(K, np.float32)
+    c = np.full(K, 0.37, np.float32)
+    t = synth.gaussian(seed + 3, K, 0, 1e-6)
+    s = np.zeros(K, np.float32)
+    s[:: 37] = synth.gaussian(seed + 4, len(s[:: 37]))
+    return np.stack([g, o, z, c, t, s]).astype(np.float32)
+
+
+def main():
+    assert O.ref_available(), "build oracle/_ref first: make -f oracle/ref.mk"
+    K = 512
+    for t in TYPES:
+        x = enc_rows(0x5EED4000 + t, K)
+        b = O.ref_quantize(t, x)
+        dec = O.ref_to_float(t, b, K)
+        np.savez_compressed(os.path.join(HERE, f"enc_{t}.npz"), type=t, K=K, x=x, bytes=b, dec=dec)
+    x = synth.with_outliers(synth.gaussian(0x5EED4100, 1024), 0x5EED4101, 0.01, 20.0)
+    x[256:288] = 0.0
+    q, d = O.ref_cpu_q8_0_quantize(x)
+    np.savez_compressed(os.path.join(HERE, "act_q8_0.npz"), x=x, q=q, d=d)
+    for t, (N, K) in ((8, (48, 1024)), (101, (48, 1024))):
+        W = O.ref_quantize(t, synth.gaussian(0x5EED4200 + t, N * K, 0, 0.02).reshape(N, K))
+        xa = synth.gaussian(0x5EED4300 + t, K)
+        qa, da = O.ref_cpu_q8_0_quantize(xa)
+        y = O.ref_cpu_matvec(t, W, N, K, qa, da)
+        np.savez_compressed(os.path.join(HERE, f"matvec_{t}.npz"), type=t, N=N, K=K, W=W, x=xa, q=qa, d=da, y=y)
+    FE, E = 256, 512
+    gate = O.ref_quantize(101, synth.gaussian(0x5EED4400, FE * E, 0, 0.02).reshape(FE, E))
+    up = O.ref_quantize(101, synth.gaussian(0x5EED4401, FE * E, 0, 0.02).reshape(FE, E))
+    down = O.ref_quantize(101, synth.gaussian(0x5EED4402, E * FE, 0, 0.02).reshape(E, FE))
+    xe = synth.gaussian(0x5EED4403, E)
+    qe, de = O.ref_cpu_q8_0_quantize(xe)
+    out = O.ref_cpu_expert_ffn(gate, up, down, FE, E, qe, de)
+    np.savez_compressed(os.path.join(HERE, "expert_ffn.npz"), FE=FE, E=E, gate=gate, up=up, down=down, x=xe, q=qe,
+                        d=de, out=out)
+    for f in sorted(os.listdir(HERE)):
+        if f.endswith(".npz"):
+            print(f, os.path.getsize(os.path.join(HERE, f)))
+
+
+if __name__ == "__main__":
+    main()
