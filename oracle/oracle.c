@@ -990,16 +990,35 @@ int orc_moe_group(const int32_t *ids, int T, int n_used, int n_expert, int tile,
     return nt;
 }
 
-/* src/gpu_ops.hip:245-264 (moe_combine, no shared expert): out = w0 d0 + w1 d1 + ... in slot order */
-void orc_moe_combine(const float *down, const float *wts, float *out, int n_used, int n, int T) {
+/* src/gpu_ops.hip:245-264 (moe_combine): out = w0 d0 + w1 d1 + ... in slot order, each expert's output first
+ * times es[id] when es is set (moe_combine_scaled), weights 1 when wts is NULL, then + shared * sg (+ shared
+ * when sg is NULL) when shared is set. Built without contraction: every product and sum rounds on its own. */
+void orc_moe_combine(const float *down, const float *wts, const float *shared, const float *sg, const int32_t *ids,
+                     const float *es, float *out, int n_used, int n, int T) {
     for (int t = 0; t < T; ++t)
         for (int i = 0; i < n; ++i) {
             const float *dd = down + (size_t)t * n_used * n + i;
-            const float *w = wts + (size_t)t * n_used;
-            float acc = w[0] * dd[0];
-            for (int j = 1; j < n_used; ++j) acc += w[j] * dd[(size_t)j * n];
+            float acc;
+            if (!wts) {
+                acc = dd[0];
+                for (int j = 1; j < n_used; ++j) acc += dd[(size_t)j * n];
+            } else {
+                const float *w = wts + (size_t)t * n_used;
+                const int32_t *e = ids ? ids + (size_t)t * n_used : NULL;
+                acc = es ? (dd[0] * es[e[0]]) * w[0] : w[0] * dd[0];
+                for (int j = 1; j < n_used; ++j)
+                    acc += es ? (dd[(size_t)j * n] * es[e[j]]) * w[j] : w[j] * dd[(size_t)j * n];
+            }
+            if (shared) acc += sg ? shared[(size_t)t * n + i] * sg[t] : shared[(size_t)t * n + i];
             out[(size_t)t * n + i] = acc;
         }
+}
+
+/* the shared expert's gate of src/gpu_ops.hip:213-229: sg = 1 / (1 + expf(-(x . w))), the dot in double */
+float orc_shared_gate(const float *x, const float *w, int n) {
+    double d = 0.0;
+    for (int i = 0; i < n; ++i) d += (double)x[i] * (double)w[i];
+    return 1.0f / (1.0f + expf(-(float)d));
 }
 
 /* src/expert_cpu.cpp:241-248 (SiLU(g) * u with libm expf; the reference's GPU swiglu, src/gpu_ops.hip:103-113,

@@ -84,7 +84,9 @@ void orc_cpu_expert_ffn(const void *gate, const void *up, size_t row_bytes_gu, c
 void orc_moe_router(const float *logits, int T, int n_expert, int n_used, int32_t *ids, float *wts);
 int orc_moe_group(const int32_t *ids, int T, int n_used, int n_expert, int tile, int32_t *tok_rows,
                   int32_t *pair_rows, int32_t *tile_e, int32_t *tile_start, int32_t *tile_n);
-void orc_moe_combine(const float *down, const float *wts, float *out, int n_used, int n, int T);
+void orc_moe_combine(const float *down, const float *wts, const float *shared, const float *sg, const int32_t *ids,
+                     const float *es, float *out, int n_used, int n, int T);
+float orc_shared_gate(const float *x, const float *w, int n);
 void orc_swiglu(const float *g, const float *u, float *out, int64_t n);
 
 /* ---- legacy gemm_act_fp4: C[M][N] = A_fp16[M][K] x deq(W)[N][K]^T, separate-plane layout */

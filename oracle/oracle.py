@@ -63,7 +63,9 @@ def lib():
         L.orc_moe_router.argtypes = [vp, i32, i32, i32, vp, vp]
         L.orc_moe_group.restype = i32
         L.orc_moe_group.argtypes = [vp, i32, i32, i32, i32, vp, vp, vp, vp, vp]
-        L.orc_moe_combine.argtypes = [vp, vp, vp, i32, i32, i32]
+        L.orc_moe_combine.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32]
+        L.orc_shared_gate.restype = C.c_float
+        L.orc_shared_gate.argtypes = [vp, vp, i32]
         L.orc_swiglu.argtypes = [vp, vp, vp, i64]
         L.orc_gemm_act_fp4.argtypes = [vp, vp, vp, vp, i32, i32, i32]
         _lib = L
@@ -167,12 +169,21 @@ def moe_group(ids, n_expert, tile):
     return dict(tok_rows=tok, pair_rows=pair, n_tiles=nt, tile_e=te[:nt], tile_start=ts[:nt], tile_n=tn[:nt])
 
 
-def moe_combine(down, wts):
+def moe_combine(down, wts, shared=None, sg=None, ids=None, es=None):
     down = np.ascontiguousarray(down, dtype=np.float32)
     T, n_used, n = down.shape
     out = np.zeros((T, n), dtype=np.float32)
-    lib().orc_moe_combine(_ptr(down), _ptr(np.ascontiguousarray(wts, dtype=np.float32)), _ptr(out), n_used, n, T)
+    arr = lambda a, dt: None if a is None else np.ascontiguousarray(a, dtype=dt)
+    wts, shared, sg, ids, es = arr(wts, np.float32), arr(shared, np.float32), arr(sg, np.float32), arr(ids, np.int32), \
+        arr(es, np.float32)
+    opt = lambda a: None if a is None else _ptr(a)
+    lib().orc_moe_combine(_ptr(down), opt(wts), opt(shared), opt(sg), opt(ids), opt(es), _ptr(out), n_used, n, T)
     return out
+
+
+def shared_gate(x, w):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return float(lib().orc_shared_gate(_ptr(x), _ptr(np.ascontiguousarray(w, dtype=np.float32)), x.size))
 
 
 def swiglu(g, u):

@@ -1,0 +1,285 @@
+// moe.hip -- the mixture-of-experts glue around the expert matvecs (gfx950, wave64): router, grouping,
+// combine and SwiGLU with the activation quantizer fused in. The reference's gpu_ops.hip:103-330
+// (swiglu, moe_router + router_select, moe_combine, moe_group); the C ABI is include/moe_ops.h.
+//
+//   k_swiglu       out = SiLU(g) * u (g / (1 + exp(-g)) * u), and, with a qmatvec_q8, quantized in the same
+//                  launch (one 256-thread workgroup per 256-value block: q8dev.h).
+//   k_moe_router   a workgroup per token: softmax of the router logits (exp(l - max) / sum), the n_used
+//                  largest probabilities in descending order by rounds of a wave-wide argmax (equal values:
+//                  the lower expert), their weights divided by max(sum, 2^-14), and the shared-expert gate
+//                  sigmoid(x . w_shexp).
+//   k_moe_combine  out = sum_j w_j down_j in slot order (+ sg shared), rounded after every product and sum
+//                  (no contraction) as the reference's CPU add chain.
+//   k_moe_group    one 1024-thread workgroup: entries (token, slot) counted per expert in LDS, two exclusive
+//                  scans (entry and tile offsets), then each entry placed by an LDS atomic. Counts and tiles
+//                  are deterministic; the order of the entries inside an expert's run is not, and nothing
+//                  depends on it (every entry's value is computed alone).
+#include "q8dev.h"
+#include "moe_ops.h"
+
+namespace pq {
+
+constexpr int MOE_MAX_EXPERTS = 1024;
+constexpr int MOE_MAX_USED = 64;
+
+__global__ void __launch_bounds__(256) k_swiglu(const float *__restrict__ g, const float *__restrict__ u,
+                                                float *__restrict__ out, int n, Q8Ptrs o, int quantize) {
+    __shared__ Q8Shared sh;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const bool active = i < n;
+    float v = 0.0f;
+    if (active) {
+        const float a = g[i];
+        v = a / (1.0f + expf(-a)) * u[i];
+        out[i] = v;
+    }
+    if (quantize) q8_quantize_value(v, active, blockIdx.x, sh, o);  // (uniform)
+}
+
+// sum / max over the 256 threads of a workgroup (4 waves), the result in every thread
+__device__ __forceinline__ float wg_sum(float v, float *red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__device__ __forceinline__ float wg_max(float v, float *red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__global__ void __launch_bounds__(256) k_moe_router(const float *__restrict__ logits, const float *__restrict__ x,
+                                                    const float *__restrict__ w_sh, int *__restrict__ ids,
+                                                    float *__restrict__ wts, float *__restrict__ sg, int n_expert,
+                                                    int n_used, int n, int ids_stride) {
+    __shared__ float p[MOE_MAX_EXPERTS];
+    __shared__ float red[4];
+    __shared__ float selw[MOE_MAX_USED];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float *l = logits + (long long)t * n_expert;
+
+    if (w_sh) {  // (uniform) the shared expert's gate
+        const float *xt = x + (long long)t * n;
+        float dsum = 0.0f;
+        for (int i = tid; i < n; i += 256) dsum = fmaf(xt[i], w_sh[i], dsum);
+        dsum = wg_sum(dsum, red);
+        if (tid == 0) sg[t] = 1.0f / (1.0f + expf(-dsum));
+    }
+
+    float mx = -INFINITY;
+    for (int e = tid; e < n_expert; e += 256) mx = fmaxf(mx, l[e]);
+    mx = wg_max(mx, red);
+    float sum = 0.0f;
+    for (int e = tid; e < n_expert; e += 256) {
+        const float v = expf(l[e] - mx);
+        p[e] = v;
+        sum += v;
+    }
+    sum = wg_sum(sum, red);
+    const float inv = 1.0f / sum;
+    for (int e = tid; e < n_expert; e += 256) p[e] *= inv;
+    __syncthreads();
+
+    if (tid < 64) {
+        // wave 0: lane l holds experts l + 64 j; each round takes the largest remaining (the lower expert among
+        // equal values) and its lane drops it
+        constexpr int PL = MOE_MAX_EXPERTS / 64;
+        float v[PL];
+#pragma unroll
+        for (int j = 0; j < PL; ++j) {
+            const int e = tid + 64 * j;
+            v[j] = e < n_expert ? p[e] : -INFINITY;
+        }
+        for (int r = 0; r < n_used; ++r) {
+            float bv = v[0];
+            int bj = 0;
+#pragma unroll
+            for (int j = 1; j < PL; ++j)
+                if (v[j] > bv) {
+                    bv = v[j];
+                    bj = j;
+                }
+            int be = tid + 64 * bj;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const float ov = __shfl_xor(bv, off, 64);
+                const int oe = __shfl_xor(be, off, 64);
+                if (ov > bv || (ov == bv && oe < be)) {
+                    bv = ov;
+                    be = oe;
+                }
+            }
+            if (tid == 0) {
+                ids[(long long)t * ids_stride + r] = be;
+                selw[r] = bv;
+            }
+            if ((be & 63) == tid) {
+#pragma unroll
+                for (int j = 0; j < PL; ++j)
+                    if (j == (be >> 6)) v[j] = -INFINITY;
+            }
+        }
+    }
+    if (tid == n_used && ids_stride > n_used) ids[(long long)t * ids_stride + n_used] = -1;  // the shared slot
+    __syncthreads();
+    if (tid == 0) {
+        float ws = 0.0f;
+        for (int r = 0; r < n_used; ++r) ws += selw[r];
+        ws = fmaxf(ws, 6.103515625e-5f);
+        for (int r = 0; r < n_used; ++r) wts[(long long)t * n_used + r] = selw[r] / ws;
+    }
+}
+
+__global__ void __launch_bounds__(256) k_moe_combine(const float *__restrict__ down, const float *__restrict__ wts,
+                                                     const float *__restrict__ shared, const float *__restrict__ sg,
+                                                     const int *__restrict__ ids, const float *__restrict__ es,
+                                                     float *__restrict__ out, int n_used, int n) {
+#pragma clang fp contract(off)  // (every product and sum rounds on its own, as the reference's add chain)
+    const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float *d = down + (long long)t * n_used * n + i;
+    float acc;
+    if (!wts) {  // (uniform) weight 1
+        acc = d[0];
+        for (int j = 1; j < n_used; ++j) acc = acc + d[(long long)j * n];
+    } else {
+        const float *w = wts + (long long)t * n_used;
+        const int *e = ids + (long long)t * n_used;
+        acc = es ? (d[0] * es[e[0]]) * w[0] : w[0] * d[0];
+        for (int j = 1; j < n_used; ++j) {
+            const float dj = d[(long long)j * n];
+            acc = acc + (es ? (dj * es[e[j]]) * w[j] : w[j] * dj);
+        }
+    }
+    if (shared) {
+        const float s = shared[(long long)t * n + i];
+        acc = acc + (sg ? s * sg[t] : s);
+    }
+    out[(long long)t * n + i] = acc;
+}
+
+// inclusive scans of a and b over the 1024 threads (16 waves); wsum: 2 x 16 LDS ints
+__device__ __forceinline__ void scan1024(int &a, int &b, int (*wsum)[16]) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int ua = __shfl_up(a, d, 64), ub = __shfl_up(b, d, 64);
+        if (lane >= d) {
+            a += ua;
+            b += ub;
+        }
+    }
+    if (lane == 63) {
+        wsum[0][w] = a;
+        wsum[1][w] = b;
+    }
+    __syncthreads();
+    int ba = 0, bb = 0;
+    for (int k = 0; k < w; ++k) {
+        ba += wsum[0][k];
+        bb += wsum[1][k];
+    }
+    a += ba;
+    b += bb;
+}
+
+__global__ void __launch_bounds__(1024) k_moe_group(const int *__restrict__ ids, int T, int n_used, int n_expert,
+                                                    int tile, int *__restrict__ tok_rows, int *__restrict__ pair_rows,
+                                                    int *__restrict__ n_tiles, int *__restrict__ tile_e,
+                                                    int *__restrict__ tile_start, int *__restrict__ tile_n) {
+    __shared__ int cnt[MOE_MAX_EXPERTS], slot[MOE_MAX_EXPERTS];
+    __shared__ int wsum[2][16];
+    const int tid = threadIdx.x, n = T * n_used;
+    cnt[tid] = 0;
+    __syncthreads();
+    for (int i = tid; i < n; i += 1024) {
+        const int e = ids[i];
+        if (e >= 0 && e < n_expert) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    const int c = tid < n_expert ? cnt[tid] : 0, nt = (c + tile - 1) / tile;
+    int a = c, b = nt;
+    scan1024(a, b, wsum);
+    const int eo = a - c, to = b - nt;  // exclusive: expert tid's first entry and first tile
+    slot[tid] = eo;
+    if (tid < n_expert) {
+        for (int k = 0; k < nt; ++k) {
+            tile_e[to + k] = tid;
+            tile_start[to + k] = eo + k * tile;
+            tile_n[to + k] = min(tile, c - k * tile);
+        }
+        if (tid == n_expert - 1) *n_tiles = to + nt;
+    }
+    __syncthreads();
+    for (int i = tid; i < n; i += 1024) {
+        const int e = ids[i];
+        if (e < 0 || e >= n_expert) continue;
+        const int p = atomicAdd(&slot[e], 1);
+        tok_rows[p] = i / n_used;
+        pair_rows[p] = i;
+    }
+}
+
+}  // namespace pq
+
+using namespace pq;
+
+extern "C" {
+
+hipError_t gpu_swiglu(const float *g, const float *u, float *out, int n, const qmatvec_q8 *q8, hipStream_t stream) {
+    if (!g || !u || !out || n < 0) return hipErrorInvalidValue;
+    if (n == 0) return hipSuccess;
+    Q8Ptrs o{};
+    if (q8) {
+        if (n % 32 != 0 || n > q8->max_k) return hipErrorInvalidValue;
+        o = Q8Ptrs{q8->q0, q8->d0, q8->qK, q8->dK, q8->bsK, q8->s0};
+    }
+    hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, g, u, out, n, o, q8 ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t gpu_moe_router(const float *logits, const float *x, const float *w_shexp, int *ids, float *wts, float *sg,
+                          int n_expert, int n_used, int n, int T, hipStream_t stream, int ids_stride) {
+    if (ids_stride == 0) ids_stride = n_used;
+    if (!logits || !ids || !wts || n_expert < 1 || n_expert > MOE_MAX_EXPERTS || n_used < 1 ||
+        n_used > MOE_MAX_USED || n_used > n_expert || T < 0 || ids_stride < n_used || (w_shexp && (!x || !sg || n <= 0)))
+        return hipErrorInvalidValue;
+    if (T == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_moe_router, dim3((unsigned)T), dim3(256), 0, stream, logits, x, w_shexp, ids, wts, sg, n_expert,
+                       n_used, n, ids_stride);
+    return hipGetLastError();
+}
+
+hipError_t gpu_moe_combine_scaled(const float *down, const float *wts, const float *shared, const float *sg,
+                                  const int *ids, const float *exp_scale, float *out, int n_used, int n, int T,
+                                  hipStream_t stream) {
+    if (!down || !out || n_used < 1 || n < 0 || T < 0 || (exp_scale && (!ids || !wts))) return hipErrorInvalidValue;
+    if (n == 0 || T == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n + 255) / 256), (unsigned)T), dim3(256), 0, stream, down, wts,
+                       shared, sg, ids, exp_scale, out, n_used, n);
+    return hipGetLastError();
+}
+
+hipError_t gpu_moe_combine(const float *down, const float *wts, const float *shared, const float *sg, float *out,
+                           int n_used, int n, int T, hipStream_t stream) {
+    return gpu_moe_combine_scaled(down, wts, shared, sg, nullptr, nullptr, out, n_used, n, T, stream);
+}
+
+hipError_t gpu_moe_group(const int *ids, int T, int n_used, int n_expert, int tile, int *tok_rows, int *pair_rows,
+                         int *n_tiles, int *tile_e, int *tile_start, int *tile_n, hipStream_t stream) {
+    if (!ids || !tok_rows || !pair_rows || !n_tiles || !tile_e || !tile_start || !tile_n || T < 0 || n_used < 1 ||
+        n_expert < 1 || n_expert > MOE_MAX_EXPERTS || tile < 1)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(1024), 0, stream, ids, T, n_used, n_expert, tile, tok_rows, pair_rows,
+                       n_tiles, tile_e, tile_start, tile_n);
+    return hipGetLastError();
+}
+
+}  // extern "C"

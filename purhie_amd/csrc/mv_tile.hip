@@ -19,10 +19,11 @@
 //      its unit back (LDS is in order within a wave: no barrier);
 //   4. each lane forms its unit's exact per-block integer dots (v_dot4_i32_i8 on codes decoded by masks or
 //      v_perm_b32 tables) and one float partial per token in the reference's per-block form;
-//   5. partials go to LDS; barrier; thread r adds row r's partials over its units in order.
+//   5. partials go to LDS (the wave's region); barrier; a few threads per row add its partials in a fixed
+//      order set by K.
 // The grid holds every tile of the launch (no persistent loop): all weight loads of a launch are in flight
-// from the start and each wave computes as its data arrives. A row's result is a fixed-order sum of
-// per-unit partials: it does not depend on the tile size, the other matrices of the launch, or how many
+// from the start and each wave computes as its data arrives. A row's result is a sum of per-unit partials
+// in an order set by K alone: it does not depend on the other matrices of the launch or on how many
 // tokens share it.
 #include "device.h"
 #include "kernels.h"
@@ -317,8 +318,9 @@ template <int TYPE>
 struct TileLds {
     static constexpr int REGION = (64 * Tu<TYPE>::BYTES + Tu<TYPE>::LEAD + 15) & ~15;  // a wave's weight bytes
     static constexpr int CH = (REGION / 16 + 63) / 64;                                  // its 16-byte chunks a lane
+    static_assert(REGION >= 4 * 64 * 4, "a region also holds its wave's partials of up to 4 tokens");
     int xt, nd, ns;                                                                     // per token
-    int off_d, off_s, off_lut, off_p, off_w, bytes;
+    int off_d, off_s, off_lut, off_w, bytes;
     __host__ __device__ TileLds(int K, int NT) {
         using P = Tu<TYPE>;
         xt = (K + 255) / 256 * TL_PAD;
@@ -327,8 +329,7 @@ struct TileLds {
         off_d = NT * xt;
         off_s = off_d + ((NT * nd * 4 + 15) & ~15);
         off_lut = off_s + ((NT * ns * 4 + 15) & ~15);
-        off_p = off_lut + (P::LUT ? 1024 : 0);
-        off_w = off_p + NT * TL_THREADS * 4;
+        off_w = off_lut + (P::LUT ? 1024 : 0);
         bytes = off_w + (TL_THREADS / 64) * REGION;
     }
 };
@@ -416,7 +417,7 @@ struct Stager {
 
 // One tile: rows [row0, row0 + nr) of one matrix (contiguous, nb units each, nr * nb <= 256).
 template <int TYPE, int NT, class Rows>
-__device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int row0, int nr, int K, int nb,
+__device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int row0, int nr, int K, int nb, int lg,
                                           const int8_t *q, const float *d, const int32_t *bs) {
     using P = Tu<TYPE>;
     using TL = TileLds<TYPE>;
@@ -469,27 +470,42 @@ __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int r
     float acc[NT];
     P::template compute<NT>(w, aux, x, acc);
 
-    float *part = (float *)(smem + L.off_p);
+    // partials into the wave's own region (its units were read above; LDS is in order within a wave)
+    float *part = (float *)region;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) part[t * TL_THREADS + tid] = acc[t];
+    for (int t = 0; t < NT; ++t) part[t * 64 + lane] = acc[t];
     __syncthreads();
-    if (tid < nr) {
+    // row r's sum: G = 2^lg threads per row each add every G-th partial, then a butterfly over the G
+    // (a fixed order, set by K alone)
+    const int G = 1 << lg, r = tid >> lg, i = tid & (G - 1);
+    const int rr = r < nr ? r : 0;
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const float *pr = part + t * TL_THREADS + tid * nb;
-            float s = 0.0f;
-            for (int kk = 0; kk < nb; ++kk) s += pr[kk];
-            rows.store(row0 + tid, t, s);
+    for (int t = 0; t < NT; ++t) {
+        float s = 0.0f;
+        for (int kk = i; kk < nb; kk += G) {
+            const int uu = rr * nb + kk;
+            s += ((const float *)(smem + L.off_w + (uu >> 6) * TL::REGION))[t * 64 + (uu & 63)];
         }
+        s = group_sum(s, G);
+        if (i == 0 && r < nr) rows.store(row0 + r, t, s);
     }
 }
 
 // ---------------------------------------------------------------- kernels
 
-// tiles of R rows, per matrix: matrix m owns tiles [tp[m - 1], tp[m]) of the grid
+// tiles of R rows, per matrix: matrix m owns tiles [tp[m - 1], tp[m]) of the grid; 2^lg threads add a row
 struct TileArgs {
-    int R, nb, tp[4];
+    int R, nb, lg, tp[4];
 };
+
+static TileArgs tile_args(int nb) {
+    TileArgs ta = {};
+    ta.nb = nb;
+    ta.R = TL_THREADS / nb;
+    ta.lg = 0;
+    while (ta.lg < 6 && (ta.R << (ta.lg + 1)) <= TL_THREADS) ++ta.lg;
+    return ta;
+}
 
 template <int TYPE, int NT>
 __global__ void __launch_bounds__(TL_THREADS) k_mv_tile(MvArgs a, TileArgs ta) {
@@ -501,7 +517,7 @@ __global__ void __launch_bounds__(TL_THREADS) k_mv_tile(MvArgs a, TileArgs ta) {
     const int row0 = rows.base(m) + (bx - first) * ta.R;
     const int end = DenseRows::pick(m, a.bound[0], a.bound[1], a.bound[2], a.bound[3]);
     const int nr = end - row0 < ta.R ? end - row0 : ta.R;
-    tile_body<TYPE, NT>(smem, rows, row0, nr, a.K, ta.nb, a.q, a.d, a.bs);
+    tile_body<TYPE, NT>(smem, rows, row0, nr, a.K, ta.nb, ta.lg, a.q, a.d, a.bs);
 }
 
 // MoE: grid (tiles, n_used * nmat, T); slot j of token t uses expert ids[t * n_used + j] (-1: Wx)
@@ -518,7 +534,7 @@ __global__ void __launch_bounds__(TL_THREADS) k_mv_tile_id(MvIdArgs a, TileArgs 
                       e < 0 ? a.sx[m] : a.es[m] ? a.es[m][e] : a.s[m]};
     const int row0 = (int)blockIdx.x * ta.R;
     const int nr = a.N - row0 < ta.R ? a.N - row0 : ta.R;
-    tile_body<TYPE, 1>(smem, rows, row0, nr, K, ta.nb, a.q + in_row * K, a.d + in_row * (K / Tu<TYPE>::ACT),
+    tile_body<TYPE, 1>(smem, rows, row0, nr, K, ta.nb, ta.lg, a.q + in_row * K, a.d + in_row * (K / Tu<TYPE>::ACT),
                        a.bs ? a.bs + in_row * (K / 16) : nullptr);
 }
 
@@ -549,9 +565,7 @@ static hipError_t tile_dense(const MvArgs &a, hipStream_t stream) {
     int nW = 1;
     while (nW < 4 && a.bound[nW - 1] < a.Nt) ++nW;
     if (!tile_takes<TYPE>(a.K, NT, a.W, nW, a.row_bytes, a.q, a.d, a.bs)) return hipErrorNotSupported;
-    TileArgs ta;
-    ta.nb = a.K / Tu<TYPE>::VALS;
-    ta.R = TL_THREADS / ta.nb;
+    TileArgs ta = tile_args(a.K / Tu<TYPE>::VALS);
     int tiles = 0, lo = 0;
     for (int i = 0; i < 4; ++i) {
         const int n = a.bound[i] - lo;
@@ -592,9 +606,7 @@ static hipError_t tile_id(const MvIdArgs &a, hipStream_t stream) {
     // sums on from the previous one, which keeps every row as aligned as the first when K % VALS == 0)
     const uint8_t *W[4] = {a.W[0], a.Wx[0], a.nmat > 1 ? a.W[1] : nullptr, a.nmat > 1 ? a.Wx[1] : nullptr};
     if (!tile_takes<TYPE>(a.K, 1, W, 4, a.row_bytes, a.q, a.d, a.bs)) return hipErrorNotSupported;
-    TileArgs ta = {};
-    ta.nb = a.K / Tu<TYPE>::VALS;
-    ta.R = TL_THREADS / ta.nb;
+    const TileArgs ta = tile_args(a.K / Tu<TYPE>::VALS);
     const dim3 grid((unsigned)((a.N + ta.R - 1) / ta.R), (unsigned)(a.n_used * a.nmat), (unsigned)a.T);
     const size_t lds = (size_t)TileLds<TYPE>(a.K, 1).bytes;
     hipLaunchKernelGGL((k_mv_tile_id<TYPE>), grid, dim3(TL_THREADS), lds, stream, a, ta);

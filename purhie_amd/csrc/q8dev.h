@@ -1,0 +1,94 @@
+// q8dev.h -- the activation quantizer's per-value step, shared by the standalone quantizer (q8act.hip) and
+// the producer kernels that quantize their own output (moe.hip's swiglu), as the reference's q8_block_value
+// (src/q8_device.h:54-104).
+//
+// A 256-thread workgroup (4 waves) holds one 256-value block, one value per thread, and writes both of
+// ggml's activation formats, bit-identical to the reference:
+//   Q8_0: per 32 values am = max|x|, q = rint(x * (127 / am)) (ties to even), d = fp16(am / 127),
+//         s0 = fp16((am / 127) * sum q) kept as float bits (the Q8_1 block sum);
+//   Q8_K: per 256 values v = the signed value of largest |x| (lowest index on ties), iscale = -127 / v,
+//         q = min(127, rint(iscale * x)), d = 1 / iscale (0 for an all-zero block), sums of every 16 q.
+// A 32-value Q8_0 block is half a wave: the xor reductions use offsets 16..1, which stay inside it.
+#pragma once
+
+#include "device.h"
+#include "kernels.h"
+
+namespace pq {
+
+struct Q8Shared {
+    float a[4], v[4];
+    int i[4];
+};
+
+// value v of thread t of block b (i = 256 b + t; inactive threads past the end hold 0); every thread of the
+// workgroup calls it (a barrier inside when o.qK is set)
+__device__ __forceinline__ void q8_quantize_value(float v, bool active, int b, Q8Shared &sh, const Q8Ptrs &o) {
+    const int t = threadIdx.x, i = b * 256 + t;
+    const int lane = t & 63, w = t >> 6;
+    const float a = fabsf(v);
+
+    // Q8_0 over the 32 values of this half-wave
+    float am = a;
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+    const float id0 = am != 0.0f ? 127.0f / am : 0.0f;
+    const int q0 = active ? (int)rintf(v * id0) : 0;
+    int s0 = q0;
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) s0 += __shfl_xor(s0, off, 64);
+    if (active) {
+        o.q0[i] = (int8_t)q0;
+        if ((lane & 31) == 0) {
+            const float d = am / 127.0f;
+            o.d0[i >> 5] = __half2float(__float2half(d));
+            if (o.s0) o.s0[i >> 5] = __float_as_int(__half2float(__float2half(d * (float)s0)));
+        }
+    }
+    if (!o.qK) return;  // (uniform)
+
+    // Q8_K over the 256 values: largest |x|, the lowest index on ties
+    float ba = a, bv = v;
+    int bi = t;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float oa = __shfl_xor(ba, off, 64), ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (oa > ba || (oa == ba && oi < bi)) {
+            ba = oa;
+            bi = oi;
+            bv = ov;
+        }
+    }
+    if (lane == 0) {
+        sh.a[w] = ba;
+        sh.v[w] = bv;
+        sh.i[w] = bi;
+    }
+    __syncthreads();
+    float fa = sh.a[0], fv = sh.v[0];
+    int fi = sh.i[0];
+#pragma unroll
+    for (int k = 1; k < 4; ++k)
+        if (sh.a[k] > fa || (sh.a[k] == fa && sh.i[k] < fi)) {
+            fa = sh.a[k];
+            fi = sh.i[k];
+            fv = sh.v[k];
+        }
+    int q = 0;
+    float iscale = 0.0f;
+    if (fa != 0.0f) {
+        iscale = -127.0f / fv;
+        q = min(127, (int)rintf(iscale * v));
+    }
+    int s16 = q;
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) s16 += __shfl_xor(s16, off, 64);
+    if (active) {
+        o.qK[i] = (int8_t)q;
+        if (t == 0) o.dK[b] = fa != 0.0f ? 1.0f / iscale : 0.0f;
+        if ((lane & 15) == 0) o.bsK[i >> 4] = s16;
+    }
+}
+
+}  // namespace pq

@@ -1,0 +1,77 @@
+"""ctypes mirror of include/moe_ops.h (the MoE router, grouping, combine and fused SwiGLU + quantize of
+libpurhie_qmv.so), the reference's src/gpu_ops.h MoE entry points. Device buffers are torch tensors; every
+call runs the library's HIP kernels (no CPU path)."""
+import ctypes as C
+
+import numpy as np
+
+from . import qmatvec as Q
+
+_sigs_done = False
+
+
+def lib():
+    global _sigs_done
+    L = Q.lib()
+    if not _sigs_done:
+        vp, i32 = C.c_void_p, C.c_int
+        pq8 = C.POINTER(Q.qmatvec_q8)
+        for name, args in {
+            "gpu_swiglu": [vp, vp, vp, i32, pq8, vp],
+            "gpu_moe_router": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32],
+            "gpu_moe_combine": [vp, vp, vp, vp, vp, i32, i32, i32, vp],
+            "gpu_moe_combine_scaled": [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp],
+            "gpu_moe_group": [vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp],
+        }.items():
+            f = getattr(L, name)
+            f.restype, f.argtypes = i32, args
+        _sigs_done = True
+    return L
+
+
+def _p(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _check(fn, rc):
+    if rc != 0:
+        raise Q.HipError(fn, rc)
+
+
+def max_tiles(T, n_used, n_expert, tile):
+    """gpu_moe_max_tiles (include/moe_ops.h)"""
+    n = T * n_used
+    return min(n, n_expert + n // tile)
+
+
+def swiglu(g, u, out, n, q8=None, stream=None):
+    _check("gpu_swiglu", lib().gpu_swiglu(_p(g), _p(u), _p(out), n, None if q8 is None else q8.ref, stream))
+
+
+def router(logits, ids, wts, n_expert, n_used, T, x=None, w_shexp=None, sg=None, n=0, ids_stride=0, stream=None):
+    _check("gpu_moe_router", lib().gpu_moe_router(_p(logits), _p(x), _p(w_shexp), _p(ids), _p(wts), _p(sg), n_expert,
+                                                  n_used, n, T, stream, ids_stride))
+
+
+def combine(down, wts, out, n_used, n, T, shared=None, sg=None, ids=None, exp_scale=None, stream=None):
+    if ids is None and exp_scale is None:
+        rc = lib().gpu_moe_combine(_p(down), _p(wts), _p(shared), _p(sg), _p(out), n_used, n, T, stream)
+    else:
+        rc = lib().gpu_moe_combine_scaled(_p(down), _p(wts), _p(shared), _p(sg), _p(ids), _p(exp_scale), _p(out),
+                                          n_used, n, T, stream)
+    _check("gpu_moe_combine", rc)
+
+
+def group(ids, T, n_used, n_expert, tile, stream=None):
+    """gpu_moe_group into fresh device buffers; returns them as numpy arrays (n_tiles entries of the tiles)"""
+    import torch
+    n = T * n_used
+    mt = max(1, max_tiles(T, n_used, n_expert, tile))
+    z = lambda k: torch.full((k,), -7, dtype=torch.int32, device="cuda")
+    tok, pair, nt, te, ts, tn = z(max(n, 1)), z(max(n, 1)), z(1), z(mt), z(mt), z(mt)
+    _check("gpu_moe_group", lib().gpu_moe_group(_p(ids), T, n_used, n_expert, tile, _p(tok), _p(pair), _p(nt), _p(te),
+                                                _p(ts), _p(tn), stream))
+    torch.cuda.synchronize()
+    k = int(nt.cpu()[0])
+    return dict(n_tiles=k, tok_rows=tok.cpu().numpy()[:n], pair_rows=pair.cpu().numpy()[:n],
+                tile_e=te.cpu().numpy()[:k], tile_start=ts.cpu().numpy()[:k], tile_n=tn.cpu().numpy()[:k])

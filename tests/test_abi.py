@@ -34,7 +34,8 @@ def test_headers_declare_the_reference_surface():
     names = declared_functions()
     for n in ("qmatvec_init", "qmatvec_quantize", "qmatvec_launch_q8", "qmatvec_launch_q8_multi_t",
               "qmatvec_launch_q8_batch", "qmatvec_launch_q8_id_x", "qmatvec_launch_q8_id_batch", "qt_row_size",
-              "qt_to_float", "qt_get_traits"):
+              "qt_to_float", "qt_get_traits", "gpu_swiglu", "gpu_moe_router", "gpu_moe_combine",
+              "gpu_moe_combine_scaled", "gpu_moe_group"):
         assert n in names, n
 
 

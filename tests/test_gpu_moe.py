@@ -1,0 +1,134 @@
+"""GPU parity of the MoE glue (include/moe_ops.h) against the oracle's restatement of src/gpu_ops.hip:103-330:
+router selection exact, weights and the shared gate to float tolerance, combine bit for bit (both sides round
+every product and sum), grouping counts / tiles exact with every expert run holding exactly its entries, and
+the fused SwiGLU quantization bit-identical to quantizing the SwiGLU output on its own."""
+import numpy as np
+import pytest
+
+from purhie_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def M():
+    from purhie_amd import moe
+    moe.lib()
+    return moe
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+@pytest.mark.parametrize("T,E,n_used", [(1, 128, 8), (512, 128, 8), (7, 256, 8), (3, 1024, 64), (5, 16, 4)])
+def test_router(M, oracle, T, E, n_used):
+    import torch
+    logits = synth.gaussian(900 + T + E, T * E).reshape(T, E)
+    if T >= 3:
+        logits[1, 5] = logits[1, 9] = logits[1].max() + 1.0  # equal leaders: the lower expert first
+        logits[2, :] = 0.25                                    # all equal
+    ids = torch.full((T, n_used), -9, dtype=torch.int32, device="cuda")
+    wts = torch.zeros((T, n_used), dtype=torch.float32, device="cuda")
+    M.router(dev(logits), ids, wts, E, n_used, T)
+    want_ids, want_w = oracle.moe_router(logits, n_used)
+    assert np.array_equal(host(ids), want_ids)
+    assert np.allclose(host(wts), want_w, rtol=2e-6, atol=1e-8)
+
+
+def test_router_shared_gate_and_stride(M, oracle):
+    import torch
+    T, E, n_used, n = 6, 128, 8, 2048
+    logits = synth.gaussian(950, T * E).reshape(T, E)
+    x = synth.gaussian(951, T * n).reshape(T, n)
+    w = synth.gaussian(952, n, 0, 0.02)
+    ids = torch.full((T, n_used + 1), -9, dtype=torch.int32, device="cuda")
+    wts = torch.zeros((T, n_used), dtype=torch.float32, device="cuda")
+    sg = torch.zeros(T, dtype=torch.float32, device="cuda")
+    M.router(dev(logits), ids, wts, E, n_used, T, x=dev(x), w_shexp=dev(w), sg=sg, n=n, ids_stride=n_used + 1)
+    got = host(ids)
+    want_ids, _ = oracle.moe_router(logits, n_used)
+    assert np.array_equal(got[:, :n_used], want_ids)
+    assert np.all(got[:, n_used] == -1)
+    want_sg = np.array([oracle.shared_gate(x[t], w) for t in range(T)], np.float32)
+    assert np.allclose(host(sg), want_sg, rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("variant", ["plain", "shared_gated", "shared", "scaled", "unit_weights"])
+def test_combine_bit_exact(M, oracle, variant):
+    import torch
+    T, J, n, E = 5, 8, 2048, 128
+    down = synth.gaussian(960, T * J * n).reshape(T, J, n)
+    w = np.abs(synth.gaussian(961, T * J)).reshape(T, J)
+    sh = synth.gaussian(962, T * n).reshape(T, n)
+    sg = np.abs(synth.gaussian(963, T))
+    ids = (synth.splitmix64(964, T * J) % np.uint64(E)).astype(np.int32).reshape(T, J)
+    es = synth.gaussian(965, E)
+    a = dict(plain=(w, None, None, None), shared_gated=(w, sh, sg, None), shared=(w, sh, None, None),
+             scaled=(w, None, None, es), unit_weights=(None, sh, None, None))[variant]
+    wts, shared, gate, scale = a
+    out = torch.full((T, n), float("nan"), dtype=torch.float32, device="cuda")
+    opt = lambda v: None if v is None else dev(v)
+    M.combine(dev(down), opt(wts), out, J, n, T, shared=opt(shared), sg=opt(gate),
+              ids=dev(ids) if scale is not None else None, exp_scale=opt(scale))
+    want = oracle.moe_combine(down, wts, shared, gate, ids if scale is not None else None, scale)
+    assert np.array_equal(host(out).view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("T,n_used,E,tile", [(512, 8, 128, 64), (2427, 8, 256, 64), (1, 8, 128, 16), (37, 4, 16, 5),
+                                             (0, 8, 128, 64)])
+def test_group(M, oracle, T, n_used, E, tile):
+    ids = (synth.splitmix64(970 + T, max(T, 1) * n_used) % np.uint64(E)).astype(np.int32)[:T * n_used]
+    if T >= 37:
+        ids[: 3 * n_used] = 3  # a heavy expert
+    got = M.group(dev(ids if T else np.zeros(1, np.int32)), T, n_used, E, tile)
+    if T == 0:
+        assert got["n_tiles"] == 0
+        return
+    want = oracle.moe_group(ids.reshape(T, n_used), E, tile)
+    assert got["n_tiles"] == want["n_tiles"] <= M.max_tiles(T, n_used, E, tile)
+    for k in ("tile_e", "tile_start", "tile_n"):
+        assert np.array_equal(got[k], want[k][:want["n_tiles"]]), k
+    for k in range(got["n_tiles"]):
+        s, n = got["tile_start"][k], got["tile_n"][k]
+        assert np.all(ids[got["pair_rows"][s:s + n]] == got["tile_e"][k])
+    # every expert's run holds exactly its entries (the order inside a run is free)
+    cnt = np.bincount(ids, minlength=E)
+    off = np.concatenate([[0], np.cumsum(cnt)])
+    for e in range(E):
+        run = np.sort(got["pair_rows"][off[e]:off[e + 1]])
+        assert np.array_equal(run, np.nonzero(ids == e)[0])
+    assert np.array_equal(got["tok_rows"], got["pair_rows"] // n_used)
+
+
+@pytest.mark.parametrize("n", [768, 2048, 3072, 96])
+def test_swiglu_fused_quantize(M, oracle, n):
+    import torch
+    from purhie_amd import qmatvec as Q
+    g = synth.gaussian(980 + n, n) * 3.0
+    u = synth.gaussian(981 + n, n)
+    out = torch.zeros(n, dtype=torch.float32, device="cuda")
+    q = Q.Q8(((n + 255) // 256) * 256)
+    M.swiglu(dev(g), dev(u), out, n, q)
+    got = host(out)
+    assert np.allclose(got, oracle.swiglu(g, u), rtol=1e-6, atol=1e-30)
+    v = {k: host(t) for k, t in q.views(n).items()}
+    a0 = oracle.quantize_act(got, kq=False)
+    assert np.array_equal(v["q0"], a0["q"])
+    assert np.array_equal(v["d0"].view(np.uint32), a0["d"].view(np.uint32))
+    assert np.array_equal(v["s0"], a0["s0"])
+    if n % 256 == 0:
+        aK = oracle.quantize_act(got, kq=True)
+        assert np.array_equal(v["qK"], aK["q"])
+        assert np.array_equal(v["dK"].view(np.uint32), aK["d"].view(np.uint32))
+        assert np.array_equal(v["bsK"], aK["bs"])
+    out2 = torch.zeros(n, dtype=torch.float32, device="cuda")
+    M.swiglu(dev(g), dev(u), out2, n)  # without quantization: the same values
+    assert np.array_equal(host(out2).view(np.uint32), got.view(np.uint32))

@@ -337,3 +337,40 @@ def test_moe_combine_and_swiglu(oracle):
     g, u = synth.gaussian(98, 1000), synth.gaussian(99, 1000)
     s = oracle.swiglu(g, u)
     assert np.allclose(s, g / (1 + np.exp(-g.astype(np.float64))) * u, rtol=1e-6, atol=1e-7)
+
+
+def test_moe_combine_variants_step_by_step(oracle):
+    """shared expert (gated and ungated), per-expert scales and unit weights, against float32 steps in the
+    reference's order (src/gpu_ops.hip:245-264): the oracle rounds every product and sum on its own"""
+    T, J, n, E = 3, 4, 40, 10
+    down = synth.gaussian(196, T * J * n).reshape(T, J, n)
+    w = np.abs(synth.gaussian(197, T * J)).reshape(T, J)
+    sh = synth.gaussian(198, T * n).reshape(T, n)
+    sg = np.abs(synth.gaussian(199, T))
+    ids = (synth.splitmix64(200, T * J) % np.uint64(E)).astype(np.int32).reshape(T, J)
+    es = synth.gaussian(201, E)
+    f = np.float32
+
+    def want(wts, shared, gate, scale):
+        out = np.zeros((T, n), f)
+        for t in range(T):
+            for i in range(n):
+                if wts is None:
+                    acc = down[t, 0, i]
+                    for j in range(1, J):
+                        acc = f(acc + down[t, j, i])
+                else:
+                    term = lambda j: (f(f(down[t, j, i] * scale[ids[t, j]]) * wts[t, j]) if scale is not None
+                                      else f(wts[t, j] * down[t, j, i]))
+                    acc = term(0)
+                    for j in range(1, J):
+                        acc = f(acc + term(j))
+                if shared is not None:
+                    acc = f(acc + (f(shared[t, i] * gate[t]) if gate is not None else shared[t, i]))
+                out[t, i] = acc
+        return out
+
+    for wts, shared, gate, scale in ((w, None, None, None), (w, sh, sg, None), (w, sh, None, None),
+                                     (w, None, None, es), (None, sh, None, None)):
+        got = oracle.moe_combine(down, wts, shared, gate, ids if scale is not None else None, scale)
+        assert np.array_equal(got.view(np.uint32), want(wts, shared, gate, scale).view(np.uint32))
