@@ -400,4 +400,253 @@ hipError_t launch_gemm(int type, const GemmArgs &a, dim3 grid, hipStream_t strea
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- split-activation GEMM (ROCmFP4, FAST)
+// The activation value X = q dx (int8 q times its fp16-rounded block scale: at most 19 significant bits,
+// exact in fp32) is written as two fp16 planes, hi = fp16(X 2^s) and lo = fp16(X 2^s - hi), with a per-token
+// power of two 2^s that puts the row's largest |X| just under 2^14. hi + lo carries X to 2^-22 relative (the
+// lo rounding), products with the weight value CB * scale (exact in fp16) are exact in fp32, so the MFMAs
+// chain straight through K with no per-block epilogue: y = (sum_k W'[n][k] (hi + lo)[t][k]) 2^-s. The
+// matrix core does twice the multiplies of the per-block form, and the vector ALU only decodes weights.
+
+// one workgroup per token row (rows >= T, up to Tpad + 1, are zero): hi / lo planes in the GEMM's K order
+// (perm: position 2j <- value j, 2j + 1 <- value j + 16 of each 32-block) and ts[t] = 2^-s
+__global__ void __launch_bounds__(256) k_act_split(const int8_t *__restrict__ q, const float *__restrict__ d, int T,
+                                                   int K, int perm, _Float16 *__restrict__ xh,
+                                                   _Float16 *__restrict__ xl, float *__restrict__ ts) {
+    __shared__ float red[4];
+    const int t = blockIdx.x, tid = threadIdx.x, nb = K / 32;
+    _Float16 *oh = xh + (long long)t * K, *ol = xl + (long long)t * K;
+    if (t >= T) {  // (uniform)
+        for (int k = tid; k < K; k += 256) {
+            oh[k] = (_Float16)0.0f;
+            ol[k] = (_Float16)0.0f;
+        }
+        if (tid == 0) ts[t] = 0.0f;
+        return;
+    }
+    const float *dt = d + (long long)t * nb;
+    float m = 0.0f;
+    for (int b = tid; b < nb; b += 256) m = fmaxf(m, dt[b]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // 127 m = f 2^e with f in [0.5, 1): |X| 2^s < 2^14 for s = 14 - e (clamped so that 2^s and 2^-s stay normal)
+    int e = 0;
+    if (m > 0.0f) (void)frexpf(127.0f * m, &e);
+    int sh = 14 - e;
+    sh = sh > 100 ? 100 : sh < -100 ? -100 : sh;
+    const float up = ldexpf(1.0f, sh);
+    if (tid == 0) ts[t] = ldexpf(1.0f, -sh);
+    const int8_t *qt = q + (long long)t * K;
+    for (int i = tid; i < K; i += 256) {
+        const int b = i >> 5, j = i & 31;
+        const float x = (float)qt[i] * dt[b] * up;  // exact: 8 x 11 significant bits, times a power of two
+        const _Float16 h = (_Float16)x;
+        const _Float16 l = (_Float16)(x - (float)h);
+        const int pos = perm ? 32 * b + (j < 16 ? 2 * j : 2 * (j - 16) + 1) : i;
+        oh[pos] = h;
+        ol[pos] = l;
+    }
+}
+
+constexpr int GS_K = 64;                  // K per stage (two 32-blocks)
+constexpr int GS_ROW = GS_K + 8;          // halves per LDS row (16 bytes of padding: conflict-free b128 reads)
+constexpr int GS_N = 256;                 // weight rows per workgroup (one per thread when staging)
+constexpr int GS_T = 128;                 // tokens per workgroup
+
+// the stage's two weight blocks of row n0 + t (thread t), decoded into the 64 halves of its LDS row
+template <int TYPE>
+struct SplitStage {
+    static constexpr int BB = TYPE == TY_FP4 ? 18 : 17;  // block bytes
+    struct Raw {
+        uint32_t w[9];
+        uint32_t off;
+    };
+    __device__ static void load(const uint8_t *W, long long rb, int N, int n0, int k0, Raw &r) {
+        const int row = n0 + threadIdx.x;
+        const int rr = row < N ? row : N - 1;  // (rows past the end repeat the last; their outputs are not stored)
+        // nine dwords from the 4-aligned address at or below the pair (it starts 0 or 2 bytes past one: 2 BB k0 / 64
+        // is even for ROCmFP4, and 34 m leaves 0 or 2 for FAST); each holds at least one byte of the pair
+        const uint8_t *b = W + (long long)rr * rb + (long long)(k0 / 32) * BB;
+        r.off = (uint32_t)((uintptr_t)b & 3u);
+        const uint8_t *a = b - r.off;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) r.w[k] = ld32(a + 4 * k);
+    }
+    __device__ static void store(const Raw &r, const uint32_t *lut, _Float16 *sW) {
+        uint32_t w[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) w[k] = align_bytes(k < 8 ? r.w[k + 1] : 0u, r.w[k], r.off);
+        _Float16 *dst = sW + threadIdx.x * GS_ROW;
+        // block 0 at byte 0, block 1 at byte BB (values then scale bytes)
+        const uint32_t qa[4] = {w[0], w[1], w[2], w[3]};
+        uint32_t qb[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) qb[k] = align_bytes(w[k + 5], w[k + 4], BB - 16);
+        if (TYPE == TY_FP4) {
+            fp4_block_to_lds(qa, ue4m3_half(w[4]), ue4m3_half(w[4] >> 8), lut, dst);
+            fp4_block_to_lds(qb, ue4m3_half(w[8] >> 16), ue4m3_half(w[8] >> 24), lut, dst + 32);
+        } else {
+            const float ea = ue4m3_half(w[4]), eb = ue4m3_half(w[8] >> 8);
+            fp4_block_to_lds(qa, ea, ea, lut, dst);
+            fp4_block_to_lds(qb, eb, eb, lut, dst + 32);
+        }
+    }
+};
+
+// workgroup tile 256 weight rows x 128 tokens; wave w computes rows 128 (w & 1) .. + 127 x tokens 64 (w >> 1) ..
+// + 63 (8 x 4 MFMA tiles): a wave reads 8 weight and 2 x 4 token fragments per 32-block for 64 MFMAs
+template <int TYPE>
+__global__ void __launch_bounds__(G_THREADS, 2) k_gemm_split(GemmArgs a) {
+    using S = SplitStage<TYPE>;
+    __shared__ __attribute__((aligned(16))) _Float16 sW[GS_N * GS_ROW];
+    __shared__ __attribute__((aligned(16))) _Float16 sH[GS_T * GS_ROW];
+    __shared__ __attribute__((aligned(16))) _Float16 sL[GS_T * GS_ROW];
+    __shared__ uint32_t lut[256];
+
+    int n0, e = 0;
+    TokMap tm;
+    const int32_t *orow = nullptr;
+    if (a.n_tiles) {  // MoE: grid (row tiles, tiles)
+        const int k = blockIdx.y;
+        if (k >= *a.n_tiles) return;
+        e = a.tile_e[k];
+        const int st = a.tile_start[k];
+        tm = {a.in_rows + st, 0, a.tile_n[k], a.zero_row};
+        orow = a.out_rows + st;
+        n0 = blockIdx.x * GS_N;
+    } else {          // dense: grid (token tiles, row tiles); a row tile's token tiles are adjacent
+        tm = {nullptr, (int)blockIdx.x * GS_T, GS_T, a.zero_row};
+        n0 = blockIdx.y * GS_N;
+    }
+    const uint8_t *W = a.W + (long long)e * a.N * a.row_bytes;
+    init_fp4_lut(lut);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wn = (wave & 1) * 128, wt = (wave >> 1) * 64;
+
+    // token staging: thread t copies 32 halves (64 bytes) of hi and of lo of token row t / 2
+    const int xr = tid >> 1, xp = tid & 1;
+    const long long xoff = (long long)tm.row(xr) * a.K + 32 * xp;
+    const _Float16 *hsrc = a.xh + xoff, *lsrc = a.xl + xoff;
+
+    typename S::Raw raw;
+    uint4 hv0, hv1, hv2, hv3, lv0, lv1, lv2, lv3;  // (scalars: an array here ends up in scratch)
+#define GSPLIT_ISSUE(k0)                                                \
+    do {                                                                \
+        S::load(W, a.row_bytes, a.N, n0, (k0), raw);                    \
+        const uint4 *h4 = (const uint4 *)(hsrc + (k0));                 \
+        const uint4 *l4 = (const uint4 *)(lsrc + (k0));                 \
+        hv0 = h4[0];                                                    \
+        hv1 = h4[1];                                                    \
+        hv2 = h4[2];                                                    \
+        hv3 = h4[3];                                                    \
+        lv0 = l4[0];                                                    \
+        lv1 = l4[1];                                                    \
+        lv2 = l4[2];                                                    \
+        lv3 = l4[3];                                                    \
+    } while (0)
+
+    f4 acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    GSPLIT_ISSUE(0);
+    for (int k0 = 0; k0 < a.K; k0 += GS_K) {
+        __syncthreads();  // the previous stage's LDS reads are done (and the table is written)
+        S::store(raw, lut, sW);
+        uint4 *hd = (uint4 *)(sH + xr * GS_ROW + 32 * xp), *ld = (uint4 *)(sL + xr * GS_ROW + 32 * xp);
+        hd[0] = hv0;
+        hd[1] = hv1;
+        hd[2] = hv2;
+        hd[3] = hv3;
+        ld[0] = lv0;
+        ld[1] = lv1;
+        ld[2] = lv2;
+        ld[3] = lv3;
+        __syncthreads();
+        if (k0 + GS_K < a.K) GSPLIT_ISSUE(k0 + GS_K);  // next stage's global loads in flight during the MFMAs
+
+#pragma unroll
+        for (int b = 0; b < GS_K / 32; ++b) {
+            const int kk = b * 32 + 8 * (lane >> 4);
+            h8 fh[4], fl[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                fh[j] = *(const h8 *)(sH + (wt + 16 * j + (lane & 15)) * GS_ROW + kk);
+                fl[j] = *(const h8 *)(sL + (wt + 16 * j + (lane & 15)) * GS_ROW + kk);
+            }
+            h8 fa[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) fa[i] = *(const h8 *)(sW + (wn + 16 * i + (lane & 15)) * GS_ROW + kk);
+            // (the four hi products of a weight fragment first: a lo product then finds its accumulator's hi result
+            // ready)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fh[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fl[j], acc[i][j], 0, 0, 0);
+            }
+            // the block's 16 fragment reads are issued before its 64 MFMAs (left alone, the scheduler moves each
+            // weight fragment's read next to its first use and waits for it there)
+            __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 64, 0);
+        }
+    }
+#undef GSPLIT_ISSUE
+
+    // store: lane holds rows 4 (lane / 16) .. + 3 of each 16 x 16 tile, token column lane % 16
+    const float sc = a.es ? a.es[e] : a.osc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int tt = wt + 16 * j + (lane & 15);
+        long long yrow;
+        if (orow) {
+            if (tt >= tm.n) continue;
+            yrow = (long long)orow[tt] * a.N;
+        } else {
+            const int t = tm.base + tt;
+            if (t >= a.T) continue;
+            yrow = (long long)t * a.ldy;
+        }
+        const float s = sc * a.ts[tm.row(tt)];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int n = n0 + wn + 16 * i + 4 * (lane >> 4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (n + r < a.N) a.y[yrow + n + r] = acc[i][j][r] * s;
+        }
+    }
+}
+
+bool gemm_split(int type) { return type == TY_FP4 || type == TY_FAST; }
+
+int gemm_split_k_multiple() { return GS_K; }
+
+int gemm_rows_per_wg(int type) { return gemm_split(type) ? GS_N : GB_N; }
+
+hipError_t launch_act_split(int type, const int8_t *q, const float *d, int T, int K, int rows, _Float16 *xh,
+                            _Float16 *xl, float *ts, hipStream_t stream) {
+    hipLaunchKernelGGL(k_act_split, dim3((unsigned)rows), dim3(256), 0, stream, q, d, T, K,
+                       (type == TY_FP4 || type == TY_FAST) ? 1 : 0, xh, xl, ts);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_split(int type, const GemmArgs &a, dim3 grid, hipStream_t stream) {
+    switch (type) {
+    case TY_FP4: hipLaunchKernelGGL(k_gemm_split<TY_FP4>, grid, dim3(G_THREADS), 0, stream, a); break;
+    case TY_FAST: hipLaunchKernelGGL(k_gemm_split<TY_FAST>, grid, dim3(G_THREADS), 0, stream, a); break;
+    default: return hipErrorInvalidDeviceFunction;
+    }
+    return hipGetLastError();
+}
+
 }  // namespace pq

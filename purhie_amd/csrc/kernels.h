@@ -68,8 +68,10 @@ hipError_t launch_block_dots(int type, const uint8_t *W, long long row_bytes, co
 struct GemmArgs {
     const uint8_t *W;       // dense: the matrix; MoE: stacked experts
     long long row_bytes;
-    const _Float16 *xh;     // token operand [rows][K] (pre-pass)
-    const float *dx;        // block scales [rows][K / 32]
+    const _Float16 *xh;     // token operand [rows][K] (pre-pass); split GEMM: the hi plane
+    const float *dx;        // block scales [rows][K / 32] (per-block GEMM)
+    const _Float16 *xl;     // split GEMM: the lo plane [rows][K]
+    const float *ts;        // split GEMM: per-row output factor 2^-s
     float *y;
     long long ldy;
     int N, K, T, zero_row;
@@ -85,6 +87,13 @@ int gemm_token_tile();
 hipError_t launch_act_f16(int type, const int8_t *q, const float *d, int T, int K, int Tpad, _Float16 *xh, float *dxp,
                           hipStream_t stream);
 hipError_t launch_gemm(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);
+// the split-activation GEMM (ROCmFP4, FAST): pre-pass of `rows` rows (T real, the rest zero) and the kernel
+bool gemm_split(int type);
+int gemm_split_k_multiple();
+int gemm_rows_per_wg(int type);  // weight rows per GEMM workgroup (token tiles: gemm_token_tile())
+hipError_t launch_act_split(int type, const int8_t *q, const float *d, int T, int K, int rows, _Float16 *xh,
+                            _Float16 *xl, float *ts, hipStream_t stream);
+hipError_t launch_gemm_split(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);
 
 // lanes per row the decode kernels use for a matrix of K columns and `rows` rows in total
 int matvec_lanes(int type, int K, long long rows);

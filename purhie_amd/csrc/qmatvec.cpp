@@ -83,35 +83,54 @@ int gemm_min_t() {
 
 size_t align16z(size_t n) { return (n + 15) & ~(size_t)15; }
 
-// The GEMM's token operand: rows of q as fp16 in the weight type's K order plus the block scales, in a
-// stream-ordered allocation (freed on the same stream after the GEMM).
+// The GEMM's token operand in a stream-ordered allocation (freed on the same stream after the GEMM): for
+// ROCmFP4 / FAST the split planes hi, lo (fp16) and the per-row factors; for Q8_0 the int8 rows as fp16 and
+// their block scales. `rows` rows are converted (the first T from q, the rest zero: padding and the zero
+// row MoE tiles point past their entries).
 struct TokWs {
     void *mem = nullptr;
-    _Float16 *xh = nullptr;
-    float *dx = nullptr;
+    _Float16 *xh = nullptr, *xl = nullptr;
+    float *dx = nullptr, *ts = nullptr;
 };
 
-hipError_t tokens_to_f16(int type, const qmatvec_q8 *q, int rows, int K, int Tpad, TokWs &w, hipStream_t stream) {
-    const size_t xb = align16z((size_t)(Tpad + 1) * K * 2), db = (size_t)(Tpad + 1) * (K / 32) * 4;
-    hipError_t e = hipMallocAsync(&w.mem, xb + db, stream);
+hipError_t tokens_prep(int type, const qmatvec_q8 *q, int T, int K, int rows, TokWs &w, hipStream_t stream) {
+    const size_t plane = align16z((size_t)rows * K * 2);
+    if (gemm_split(type)) {
+        hipError_t e = hipMallocAsync(&w.mem, 2 * plane + (size_t)rows * 4, stream);
+        if (e != hipSuccess) return e;
+        w.xh = (_Float16 *)w.mem;
+        w.xl = (_Float16 *)((char *)w.mem + plane);
+        w.ts = (float *)((char *)w.mem + 2 * plane);
+        return launch_act_split(type, q->q0, q->d0, T, K, rows, w.xh, w.xl, w.ts, stream);
+    }
+    hipError_t e = hipMallocAsync(&w.mem, plane + (size_t)rows * (K / 32) * 4, stream);
     if (e != hipSuccess) return e;
     w.xh = (_Float16 *)w.mem;
-    w.dx = (float *)((char *)w.mem + xb);
-    return launch_act_f16(type, q->q0, q->d0, rows, K, Tpad, w.xh, w.dx, stream);
+    w.dx = (float *)((char *)w.mem + plane);
+    return launch_act_f16(type, q->q0, q->d0, T, K, rows - 1, w.xh, w.dx, stream);
 }
+
+hipError_t gemm_launch(int type, const GemmArgs &a, dim3 grid, hipStream_t stream) {
+    return gemm_split(type) ? launch_gemm_split(type, a, grid, stream) : launch_gemm(type, a, grid, stream);
+}
+
+// K multiple the GEMM of a type needs
+int gemm_k_mult(int type) { return gemm_split(type) ? gemm_split_k_multiple() : gemm_k_multiple(); }
 
 hipError_t gemm_dense(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, long long ldy, int N,
                       int K, int T, hipStream_t stream) {
     const int BT = gemm_token_tile();
     const int Tpad = (T + BT - 1) / BT * BT;
     TokWs w;
-    hipError_t e = tokens_to_f16(type, q, T, K, Tpad, w, stream);
+    hipError_t e = tokens_prep(type, q, T, K, Tpad + 1, w, stream);
     if (e == hipSuccess) {
         GemmArgs a{};
         a.W = (const uint8_t *)W;
         a.row_bytes = (long long)row_bytes;
         a.xh = w.xh;
         a.dx = w.dx;
+        a.xl = w.xl;
+        a.ts = w.ts;
         a.y = y;
         a.ldy = ldy;
         a.N = N;
@@ -119,7 +138,8 @@ hipError_t gemm_dense(int type, const void *W, size_t row_bytes, const qmatvec_q
         a.T = T;
         a.zero_row = Tpad;
         a.osc = dense_scale(W);
-        e = launch_gemm(type, a, dim3((unsigned)(Tpad / BT), (unsigned)((N + 127) / 128)), stream);
+        const int RN = gemm_rows_per_wg(type);
+        e = gemm_launch(type, a, dim3((unsigned)(Tpad / BT), (unsigned)((N + RN - 1) / RN)), stream);
     }
     if (w.mem) {
         const hipError_t f = hipFreeAsync(w.mem, stream);
@@ -317,7 +337,7 @@ hipError_t qmatvec_launch_q8_batch(int type, const void *W, size_t row_bytes, co
         (long long)T * K > q->max_k || ldy < N)
         return hipErrorInvalidValue;
     // prefill mode or a batch of 32+ tokens: the MFMA GEMM (the reference's WMMA threshold, src/qmatvec.cpp:553)
-    if (gemm_supported(type) && K % gemm_k_multiple() == 0 && (g_prefill || T >= gemm_min_t()) && N >= 64)
+    if (gemm_supported(type) && K % gemm_k_mult(type) == 0 && (g_prefill || T >= gemm_min_t()) && N >= 64)
         return gemm_dense(type, W, row_bytes, q, y, ldy, N, K, T, stream);
     // tokens in groups of up to 4 through the decode kernel (weights read once per group)
     MvArgs a{};
@@ -347,7 +367,7 @@ hipError_t qmatvec_launch_q8_batch(int type, const void *W, size_t row_bytes, co
 }
 
 int qmatvec_q8_id_batch_supported(int type, int K) {
-    return qmatvec_q8_supported(type, K) && gemm_supported(type) && K % gemm_k_multiple() == 0;
+    return qmatvec_q8_supported(type, K) && gemm_supported(type) && K % gemm_k_mult(type) == 0;
 }
 
 // the largest tile the expert-tiled GEMM takes: each expert's weights are read once per this many entries
@@ -367,13 +387,15 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
     // every input row the buffer can hold (in_rows index them) goes through the pre-pass; row `rows` is zero
     const int rows = q->max_k / K;
     TokWs w;
-    hipError_t e = tokens_to_f16(type, q, rows, K, rows, w, stream);
+    hipError_t e = tokens_prep(type, q, rows, K, rows + 1, w, stream);
     if (e == hipSuccess) {
         GemmArgs a{};
         a.W = (const uint8_t *)W;
         a.row_bytes = (long long)row_bytes;
         a.xh = w.xh;
         a.dx = w.dx;
+        a.xl = w.xl;
+        a.ts = w.ts;
         a.y = y;
         a.N = N;
         a.K = K;
@@ -390,7 +412,8 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
             if (o.n > 1) a.es = o.s;
             else a.osc = o.s[0];
         }
-        e = launch_gemm(type, a, dim3((unsigned)((N + 127) / 128), (unsigned)max_tiles), stream);
+        const int RN = gemm_rows_per_wg(type);
+        e = gemm_launch(type, a, dim3((unsigned)((N + RN - 1) / RN), (unsigned)max_tiles), stream);
     }
     if (w.mem) {
         const hipError_t f = hipFreeAsync(w.mem, stream);
