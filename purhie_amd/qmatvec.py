@@ -87,6 +87,15 @@ def lib():
             "qt_to_float_device": (i32, [i32, vp, vp, i64, vp]),
             "qt_vec_dot_q8k": (i32, [i32]),
             "qt_fp16_to_fp32": (C.c_float, [C.c_uint16]),
+            "qz_supported": (i32, [i32]),
+            "qz_quantize": (i32, [i32, vp, i32, vp, i64, i64, i32, C.c_char_p, sz]),
+            "qz_quantize_im": (i32, [i32, vp, i32, vp, i64, i64, vp, i32, C.c_char_p, sz]),
+            "qz_quantize_device": (i32, [i32, vp, vp, i64, i64, vp]),
+            "qz_row_q8_0": (None, [vp, vp, i64]),
+            "qz_row_rocmfp4": (None, [vp, vp, i64]),
+            "qz_row_rocmfp4_fast": (None, [vp, vp, i64]),
+            "qz_fp32_to_fp16": (C.c_uint16, [C.c_float]),
+            "qz_fp32_to_bf16": (C.c_uint16, [C.c_float]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name, None)
@@ -191,3 +200,21 @@ def to_float_host(t, src, n):
     if rc != 0:
         raise RuntimeError(f"qt_to_float({t}) failed")
     return out
+
+
+def encode(t, src, ncols, src_type=QT_F32):
+    """qz_quantize: host rows (src_type; fp32 by default) -> host bytes of type t, [rows][row_size(t, ncols)]"""
+    src = np.ascontiguousarray(src)
+    nrows = src.nbytes // row_size(src_type, ncols) if src_type != QT_F32 else src.size // ncols
+    out = np.zeros((nrows, row_size(t, ncols)), dtype=np.uint8)
+    err = C.create_string_buffer(256)
+    rc = lib().qz_quantize(t, out.ctypes.data_as(C.c_void_p), src_type, src.ctypes.data_as(C.c_void_p), nrows, ncols,
+                           0, err, 256)
+    if rc != 0:
+        raise RuntimeError(err.value.decode())
+    return out
+
+
+def encode_device(t, src, dst, nrows, ncols, stream=None):
+    """qz_quantize_device: fp32 rows in device memory -> type t rows in device memory"""
+    _check("qz_quantize_device", lib().qz_quantize_device(t, _p(dst), _p(src), nrows, ncols, stream))
