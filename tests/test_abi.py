@@ -36,7 +36,8 @@ def test_headers_declare_the_reference_surface():
               "qmatvec_launch_q8_batch", "qmatvec_launch_q8_id_x", "qmatvec_launch_q8_id_batch", "qt_row_size",
               "qt_to_float", "qt_get_traits", "gpu_swiglu", "gpu_moe_router", "gpu_moe_combine",
               "gpu_moe_combine_scaled", "gpu_moe_group", "qz_supported", "qz_quantize", "qz_quantize_im",
-              "qz_row_q8_0", "qz_row_rocmfp4", "qz_row_rocmfp4_fast", "qz_fp32_to_fp16", "qz_fp32_to_bf16"):
+              "qz_row_q8_0", "qz_row_rocmfp4", "qz_row_rocmfp4_fast", "qz_fp32_to_fp16", "qz_fp32_to_bf16",
+              "gemm_act_fp4_launch"):
         assert n in names, n
 
 
