@@ -130,4 +130,12 @@ struct IdRows {
     __device__ void store(int row, int, float v) const { y[row] = v * sc; }
 };
 
+// Token rows of a GEMM tile: dense tiles take rows base .. base + tile - 1 of the pre-pass output; MoE tiles take
+// their entries' input rows, and the zero row past the last entry
+struct TokMap {
+    const int32_t *rows;  // MoE: in_rows + tile_start (null: dense)
+    int base, n, zero_row;
+    __device__ int row(int j) const { return rows ? (j < n ? rows[j] : zero_row) : base + j; }
+};
+
 }  // namespace pq

@@ -223,13 +223,6 @@ struct GStage<TY_Q8_0> {
     }
 };
 
-// ---------------------------------------------------------------- token rows of a tile
-struct TokMap {
-    const int32_t *rows;  // MoE: in_rows + tile_start (null: dense)
-    int base, n, zero_row;
-    __device__ int row(int j) const { return rows ? (j < n ? rows[j] : zero_row) : base + j; }
-};
-
 
 template <int TYPE>
 __global__ void __launch_bounds__(G_THREADS, 2) k_gemm(GemmArgs a) {
@@ -375,7 +368,9 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm(GemmArgs a) {
 
 // ---------------------------------------------------------------- host launchers
 
-int gemm_supported(int type) { return type == TY_FP4 || type == TY_FAST || type == TY_Q8_0; }
+int gemm_supported(int type) {
+    return type == TY_FP4 || type == TY_FAST || type == TY_Q8_0 || type == TY_Q4_K || type == TY_Q6_K;
+}
 
 int gemm_k_multiple() { return GB_K; }
 
@@ -631,7 +626,7 @@ bool gemm_split(int type) { return type == TY_FP4 || type == TY_FAST; }
 
 int gemm_split_k_multiple() { return GS_K; }
 
-int gemm_rows_per_wg(int type) { return gemm_split(type) ? GS_N : GB_N; }
+int gemm_rows_per_wg(int type) { return gemm_split(type) ? GS_N : gemm_kquant(type) ? GEMM_KQ_ROWS : GB_N; }
 
 hipError_t launch_act_split(int type, const int8_t *q, const float *d, int T, int K, int rows, _Float16 *xh,
                             _Float16 *xl, float *ts, hipStream_t stream) {

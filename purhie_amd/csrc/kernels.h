@@ -72,6 +72,7 @@ struct GemmArgs {
     const float *dx;        // block scales [rows][K / 32] (per-block GEMM)
     const _Float16 *xl;     // split GEMM: the lo plane [rows][K]
     const float *ts;        // split GEMM: per-row output factor 2^-s
+    const _Float16 *xb;     // K-quant GEMM: the token's 16-value group sums [rows][K / 16] (dx: dK [rows][K / 256])
     float *y;
     long long ldy;
     int N, K, T, zero_row;
@@ -94,6 +95,12 @@ int gemm_rows_per_wg(int type);  // weight rows per GEMM workgroup (token tiles:
 hipError_t launch_act_split(int type, const int8_t *q, const float *d, int T, int K, int rows, _Float16 *xh,
                             _Float16 *xl, float *ts, hipStream_t stream);
 hipError_t launch_gemm_split(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);
+// the K-quant GEMM (Q4_K, Q6_K): pre-pass of the Q8_K activation (`rows` rows, T real) and the kernel
+bool gemm_kquant(int type);
+constexpr int GEMM_KQ_ROWS = 128;  // weight rows per K-quant GEMM workgroup
+hipError_t launch_act_q8k(const int8_t *q, const float *dK, const int32_t *bs, int T, int K, int rows, _Float16 *xh,
+                          _Float16 *xb, float *xd, hipStream_t stream);
+hipError_t launch_gemm_kquant(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);
 
 // lanes per row the decode kernels use for a matrix of K columns and `rows` rows in total
 int matvec_lanes(int type, int K, long long rows);

@@ -85,16 +85,25 @@ size_t align16z(size_t n) { return (n + 15) & ~(size_t)15; }
 
 // The GEMM's token operand in a stream-ordered allocation (freed on the same stream after the GEMM): for
 // ROCmFP4 / FAST the split planes hi, lo (fp16) and the per-row factors; for Q8_0 the int8 rows as fp16 and
-// their block scales. `rows` rows are converted (the first T from q, the rest zero: padding and the zero
-// row MoE tiles point past their entries).
+// their block scales; for Q4_K / Q6_K the Q8_K rows as fp16, their group sums as fp16 and dK. `rows` rows are
+// converted (the first T from q, the rest zero: padding and the zero row MoE tiles point past their entries).
 struct TokWs {
     void *mem = nullptr;
-    _Float16 *xh = nullptr, *xl = nullptr;
+    _Float16 *xh = nullptr, *xl = nullptr, *xb = nullptr;
     float *dx = nullptr, *ts = nullptr;
 };
 
 hipError_t tokens_prep(int type, const qmatvec_q8 *q, int T, int K, int rows, TokWs &w, hipStream_t stream) {
     const size_t plane = align16z((size_t)rows * K * 2);
+    if (gemm_kquant(type)) {
+        const size_t sums = align16z((size_t)rows * (K / 16) * 2);
+        hipError_t e = hipMallocAsync(&w.mem, plane + sums + (size_t)rows * (K / 256) * 4, stream);
+        if (e != hipSuccess) return e;
+        w.xh = (_Float16 *)w.mem;
+        w.xb = (_Float16 *)((char *)w.mem + plane);
+        w.dx = (float *)((char *)w.mem + plane + sums);
+        return launch_act_q8k(q->qK, q->dK, q->bsK, T, K, rows, w.xh, w.xb, w.dx, stream);
+    }
     if (gemm_split(type)) {
         hipError_t e = hipMallocAsync(&w.mem, 2 * plane + (size_t)rows * 4, stream);
         if (e != hipSuccess) return e;
@@ -111,11 +120,14 @@ hipError_t tokens_prep(int type, const qmatvec_q8 *q, int T, int K, int rows, To
 }
 
 hipError_t gemm_launch(int type, const GemmArgs &a, dim3 grid, hipStream_t stream) {
+    if (gemm_kquant(type)) return launch_gemm_kquant(type, a, grid, stream);
     return gemm_split(type) ? launch_gemm_split(type, a, grid, stream) : launch_gemm(type, a, grid, stream);
 }
 
 // K multiple the GEMM of a type needs
-int gemm_k_mult(int type) { return gemm_split(type) ? gemm_split_k_multiple() : gemm_k_multiple(); }
+int gemm_k_mult(int type) {
+    return gemm_kquant(type) ? 256 : gemm_split(type) ? gemm_split_k_multiple() : gemm_k_multiple();
+}
 
 hipError_t gemm_dense(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, long long ldy, int N,
                       int K, int T, hipStream_t stream) {
@@ -130,6 +142,7 @@ hipError_t gemm_dense(int type, const void *W, size_t row_bytes, const qmatvec_q
         a.xh = w.xh;
         a.dx = w.dx;
         a.xl = w.xl;
+        a.xb = w.xb;
         a.ts = w.ts;
         a.y = y;
         a.ldy = ldy;
@@ -395,6 +408,7 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
         a.xh = w.xh;
         a.dx = w.dx;
         a.xl = w.xl;
+        a.xb = w.xb;
         a.ts = w.ts;
         a.y = y;
         a.N = N;

@@ -9,7 +9,7 @@ from purhie_amd import synth
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
-GEMM_TYPES = (100, 101, 8)
+GEMM_TYPES = (100, 101, 8, 12, 14)
 
 
 @pytest.fixture(scope="module")
@@ -85,10 +85,11 @@ def test_gemm_ldy_and_split_invariance(Q, oracle, t):
     check_tokens(oracle, t, W, N, K, x[:3], full[:3])
 
 
-@pytest.mark.parametrize("t,N,K", [(100, 768, 2048), (100, 2048, 768), (8, 512, 1024), (101, 256, 1024)])
+@pytest.mark.parametrize("t,N,K", [(100, 768, 2048), (100, 2048, 768), (8, 512, 1024), (101, 256, 1024),
+                                   (12, 768, 2048), (14, 2048, 768), (12, 200, 512)])
 def test_moe_tiled_gemm(Q, oracle, t, N, K):
-    """expert tiles from the grouping (config 4 shapes): entry i of tile k multiplies input row in_rows[i] by
-    expert tile_e[k] into output row out_rows[i]"""
+    """expert tiles from the grouping (config 4 shapes, and K-quant experts): entry i of tile k multiplies input
+    row in_rows[i] by expert tile_e[k] into output row out_rows[i]"""
     import torch
     E, n_used, T = 16, 4, 48
     W = oracle.quantize(t, synth.gaussian(9, E * N * K, 0, 0.02).reshape(E * N, K))
