@@ -3,7 +3,8 @@ construction (tests/actfp4_verify.cpp:30-100: an LCG from 55, A uniform in [-2, 
 UE4M3 scale bytes whose fp4_common.h value lies in [0.1, 1]) against the oracle's double-precision restatement
 of the same products: fp32 accumulation keeps the error near 1e-6 of sum |a w| (the reference's GPU rounds each
 16-value partial sum to fp16 and is tested at rtol 0.01, atol 0.01 sqrt(K)); and the float-scale (Q4_1 layout)
-path against a numpy restatement. The oracle part is parity-unpinned: the reference checks it on a GPU only."""
+path against a numpy restatement. The oracle's restatement is pinned on the CPU (test_oracle.py:
+test_gemm_act_fp4_closed_forms: numpy matmul of an independently decoded weight, and closed forms)."""
 import ctypes as C
 
 import numpy as np

@@ -127,6 +127,47 @@ def test_ue4m3_decoders(oracle):
     assert L.orc_ue4m3_fp4common(0x7F) == 120.0 and L.orc_ue4m3_fp4common(0xFF) == 120.0
 
 
+def test_gemm_act_fp4_closed_forms(oracle):
+    """orc_gemm_act_fp4 (the restatement of src/gemm_act_fp4.hip:27-157) against numpy's matmul of an
+    independently decoded weight: W[n] packs value k in byte k / 2, even k in the low nibble
+    (tests/actfp4_verify.cpp:86), one fp4_common.h scale byte per 16 values of a row. Non-square shapes so
+    that a transposed operand fails; rows of one code and one scale reduce to a scaled row sum of A; a weight
+    with only even-k codes fails a nibble swap."""
+    L = oracle.lib()
+    cb = np.array([0, 1, 2, 3, 4, 6, 8, 10, 0, -1, -2, -3, -4, -6, -8, -10], np.float64)
+    sval = np.array([L.orc_ue4m3_fp4common(e) for e in range(256)], np.float64)  # pinned in test_ue4m3_decoders
+
+    def f16(x):
+        return np.asarray(x, np.float64).astype(np.float16).astype(np.float64)
+
+    def want(A16, W, Ws, M, N, K):
+        nib = np.empty((N, K), np.int64)
+        nib[:, 0::2] = W & 15
+        nib[:, 1::2] = W >> 4
+        wd = f16(cb[nib] * np.repeat(sval[Ws], 16, axis=1))  # the reference rounds each weight to fp16
+        return A16.astype(np.float64) @ wd.T
+
+    rng = np.random.default_rng(7)
+    for M, N, K in ((3, 5, 32), (7, 2, 64), (1, 9, 16)):
+        A16 = rng.uniform(-2, 2, (M, K)).astype(np.float16)
+        W = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+        Ws = rng.integers(0x08, 0x78, (N, K // 16), dtype=np.uint8)
+        got = oracle.gemm_act_fp4(A16.view(np.uint16), W, Ws, M, N, K)
+        assert got.shape == (M, N)
+        np.testing.assert_allclose(got, want(A16, W, Ws, M, N, K), rtol=1e-6, atol=1e-6)
+    # one code (1, both nibbles) and one scale per row: C[m][n] = s_n * sum_k A[m][k]
+    M, N, K = 4, 3, 48
+    A16 = rng.uniform(-2, 2, (M, K)).astype(np.float16)
+    Ws = np.repeat(np.array([[0x38], [0x41], [0x2B]], np.uint8), K // 16, axis=1)
+    got = oracle.gemm_act_fp4(A16.view(np.uint16), np.full((N, K // 2), 0x11, np.uint8), Ws, M, N, K)
+    ref = A16.astype(np.float64).sum(axis=1)[:, None] * f16(sval[Ws[:, 0]])[None, :]
+    np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-6)
+    # codes only in the low nibbles: only the even-k columns of A count
+    got = oracle.gemm_act_fp4(A16.view(np.uint16), np.full((N, K // 2), 0x01, np.uint8), Ws, M, N, K)
+    ref = A16[:, 0::2].astype(np.float64).sum(axis=1)[:, None] * f16(sval[Ws[:, 0]])[None, :]
+    np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-6)
+
+
 def test_kat_q8_0_block(oracle):
     """t/95-quantize.t:28-32: x = i - 15, values scaled by 127 / max, rounded half away from zero"""
     x = (np.arange(32, dtype=np.float32) - 15).reshape(1, 32)
