@@ -130,6 +130,33 @@ struct IdRows {
     __device__ void store(int row, int, float v) const { y[row] = v * sc; }
 };
 
+// The entry a block of an expert-indexed launch computes. ids mode: grid.y = slot + n_used * matrix, grid.z =
+// token t; the expert is ids[t * n_used + slot] (-1: the matrix Wx), the input row t (or t * n_used + slot with
+// x_per_slot), the output row t * n_used + slot. Tiles mode (n_tiles set): grid.y = entry i, grid.z = tile k of
+// moe_group's expert tiles; false for the blocks past the last entry (uniform over the block).
+struct IdEntry {
+    int m, e;
+    long long in_row, out_row;
+};
+__device__ __forceinline__ bool id_entry(const MvIdArgs &a, IdEntry &o) {
+    if (a.n_tiles) {
+        const int i = blockIdx.y, k = blockIdx.z;
+        if (k >= *a.n_tiles || i >= a.tile_n[k]) return false;
+        const int st = a.tile_start[k] + i;
+        o.m = 0;
+        o.e = a.tile_e[k];
+        o.in_row = a.in_rows[st];
+        o.out_row = a.out_rows[st];
+        return true;
+    }
+    o.m = (int)blockIdx.y >= a.n_used ? 1 : 0;
+    const int slot = (int)blockIdx.y - o.m * a.n_used, t = blockIdx.z;
+    o.e = a.ids[t * a.n_used + slot];
+    o.out_row = (long long)t * a.n_used + slot;
+    o.in_row = a.x_per_slot ? o.out_row : t;
+    return true;
+}
+
 // Token rows of a GEMM tile: dense tiles take rows base .. base + tile - 1 of the pre-pass output; MoE tiles take
 // their entries' input rows, and the zero row past the last entry
 struct TokMap {

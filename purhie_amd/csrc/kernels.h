@@ -51,6 +51,10 @@ struct MvIdArgs {
     const float *d;
     const int32_t *bs;
     int n_used, x_per_slot, N, K, L, nmat, T;
+    // tiles mode (n_tiles set; nmat 1, grid.y = entry i of a tile, grid.z = tile k): entry i of tile k (i <
+    // tile_n[k]) multiplies input row in_rows[tile_start[k] + i] by expert tile_e[k] into output row out_rows[..]
+    const int32_t *n_tiles, *tile_e, *tile_start, *tile_n, *in_rows, *out_rows;
+    int tile, max_tiles;
 };
 hipError_t launch_matvec_id(int type, const MvIdArgs &a, hipStream_t stream);
 

@@ -479,11 +479,10 @@ template <int TYPE, int L>
 __global__ void __launch_bounds__(MV_THREADS) k_matvec_id(MvIdArgs a) {
     const int lane = threadIdx.x & 63, gl = lane & (L - 1);
     const int row = (blockIdx.x * (MV_THREADS / 64) + (threadIdx.x >> 6)) * (64 / L) + lane / L;
-    if (row >= a.N) return;
-    const int m = (int)blockIdx.y >= a.n_used ? 1 : 0;
-    const int slot = (int)blockIdx.y - m * a.n_used, t = blockIdx.z;
-    const int e = a.ids[t * a.n_used + slot];
-    const long long in_row = a.x_per_slot ? (long long)t * a.n_used + slot : t;
+    IdEntry en;
+    if (row >= a.N || !id_entry(a, en)) return;
+    const int m = en.m, e = en.e;
+    const long long in_row = en.in_row;
     const int K = a.K;
     const int kb = K / act_blk<TYPE>();
     const uint8_t *wr = e >= 0 ? a.W[m] + ((long long)e * a.N + row) * a.row_bytes : a.Wx[m] + (long long)row * a.row_bytes;
@@ -493,7 +492,7 @@ __global__ void __launch_bounds__(MV_THREADS) k_matvec_id(MvIdArgs a) {
     row_sum<TYPE, 1, L>(wr, K, gl, x, acc);
     const float v = group_sum(acc[0], L);
     const float sc = e < 0 ? a.sx[m] : a.es[m] ? a.es[m][e] : a.s[m];
-    if (gl == 0) a.y[m][((long long)t * a.n_used + slot) * a.N + row] = v * sc;
+    if (gl == 0) a.y[m][en.out_row * a.N + row] = v * sc;
 }
 
 // ---------------------------------------------------------------- per-group integer dots (test hook)
@@ -620,7 +619,9 @@ hipError_t launch_matvec(int type, const MvArgs &a, hipStream_t stream) {
 template <int TYPE, int L>
 static hipError_t launch_id_tl(const MvIdArgs &a, hipStream_t stream) {
     const int rows_per_wg = (MV_THREADS / 64) * (64 / L);
-    const dim3 grid((unsigned)((a.N + rows_per_wg - 1) / rows_per_wg), (unsigned)(a.n_used * a.nmat), (unsigned)a.T);
+    const unsigned gx = (unsigned)((a.N + rows_per_wg - 1) / rows_per_wg);
+    const dim3 grid = a.n_tiles ? dim3(gx, (unsigned)a.tile, (unsigned)a.max_tiles)
+                                : dim3(gx, (unsigned)(a.n_used * a.nmat), (unsigned)a.T);
     hipLaunchKernelGGL((k_matvec_id<TYPE, L>), grid, dim3(MV_THREADS), 0, stream, a);
     return hipGetLastError();
 }

@@ -520,18 +520,18 @@ __global__ void __launch_bounds__(TL_THREADS) k_mv_tile(MvArgs a, TileArgs ta) {
     tile_body<TYPE, NT>(smem, rows, row0, nr, a.K, ta.nb, ta.lg, a.q, a.d, a.bs);
 }
 
-// MoE: grid (tiles, n_used * nmat, T); slot j of token t uses expert ids[t * n_used + j] (-1: Wx)
+// MoE: grid (tiles, n_used * nmat, T); slot j of token t uses expert ids[t * n_used + j] (-1: Wx). Tiles mode:
+// grid (tiles, tile, max_tiles) over moe_group's expert tiles, one entry per block.
 template <int TYPE>
 __global__ void __launch_bounds__(TL_THREADS) k_mv_tile_id(MvIdArgs a, TileArgs ta) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int m = (int)blockIdx.y >= a.n_used ? 1 : 0;
-    const int slot = (int)blockIdx.y - m * a.n_used, t = blockIdx.z;
-    const int e = a.ids[t * a.n_used + slot];
-    const long long in_row = a.x_per_slot ? (long long)t * a.n_used + slot : t;
+    IdEntry en;
+    if (!id_entry(a, en)) return;  // (uniform: before any barrier)
+    const int m = en.m, e = en.e;
+    const long long in_row = en.in_row;
     const int K = a.K;
     const IdRows rows{e >= 0 ? a.W[m] + (long long)e * a.N * a.row_bytes : a.Wx[m], a.row_bytes,
-                      a.y[m] + ((long long)t * a.n_used + slot) * a.N,
-                      e < 0 ? a.sx[m] : a.es[m] ? a.es[m][e] : a.s[m]};
+                      a.y[m] + en.out_row * a.N, e < 0 ? a.sx[m] : a.es[m] ? a.es[m][e] : a.s[m]};
     const int row0 = (int)blockIdx.x * ta.R;
     const int nr = a.N - row0 < ta.R ? a.N - row0 : ta.R;
     tile_body<TYPE, 1>(smem, rows, row0, nr, K, ta.nb, ta.lg, a.q + in_row * K, a.d + in_row * (K / Tu<TYPE>::ACT),
@@ -607,7 +607,9 @@ static hipError_t tile_id(const MvIdArgs &a, hipStream_t stream) {
     const uint8_t *W[4] = {a.W[0], a.Wx[0], a.nmat > 1 ? a.W[1] : nullptr, a.nmat > 1 ? a.Wx[1] : nullptr};
     if (!tile_takes<TYPE>(a.K, 1, W, 4, a.row_bytes, a.q, a.d, a.bs)) return hipErrorNotSupported;
     const TileArgs ta = tile_args(a.K / Tu<TYPE>::VALS);
-    const dim3 grid((unsigned)((a.N + ta.R - 1) / ta.R), (unsigned)(a.n_used * a.nmat), (unsigned)a.T);
+    const unsigned gx = (unsigned)((a.N + ta.R - 1) / ta.R);
+    const dim3 grid = a.n_tiles ? dim3(gx, (unsigned)a.tile, (unsigned)a.max_tiles)
+                                : dim3(gx, (unsigned)(a.n_used * a.nmat), (unsigned)a.T);
     const size_t lds = (size_t)TileLds<TYPE>(a.K, 1).bytes;
     hipLaunchKernelGGL((k_mv_tile_id<TYPE>), grid, dim3(TL_THREADS), lds, stream, a, ta);
     return hipGetLastError();

@@ -81,6 +81,18 @@ int gemm_min_t() {
     return v;
 }
 
+// The MFMA GEMMs are on unless QMATVEC_NO_WMMA / QMATVEC_NO_WMMA_MM is set (read once, the reference's A/B switch,
+// src/qmatvec.cpp:149) or prefill-fp32 mode is on (src/qmatvec.cpp:49-52: prefill rows summed like the token by
+// token decoding's). Off, batches and expert tiles run through the decode kernels, one token / entry at a time
+// in the decode order.
+bool mfma_on() {
+    static const bool env = getenv("QMATVEC_NO_WMMA") == nullptr && getenv("QMATVEC_NO_WMMA_MM") == nullptr;
+    return env && !g_prefill_fp32;
+}
+
+// expert tiles in the decode order: the tile the engine's grouping may use there (the reference's QMV_MM_TB)
+constexpr int ID_DECODE_TILE = 16;
+
 size_t align16z(size_t n) { return (n + 15) & ~(size_t)15; }
 
 // The GEMM's token operand in a stream-ordered allocation (freed on the same stream after the GEMM): for
@@ -350,7 +362,8 @@ hipError_t qmatvec_launch_q8_batch(int type, const void *W, size_t row_bytes, co
         (long long)T * K > q->max_k || ldy < N)
         return hipErrorInvalidValue;
     // prefill mode or a batch of 32+ tokens: the MFMA GEMM (the reference's WMMA threshold, src/qmatvec.cpp:553)
-    if (gemm_supported(type) && K % gemm_k_mult(type) == 0 && (g_prefill || T >= gemm_min_t()) && N >= 64)
+    if (mfma_on() && gemm_supported(type) && K % gemm_k_mult(type) == 0 && (g_prefill || T >= gemm_min_t()) &&
+        N >= 64)
         return gemm_dense(type, W, row_bytes, q, y, ldy, N, K, T, stream);
     // tokens in groups of up to 4 through the decode kernel (weights read once per group)
     MvArgs a{};
@@ -379,15 +392,15 @@ hipError_t qmatvec_launch_q8_batch(int type, const void *W, size_t row_bytes, co
     return hipSuccess;
 }
 
-int qmatvec_q8_id_batch_supported(int type, int K) {
-    return qmatvec_q8_supported(type, K) && gemm_supported(type) && K % gemm_k_mult(type) == 0;
+int qmatvec_q8_id_batch_supported(int type, int K) { return qmatvec_q8_supported(type, K); }
+
+static bool id_gemm_ok(int type, int N, int K) {
+    return mfma_on() && gemm_supported(type) && K % gemm_k_mult(type) == 0 && N >= 64;
 }
 
-// the largest tile the expert-tiled GEMM takes: each expert's weights are read once per this many entries
-int qmatvec_id_batch_tile(int type, int N, int K) {
-    (void)N;
-    return qmatvec_q8_id_batch_supported(type, K) ? gemm_token_tile() : 16;
-}
+// the largest tile the expert-tiled launch takes: the GEMM reads each expert's weights once per this many
+// entries; the decode-order path takes the reference's 16 (src/qmatvec.cpp:612-615)
+int qmatvec_id_batch_tile(int type, int N, int K) { return id_gemm_ok(type, N, K) ? gemm_token_tile() : ID_DECODE_TILE; }
 
 hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N,
                                       int K, int max_tiles, int tile, const int32_t *n_tiles, const int32_t *tile_e,
@@ -397,6 +410,34 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
     if (!q || max_tiles <= 0 || tile <= 0 || tile > qmatvec_id_batch_tile(type, N, K) || N <= 0 ||
         row_bytes != qt_row_size(type, K) || ((uintptr_t)W & (w_align(type) - 1)) != 0)
         return hipErrorInvalidValue;
+    if (!id_gemm_ok(type, N, K)) {  // the decode kernels, one entry per block
+        MvIdArgs a{};
+        a.W[0] = (const uint8_t *)W;
+        a.y[0] = y;
+        a.s[0] = a.sx[0] = 1.0f;
+        OutScale o;
+        if (find_scale(W, o)) {
+            if (o.n > 1) a.es[0] = o.s;
+            else a.s[0] = o.s[0];
+        }
+        a.row_bytes = (long long)row_bytes;
+        act_ptrs(type, q, a.q, a.d, a.bs);
+        a.N = N;
+        a.K = K;
+        a.T = 1;
+        a.n_used = 1;
+        a.nmat = 1;
+        a.n_tiles = n_tiles;
+        a.tile_e = tile_e;
+        a.tile_start = tile_start;
+        a.tile_n = tile_n;
+        a.in_rows = in_rows;
+        a.out_rows = out_rows;
+        a.tile = tile;
+        a.max_tiles = max_tiles;
+        a.L = matvec_lanes(type, K, (long long)N * tile * max_tiles);
+        return launch_matvec_id(type, a, stream);
+    }
     // every input row the buffer can hold (in_rows index them) goes through the pre-pass; row `rows` is zero
     const int rows = q->max_k / K;
     TokWs w;

@@ -118,6 +118,13 @@ def _p(t):
     return None if t is None else C.c_void_p(t.data_ptr())
 
 
+def _need(t, nbytes, what):
+    """a host-side bound check before a launch: the tensor holds at least nbytes contiguous bytes"""
+    have = t.numel() * t.element_size()
+    if have < nbytes or not t.is_contiguous():
+        raise ValueError(f"{what}: {have} bytes (contiguous: {t.is_contiguous()}), the launch reads or writes {nbytes}")
+
+
 def row_size(t, k):
     return int(lib().qt_row_size(t, k))
 
@@ -157,14 +164,20 @@ class Q8:
 
 
 def quantize(x, K, q, stream=None):
+    _need(x, K * 4, "x")
     _check("qmatvec_quantize", lib().qmatvec_quantize(_p(x), K, q.ref, stream))
 
 
 def launch_q8(t, W, q, y, N, K, stream=None):
+    _need(W, N * row_size(t, K), "W")
+    _need(y, N * 4, "y")
     _check("qmatvec_launch_q8", lib().qmatvec_launch_q8(t, _p(W), row_size(t, K), q.ref, _p(y), N, K, stream))
 
 
 def launch_q8_multi_t(t, Ws, Ns, ys, q, K, T, stream=None):
+    for w, n_, y_ in zip(Ws, Ns, ys):
+        _need(w, n_ * row_size(t, K), "W")
+        _need(y_, T * n_ * 4, "y")
     n = len(Ws)
     wa = (C.c_void_p * n)(*[w.data_ptr() for w in Ws])
     na = (C.c_int * n)(*Ns)
@@ -174,6 +187,8 @@ def launch_q8_multi_t(t, Ws, Ns, ys, q, K, T, stream=None):
 
 
 def launch_q8_batch(t, W, q, y, ldy, N, K, T, stream=None):
+    _need(W, N * row_size(t, K), "W")
+    _need(y, ((T - 1) * ldy + N) * 4, "y")
     _check("qmatvec_launch_q8_batch",
            lib().qmatvec_launch_q8_batch(t, _p(W), row_size(t, K), q.ref, _p(y), ldy, N, K, T, stream))
 

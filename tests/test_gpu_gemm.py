@@ -117,3 +117,81 @@ def test_moe_tiled_gemm(Q, oracle, t, N, K):
         for j in range(n_used):
             want, _, mag = oracle.matvec(t, W.reshape(E, N, rb)[ids[tt, j]], N, K, a)
             assert np.all(np.abs(got[tt * n_used + j] - want) <= TOL * mag)
+
+
+@pytest.fixture(params=["tile", "wave"])
+def kpath(request, monkeypatch):
+    """the decode kernels under test: the one-unit-per-lane tile kernels or the per-wave kernels"""
+    monkeypatch.setenv("PURHIE_MV_TILE", "1" if request.param == "tile" else "0")
+    return request.param
+
+
+@pytest.fixture
+def fp32_mode(Q):
+    """prefill-fp32 mode (qmatvec_set_prefill_fp32, src/qmatvec.cpp:49-52): the MFMA GEMMs off"""
+    Q.lib().qmatvec_set_prefill_fp32(1)
+    yield
+    Q.lib().qmatvec_set_prefill_fp32(0)
+
+
+def single_token(Q, t, Wd, x, N, K):
+    """each token alone through the decode matvec"""
+    import torch
+    out = np.empty((x.shape[0], N), np.float32)
+    q = Q.Q8(((K + 255) // 256) * 256)
+    y = torch.empty(N, dtype=torch.float32, device="cuda")
+    for i in range(x.shape[0]):
+        Q.quantize(dev(x[i]), K, q)
+        Q.launch_q8(t, Wd, q, y, N, K)
+        out[i] = host(y)
+    return out
+
+
+@pytest.mark.parametrize("t", GEMM_TYPES)
+def test_prefill_fp32_mode_decode_order(Q, oracle, kpath, fp32_mode, t):
+    """with the MFMA GEMMs off, a 40-token batch (the GEMM's size otherwise) equals its tokens' single-token
+    decode bit for bit"""
+    N, K, T = 320, 1024, 40
+    W = oracle.quantize(t, synth.gaussian(21, N * K, 0, 0.02).reshape(N, K))
+    Wd = dev(W)
+    x = acts(22, T, K)
+    got = run_batch(Q, t, Wd, x, N, K)
+    want = single_token(Q, t, Wd, x, N, K)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("t,N,K", [(100, 768, 2048), (12, 256, 768), (14, 256, 768), (8, 96, 1024)])
+def test_moe_tiles_decode_order(Q, oracle, kpath, fp32_mode, t, N, K):
+    """with the MFMA GEMMs off, the expert tiles (the reference's tile of 16) run through the decode kernels: every
+    entry equals the single-token decode of its expert bit for bit"""
+    import ctypes as C
+    import torch
+    E, n_used, T = 8, 4, 20
+    rb = Q.row_size(t, K)
+    W = oracle.quantize(t, synth.gaussian(23, E * N * K, 0, 0.02).reshape(E * N, K))
+    Wd = dev(W)
+    ids = (synth.splitmix64(24, T * n_used) % np.uint64(E)).astype(np.int32).reshape(T, n_used)
+    L = Q.lib()
+    tile = L.qmatvec_id_batch_tile(t, N, K)
+    assert tile == 16
+    g = oracle.moe_group(ids, E, tile)
+    x = acts(25, T, K)
+    q = Q.Q8(((T * K + 255) // 256) * 256)
+    Q.quantize(dev(x.reshape(-1)), T * K, q)
+    y = torch.full((T * n_used, N), float("nan"), dtype=torch.float32, device="cuda")
+    p = lambda a: C.c_void_p(a.data_ptr())
+    bufs = [dev(np.array([g["n_tiles"]], np.int32)), dev(g["tile_e"]), dev(g["tile_start"]), dev(g["tile_n"]),
+            dev(g["tok_rows"]), dev(g["pair_rows"])]
+    rc = L.qmatvec_launch_q8_id_batch(t, p(Wd), rb, q.ref, p(y), N, K, g["n_tiles"] + 2, tile,
+                                      *[p(b) for b in bufs], None)
+    assert rc == 0
+    got = host(y)
+    for e in range(E):
+        sel = [(tt, j) for tt in range(T) for j in range(n_used) if ids[tt, j] == e]
+        if not sel:
+            continue
+        We = Wd[e * N:(e + 1) * N]  # expert e's N rows of rb bytes
+        assert We.numel() == N * rb and We.is_contiguous()
+        want = single_token(Q, t, We, x[[tt for tt, _ in sel]], N, K)
+        for r, (tt, j) in enumerate(sel):
+            assert np.array_equal(got[tt * n_used + j].view(np.uint32), want[r].view(np.uint32)), (e, tt, j)
