@@ -5,9 +5,8 @@
 //   k_swiglu       out = SiLU(g) * u (g / (1 + exp(-g)) * u), and, with a qmatvec_q8, quantized in the same
 //                  launch (one 256-thread workgroup per 256-value block: q8dev.h).
 //   k_moe_router   a workgroup per token: softmax of the router logits (exp(l - max) / sum), the n_used
-//                  largest probabilities in descending order by rounds of a wave-wide argmax (equal values:
-//                  the lower expert), their weights divided by max(sum, 2^-14), and the shared-expert gate
-//                  sigmoid(x . w_shexp).
+//                  largest probabilities in descending order (equal values: the lower expert) by each expert's
+//                  rank, their weights divided by max(sum, 2^-14), and the shared-expert gate sigmoid(x . w_shexp).
 //   k_moe_combine  out = sum_j w_j down_j in slot order (+ sg shared), rounded after every product and sum
 //                  (no contraction) as the reference's CPU add chain.
 //   k_moe_group    one 1024-thread workgroup: entries (token, slot) counted per expert in LDS, two exclusive
@@ -59,7 +58,7 @@ __global__ void __launch_bounds__(256) k_moe_router(const float *__restrict__ lo
                                                     const float *__restrict__ w_sh, int *__restrict__ ids,
                                                     float *__restrict__ wts, float *__restrict__ sg, int n_expert,
                                                     int n_used, int n, int ids_stride) {
-    __shared__ float p[MOE_MAX_EXPERTS];
+    __shared__ __attribute__((aligned(16))) float p[MOE_MAX_EXPERTS];
     __shared__ float red[4];
     __shared__ float selw[MOE_MAX_USED];
     const int t = blockIdx.x, tid = threadIdx.x;
@@ -87,44 +86,27 @@ __global__ void __launch_bounds__(256) k_moe_router(const float *__restrict__ lo
     for (int e = tid; e < n_expert; e += 256) p[e] *= inv;
     __syncthreads();
 
-    if (tid < 64) {
-        // wave 0: lane l holds experts l + 64 j; each round takes the largest remaining (the lower expert among
-        // equal values) and its lane drops it
-        constexpr int PL = MOE_MAX_EXPERTS / 64;
-        float v[PL];
-#pragma unroll
-        for (int j = 0; j < PL; ++j) {
-            const int e = tid + 64 * j;
-            v[j] = e < n_expert ? p[e] : -INFINITY;
+    // top n_used by rank: expert e's rank is the number of experts ahead of it, those with a larger probability
+    // or an equal one at a lower index (the order of the reference's rounds of argmax). Every thread ranks its
+    // experts against all of p at once (broadcast LDS reads), so no round waits on another. Ranks are distinct:
+    // the order is total once a NaN probability ranks below every number.
+    const int n4 = (n_expert + 3) & ~3;
+    for (int e = n_expert + tid; e < n4; e += 256) p[e] = -INFINITY;  // (ahead of nothing)
+    __syncthreads();
+    for (int e = tid; e < n_expert; e += 256) {
+        const float pe = p[e];
+        const float v = pe == pe ? pe : -2.0f;
+        int r = 0;
+        for (int f = 0; f < n4; f += 4) {
+            const float4 u = *(const float4 *)(p + f);
+            const float u0 = u.x == u.x ? u.x : -2.0f, u1 = u.y == u.y ? u.y : -2.0f;
+            const float u2 = u.z == u.z ? u.z : -2.0f, u3 = u.w == u.w ? u.w : -2.0f;
+            r += (u0 > v || (u0 == v && f < e)) + (u1 > v || (u1 == v && f + 1 < e)) +
+                 (u2 > v || (u2 == v && f + 2 < e)) + (u3 > v || (u3 == v && f + 3 < e));
         }
-        for (int r = 0; r < n_used; ++r) {
-            float bv = v[0];
-            int bj = 0;
-#pragma unroll
-            for (int j = 1; j < PL; ++j)
-                if (v[j] > bv) {
-                    bv = v[j];
-                    bj = j;
-                }
-            int be = tid + 64 * bj;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                const float ov = __shfl_xor(bv, off, 64);
-                const int oe = __shfl_xor(be, off, 64);
-                if (ov > bv || (ov == bv && oe < be)) {
-                    bv = ov;
-                    be = oe;
-                }
-            }
-            if (tid == 0) {
-                ids[(long long)t * ids_stride + r] = be;
-                selw[r] = bv;
-            }
-            if ((be & 63) == tid) {
-#pragma unroll
-                for (int j = 0; j < PL; ++j)
-                    if (j == (be >> 6)) v[j] = -INFINITY;
-            }
+        if (r < n_used) {
+            ids[(long long)t * ids_stride + r] = e;
+            selw[r] = pe;
         }
     }
     if (tid == n_used && ids_stride > n_used) ids[(long long)t * ids_stride + n_used] = -1;  // the shared slot
