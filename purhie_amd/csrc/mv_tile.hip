@@ -30,8 +30,8 @@
 
 namespace pq {
 
-constexpr int TL_THREADS = 256;
-constexpr int TL_PAD = 272;  // LDS bytes per 256 activation values
+constexpr int TL_THREADS = 256;  // the largest workgroup (64 and 128 threads: smaller tiles, more of them)
+constexpr int TL_PAD = 272;      // LDS bytes per 256 activation values
 
 // the dword at byte offset off (compile-time after unrolling) of the unit's dwords
 template <int N>
@@ -321,7 +321,7 @@ struct TileLds {
     static_assert(REGION >= 4 * 64 * 4, "a region also holds its wave's partials of up to 4 tokens");
     int xt, nd, ns;                                                                     // per token
     int off_d, off_s, off_lut, off_w, bytes;
-    __host__ __device__ TileLds(int K, int NT) {
+    __host__ __device__ TileLds(int K, int NT, int thr) {
         using P = Tu<TYPE>;
         xt = (K + 255) / 256 * TL_PAD;
         nd = K / P::ACT;
@@ -330,7 +330,7 @@ struct TileLds {
         off_s = off_d + ((NT * nd * 4 + 15) & ~15);
         off_lut = off_s + ((NT * ns * 4 + 15) & ~15);
         off_w = off_lut + (P::LUT ? 1024 : 0);
-        bytes = off_w + (TL_THREADS / 64) * REGION;
+        bytes = off_w + (thr / 64) * REGION;
     }
 };
 
@@ -342,7 +342,7 @@ constexpr int TL_QN = 4, TL_DN = 2, TL_SN = 4;  // activation loads a thread hol
 // bs + t K / 16) into LDS. Each thread's first TL_QN value chunks, TL_DN scales and TL_SN group sums are
 // loaded by issue() (before the weights), anything beyond by commit(). Q4_K's 32-value sums are the two
 // 16-value sums added when written (nothing in issue() waits for a load).
-template <int TYPE, int NT>
+template <int TYPE, int NT, int THR>
 struct Stager {
     static constexpr bool PAIR = Tu<TYPE>::SUMS == 32;
     int4 qv[TL_QN];
@@ -359,18 +359,18 @@ struct Stager {
         // can no longer count the loads in flight and waits for all of them, the weights included)
 #pragma unroll
         for (int i = 0; i < TL_QN; ++i) {
-            const int c = tid + i * TL_THREADS;
+            const int c = tid + i * THR;
             qv[i] = *(const int4 *)(q + 16 * (long long)(c < nq ? c : nq - 1));
         }
 #pragma unroll
         for (int i = 0; i < TL_DN; ++i) {
-            const int e = tid + i * TL_THREADS;
+            const int e = tid + i * THR;
             dv[i] = d[e < ndt ? e : ndt - 1];
         }
         if (Tu<TYPE>::SUMS) {
 #pragma unroll
             for (int i = 0; i < TL_SN; ++i) {
-                const int e = tid + i * TL_THREADS;
+                const int e = tid + i * THR;
                 sv[i] = load_s(bs, e < nst ? e : nst - 1);
             }
         }
@@ -392,38 +392,39 @@ struct Stager {
         float *ld = (float *)(smem + L.off_d);
 #pragma unroll
         for (int i = 0; i < TL_QN; ++i) {
-            const int c = tid + i * TL_THREADS;
+            const int c = tid + i * THR;
             if (c < nq) put_q(L, smem, K, c, qv[i]);
         }
 #pragma unroll
         for (int i = 0; i < TL_DN; ++i) {
-            const int e = tid + i * TL_THREADS;
+            const int e = tid + i * THR;
             if (e < ndt) ld[e] = dv[i];
         }
         if (Tu<TYPE>::SUMS) {
 #pragma unroll
             for (int i = 0; i < TL_SN; ++i) {
-                const int e = tid + i * TL_THREADS;
+                const int e = tid + i * THR;
                 if (e < nst) put_s(L, smem, e, sv[i]);
             }
         }
-        for (int c = tid + TL_QN * TL_THREADS; c < nq; c += TL_THREADS) put_q(L, smem, K, c, *(const int4 *)(q + 16 * (long long)c));
-        for (int e = tid + TL_DN * TL_THREADS; e < ndt; e += TL_THREADS) ld[e] = d[e];
+        for (int c = tid + TL_QN * THR; c < nq; c += THR) put_q(L, smem, K, c, *(const int4 *)(q + 16 * (long long)c));
+        for (int e = tid + TL_DN * THR; e < ndt; e += THR) ld[e] = d[e];
         if (Tu<TYPE>::SUMS)
-            for (int e = tid + TL_SN * TL_THREADS; e < nst; e += TL_THREADS) put_s(L, smem, e, load_s(bs, e));
-        if (Tu<TYPE>::LUT) ((float *)(smem + L.off_lut))[tid] = ue4m3_half((uint32_t)tid);
+            for (int e = tid + TL_SN * THR; e < nst; e += THR) put_s(L, smem, e, load_s(bs, e));
+        if (Tu<TYPE>::LUT)
+            for (int e = tid; e < 256; e += THR) ((float *)(smem + L.off_lut))[e] = ue4m3_half((uint32_t)e);
     }
 };
 
-// One tile: rows [row0, row0 + nr) of one matrix (contiguous, nb units each, nr * nb <= 256).
-template <int TYPE, int NT, class Rows>
+// One tile: rows [row0, row0 + nr) of one matrix (contiguous, nb units each, nr * nb <= THR).
+template <int TYPE, int NT, int THR, class Rows>
 __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int row0, int nr, int K, int nb, int lg,
                                           const int8_t *q, const float *d, const int32_t *bs) {
     using P = Tu<TYPE>;
     using TL = TileLds<TYPE>;
-    const TL L(K, NT);
+    const TL L(K, NT, THR);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    Stager<TYPE, NT> st;
+    Stager<TYPE, NT, THR> st;
     st.issue(L, q, d, bs, K);
 
     // this wave's units [64 wave, 64 wave + wu) of the tile: bytes [g, g + wu BYTES), loaded as the 16-byte
@@ -498,17 +499,21 @@ struct TileArgs {
     int R, nb, lg, tp[4];
 };
 
-static TileArgs tile_args(int nb) {
+// R = thr / nb rows a tile. The threads per row's sum, 2^lg, depend on nb alone (the count a 256-thread tile
+// allows), so a row's sum has the same order whatever the workgroup size: floor(thr / nb) 2^lg <= thr still
+// holds for thr = 64 and 128, as floor(256 / nb) >= (256 / thr) floor(thr / nb).
+static TileArgs tile_args(int nb, int thr) {
     TileArgs ta = {};
     ta.nb = nb;
-    ta.R = TL_THREADS / nb;
+    ta.R = thr / nb;
+    const int R256 = TL_THREADS / nb;
     ta.lg = 0;
-    while (ta.lg < 6 && (ta.R << (ta.lg + 1)) <= TL_THREADS) ++ta.lg;
+    while (ta.lg < 6 && (R256 << (ta.lg + 1)) <= TL_THREADS) ++ta.lg;
     return ta;
 }
 
-template <int TYPE, int NT>
-__global__ void __launch_bounds__(TL_THREADS) k_mv_tile(MvArgs a, TileArgs ta) {
+template <int TYPE, int NT, int THR>
+__global__ void __launch_bounds__(THR) k_mv_tile(MvArgs a, TileArgs ta) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const DenseRows rows{a};
     const int bx = (int)blockIdx.x;
@@ -517,13 +522,13 @@ __global__ void __launch_bounds__(TL_THREADS) k_mv_tile(MvArgs a, TileArgs ta) {
     const int row0 = rows.base(m) + (bx - first) * ta.R;
     const int end = DenseRows::pick(m, a.bound[0], a.bound[1], a.bound[2], a.bound[3]);
     const int nr = end - row0 < ta.R ? end - row0 : ta.R;
-    tile_body<TYPE, NT>(smem, rows, row0, nr, a.K, ta.nb, ta.lg, a.q, a.d, a.bs);
+    tile_body<TYPE, NT, THR>(smem, rows, row0, nr, a.K, ta.nb, ta.lg, a.q, a.d, a.bs);
 }
 
 // MoE: grid (tiles, n_used * nmat, T); slot j of token t uses expert ids[t * n_used + j] (-1: Wx). Tiles mode:
 // grid (tiles, tile, max_tiles) over moe_group's expert tiles, one entry per block.
-template <int TYPE>
-__global__ void __launch_bounds__(TL_THREADS) k_mv_tile_id(MvIdArgs a, TileArgs ta) {
+template <int TYPE, int THR>
+__global__ void __launch_bounds__(THR) k_mv_tile_id(MvIdArgs a, TileArgs ta) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     IdEntry en;
     if (!id_entry(a, en)) return;  // (uniform: before any barrier)
@@ -534,7 +539,7 @@ __global__ void __launch_bounds__(TL_THREADS) k_mv_tile_id(MvIdArgs a, TileArgs 
                       a.y[m] + en.out_row * a.N, e < 0 ? a.sx[m] : a.es[m] ? a.es[m][e] : a.s[m]};
     const int row0 = (int)blockIdx.x * ta.R;
     const int nr = a.N - row0 < ta.R ? a.N - row0 : ta.R;
-    tile_body<TYPE, 1>(smem, rows, row0, nr, K, ta.nb, ta.lg, a.q + in_row * K, a.d + in_row * (K / Tu<TYPE>::ACT),
+    tile_body<TYPE, 1, THR>(smem, rows, row0, nr, K, ta.nb, ta.lg, a.q + in_row * K, a.d + in_row * (K / Tu<TYPE>::ACT),
                        a.bs ? a.bs + in_row * (K / 16) : nullptr);
 }
 
@@ -551,7 +556,7 @@ static bool tile_takes(int K, int NT, const uint8_t *const *W, int nW, long long
                        const void *d, const void *bs) {
     using P = Tu<TYPE>;
     if (K <= 0 || K % P::VALS || K / P::VALS > TL_THREADS) return false;
-    if (TileLds<TYPE>(K, NT).bytes > 65536) return false;
+    if (TileLds<TYPE>(K, NT, TL_THREADS).bytes > 65536) return false;
     for (int i = 0; i < nW; ++i)
         if (!aligned(W[i], 16)) return false;
     if (row_bytes % (P::LEAD == 0 ? 16 : P::LEAD == 8 ? 8 : 2)) return false;
@@ -560,12 +565,29 @@ static bool tile_takes(int K, int NT, const uint8_t *const *W, int nW, long long
     return true;
 }
 
-template <int TYPE, int NT>
-static hipError_t tile_dense(const MvArgs &a, hipStream_t stream) {
-    int nW = 1;
-    while (nW < 4 && a.bound[nW - 1] < a.Nt) ++nW;
-    if (!tile_takes<TYPE>(a.K, NT, a.W, nW, a.row_bytes, a.q, a.d, a.bs)) return hipErrorNotSupported;
-    TileArgs ta = tile_args(a.K / Tu<TYPE>::VALS);
+// Workgroup size: 256 threads, halved (down to 64, while a tile still holds a whole row) as long as the launch
+// would have fewer workgroups than the chip has CUs: a small matrix then spreads over more CUs in smaller tiles.
+// (Measured: config 1's 3072 x 1024 Q8_0 matvec gains 12%; launches of 400+ workgroups lose with smaller tiles.)
+// PURHIE_MV_THREADS (read at each launch) fixes it.
+constexpr long long TL_MIN_WG = 256;
+
+static int tile_threads(int nb, long long rows) {
+    if (const char *v = getenv("PURHIE_MV_THREADS")) {
+        const int t = atoi(v);
+        if ((t == 64 || t == 128 || t == 256) && nb <= t) return t;
+    }
+    auto wgs = [&](int t) {
+        const long long R = t / nb;
+        return (rows + R - 1) / R;
+    };
+    int thr = TL_THREADS;
+    while (thr > 64 && nb <= thr / 2 && wgs(thr) < TL_MIN_WG) thr /= 2;
+    return thr;
+}
+
+template <int TYPE, int NT, int THR>
+static hipError_t tile_dense_thr(const MvArgs &a, hipStream_t stream) {
+    TileArgs ta = tile_args(a.K / Tu<TYPE>::VALS, THR);
     int tiles = 0, lo = 0;
     for (int i = 0; i < 4; ++i) {
         const int n = a.bound[i] - lo;
@@ -573,9 +595,21 @@ static hipError_t tile_dense(const MvArgs &a, hipStream_t stream) {
         ta.tp[i] = tiles;
         lo = a.bound[i] > lo ? a.bound[i] : lo;
     }
-    const size_t lds = (size_t)TileLds<TYPE>(a.K, NT).bytes;
-    hipLaunchKernelGGL((k_mv_tile<TYPE, NT>), dim3((unsigned)tiles), dim3(TL_THREADS), lds, stream, a, ta);
+    const size_t lds = (size_t)TileLds<TYPE>(a.K, NT, THR).bytes;
+    hipLaunchKernelGGL((k_mv_tile<TYPE, NT, THR>), dim3((unsigned)tiles), dim3(THR), lds, stream, a, ta);
     return hipGetLastError();
+}
+
+template <int TYPE, int NT>
+static hipError_t tile_dense(const MvArgs &a, hipStream_t stream) {
+    int nW = 1;
+    while (nW < 4 && a.bound[nW - 1] < a.Nt) ++nW;
+    if (!tile_takes<TYPE>(a.K, NT, a.W, nW, a.row_bytes, a.q, a.d, a.bs)) return hipErrorNotSupported;
+    switch (tile_threads(a.K / Tu<TYPE>::VALS, a.Nt)) {
+    case 64: return tile_dense_thr<TYPE, NT, 64>(a, stream);
+    case 128: return tile_dense_thr<TYPE, NT, 128>(a, stream);
+    default: return tile_dense_thr<TYPE, NT, 256>(a, stream);
+    }
 }
 
 template <int TYPE>
@@ -600,19 +634,29 @@ hipError_t launch_matvec_tile(int type, const MvArgs &a, hipStream_t stream) {
     return hipErrorNotSupported;
 }
 
+template <int TYPE, int THR>
+static hipError_t tile_id_thr(const MvIdArgs &a, hipStream_t stream) {
+    const TileArgs ta = tile_args(a.K / Tu<TYPE>::VALS, THR);
+    const unsigned gx = (unsigned)((a.N + ta.R - 1) / ta.R);
+    const dim3 grid = a.n_tiles ? dim3(gx, (unsigned)a.tile, (unsigned)a.max_tiles)
+                                : dim3(gx, (unsigned)(a.n_used * a.nmat), (unsigned)a.T);
+    const size_t lds = (size_t)TileLds<TYPE>(a.K, 1, THR).bytes;
+    hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR>), grid, dim3(THR), lds, stream, a, ta);
+    return hipGetLastError();
+}
+
 template <int TYPE>
 static hipError_t tile_id(const MvIdArgs &a, hipStream_t stream) {
     // (null Wx entries pass the alignment check; a row of activation is K values, K / ACT scales and K / 16
     // sums on from the previous one, which keeps every row as aligned as the first when K % VALS == 0)
     const uint8_t *W[4] = {a.W[0], a.Wx[0], a.nmat > 1 ? a.W[1] : nullptr, a.nmat > 1 ? a.Wx[1] : nullptr};
     if (!tile_takes<TYPE>(a.K, 1, W, 4, a.row_bytes, a.q, a.d, a.bs)) return hipErrorNotSupported;
-    const TileArgs ta = tile_args(a.K / Tu<TYPE>::VALS);
-    const unsigned gx = (unsigned)((a.N + ta.R - 1) / ta.R);
-    const dim3 grid = a.n_tiles ? dim3(gx, (unsigned)a.tile, (unsigned)a.max_tiles)
-                                : dim3(gx, (unsigned)(a.n_used * a.nmat), (unsigned)a.T);
-    const size_t lds = (size_t)TileLds<TYPE>(a.K, 1).bytes;
-    hipLaunchKernelGGL((k_mv_tile_id<TYPE>), grid, dim3(TL_THREADS), lds, stream, a, ta);
-    return hipGetLastError();
+    const long long blocks = a.n_tiles ? (long long)a.tile * a.max_tiles : (long long)a.n_used * a.nmat * a.T;
+    switch (tile_threads(a.K / Tu<TYPE>::VALS, (long long)a.N * blocks)) {
+    case 64: return tile_id_thr<TYPE, 64>(a, stream);
+    case 128: return tile_id_thr<TYPE, 128>(a, stream);
+    default: return tile_id_thr<TYPE, 256>(a, stream);
+    }
 }
 
 hipError_t launch_matvec_id_tile(int type, const MvIdArgs &a, hipStream_t stream) {
