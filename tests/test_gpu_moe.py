@@ -82,7 +82,7 @@ def test_combine_bit_exact(M, oracle, variant):
     assert np.array_equal(host(out).view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("T,n_used,E,tile", [(512, 8, 128, 64), (2427, 8, 256, 64), (1, 8, 128, 16), (37, 4, 16, 5),
+@pytest.mark.parametrize("T,n_used,E,tile", [(512, 8, 128, 64), (1999, 8, 160, 64), (1, 8, 128, 16), (37, 4, 16, 5),
                                              (0, 8, 128, 64)])
 def test_group(M, oracle, T, n_used, E, tile):
     ids = (synth.splitmix64(970 + T, max(T, 1) * n_used) % np.uint64(E)).astype(np.int32)[:T * n_used]
