@@ -566,6 +566,7 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm_split(GemmArgs a) {
         __syncthreads();
         if (k0 + GS_K < a.K) GSPLIT_ISSUE(k0 + GS_K);  // next stage's global loads in flight during the MFMAs
 
+        __builtin_amdgcn_s_setprio(1);  // the MFMA phase ahead of the other workgroup's staging on this SIMD
 #pragma unroll
         for (int b = 0; b < GS_K / 32; ++b) {
             const int kk = b * 32 + 8 * (lane >> 4);
@@ -594,6 +595,7 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm_split(GemmArgs a) {
             __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 64, 0);
         }
+        __builtin_amdgcn_s_setprio(0);
     }
 #undef GSPLIT_ISSUE
 
