@@ -36,6 +36,26 @@ void qmatvec_drop_out_scales(const void *owner);
  * path is the int8 one below) */
 int qmatvec_supported(int type);
 
+/* The float-activation, 16-bit-copy, low-rank, split-Q8_0 and float MoE entries of the reference
+ * (src/qmatvec.h:33-75,145-147,179-199) are outside this path. They are exported so that the engine links
+ * unchanged; their *_supported queries return 0 and the launches return hipErrorInvalidDeviceFunction,
+ * as the reference's do for a kernel its code object lacks. */
+hipError_t qmatvec_launch_bf16f(const void *W, size_t row_bytes, const float *x, float *y, int N, int K, int T,
+                                hipStream_t stream);
+hipError_t qmatvec_launch(int type, const void *W, size_t row_bytes, const float *x, float *y, int N, int K,
+                          hipStream_t stream);
+hipError_t qmatvec_launch_batch(int type, const void *W, size_t row_bytes, const float *x, float *y, int N, int K,
+                                int T, hipStream_t stream);
+hipError_t qmatvec_launch_batch_h(int type, const void *W, size_t row_bytes, const float *x, uint16_t *xh,
+                                  size_t xh_bytes, float *y, int N, int K, int T, hipStream_t stream);
+int qmatvec_half_supported(int type, const void *W, size_t row_bytes, int N, int K, int T);
+hipError_t qmatvec_round_half(int type, const float *x, uint16_t *xh, long long n, hipStream_t stream);
+hipError_t qmatvec_launch_batch_hx(int type, const void *W, size_t row_bytes, const uint16_t *xh, float *y, int N,
+                                   int K, int T, hipStream_t stream);
+int qmatvec_q8_0s_source_supported(int type, int K);
+hipError_t qmatvec_quantize_rows_q8_0(int type, const void *W, size_t row_bytes, int N, int K, int8_t *qs, uint16_t *d,
+                                      hipStream_t stream);
+
 /* replaces src/qmatvec.h:49-54 (mode flags). Prefill mode routes every batch size to the GEMM
  * kernels (so a row's sums do not depend on how the prompt was cut into batches). */
 void qmatvec_set_prefill(int on);
@@ -138,6 +158,21 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
                                       int K, int max_tiles, int tile, const int32_t *n_tiles, const int32_t *tile_e,
                                       const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
                                       const int32_t *out_rows, hipStream_t stream);
+
+/* outside this path (as qmatvec_launch above): the split-Q8_0 LM head, the low-rank and the float MoE entries
+ * (src/qmatvec.h:74-75,145-147,179-180,195-199): *_supported 0, hipErrorInvalidDeviceFunction */
+hipError_t qmatvec_launch_q8_0s(const int8_t *qs, const uint16_t *d, const qmatvec_q8 *q, float *y, int N, int K,
+                                hipStream_t stream);
+int qmatvec_q8_lr_supported(int type, int K);
+hipError_t qmatvec_launch_q8_lr(int type, const void *W, size_t row_bytes, const float *lo, int n, int K, float scale,
+                                float *y, int N, hipStream_t stream);
+hipError_t qmatvec_launch_id(int type, const void *W, size_t row_bytes, const int32_t *ids, int n_used, int x_per_slot,
+                             const float *x, float *y, int N, int K, int T, hipStream_t stream);
+int qmatvec_id_batch_f_supported(int type);
+hipError_t qmatvec_launch_id_batch_f(int type, const void *W, size_t row_bytes, const float *x, float *y, int N, int K,
+                                     int max_tiles, int tile, const int32_t *n_tiles, const int32_t *tile_e,
+                                     const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
+                                     const int32_t *out_rows, hipStream_t stream);
 
 /* No counterpart in the reference: a test hook for the parity tests. The integer dot of every weight
  * scale group (Q8_0 / FAST / Q4_K: 32 values, ROCmFP4 / Q6_K: 16) of every row against the quantized

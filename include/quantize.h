@@ -29,6 +29,14 @@ int qz_quantize(int dst_type, void *dst, int src_type, const void *src, int64_t 
 int qz_quantize_im(int dst_type, void *dst, int src_type, const void *src, int64_t nrows, int64_t ncols,
                    const float *imatrix, int n_threads, char *err, size_t err_len);
 
+/* replaces src/quantize.h:33-38: FP8 e4m3fn rows (host memory) with a float32 scale per block_rows x block_cols
+ * block (scale row r / block_rows of scale_cols values for source row r; src and scale start at a row that starts
+ * a block): value = fp8 * scale, one rounding, then encoded as dst_type. The scale rows the call's rows use must
+ * all be present. Returns 0, or -1 with a message in err. */
+int qz_quantize_fp8_blocks(int dst_type, void *dst, const uint8_t *src, const float *scale, int64_t nrows, int64_t ncols,
+                           int block_rows, int block_cols, int64_t scale_cols, int n_threads, char *err, size_t err_len);
+float qz_fp8_e4m3_to_fp32(uint8_t v);
+
 /* replace src/quantize.h:41-45: one row (host memory) at a time, and the scalar conversions */
 void qz_row_q8_0(const float *x, void *y, int64_t n);
 void qz_row_rocmfp4(const float *x, void *y, int64_t n);

@@ -470,4 +470,50 @@ hipError_t launch_encode(int type, const float *x, uint8_t *y, long long nrows, 
 uint16_t host_f32_to_f16(float f) { return f32_to_f16_bits(f); }
 uint16_t host_f32_to_bf16(float f) { return f32_to_bf16_bits(f); }
 
+// ---------------------------------------------------------------- FP8 (OCP e4m3fn) rows with block scales
+// e4m3fn: sign, 4 exponent bits (bias 7), 3 mantissa bits, no infinities, S.1111.111 NaN: exponent field 0 is
+// m 2^-9, else (8 + m) 2^(e - 10) = 1.m 2^(e - 7) (the reference's qz_fp8_e4m3_to_fp32, src/quantize.cpp:1224-1233)
+__device__ __host__ inline float fp8_e4m3fn(uint32_t v) {
+    const uint32_t e = (v >> 3) & 15u, m = v & 7u;
+    uint32_t bits;
+    if ((v & 0x7fu) == 0x7fu) {
+        bits = 0x7fc00000u;
+    } else if (e == 0) {
+        const float f = (float)m * 0x1p-9f;  // exact
+        __builtin_memcpy(&bits, &f, 4);
+    } else {
+        bits = ((e + 120u) << 23) | (m << 20);
+    }
+    bits |= (v & 0x80u) << 24;
+    float f;
+    __builtin_memcpy(&f, &bits, 4);
+    return f;
+}
+
+float host_fp8_e4m3fn(uint8_t v) { return fp8_e4m3fn(v); }
+
+// rows r0 .. r0 + nrows - 1 of the source (this chunk: src and out start at row r0): out[r][j] = fp8(src[r][j]) *
+// scale[(r0 + r) / block_rows][j / block_cols], one rounding (src/quantize.cpp:1241-1258). A NaN code stays its
+// own NaN (sign included), as the host's multiply returns a NaN operand unchanged.
+__global__ void __launch_bounds__(256) k_fp8_blocks(const uint8_t *__restrict__ src, const float *__restrict__ scale,
+                                                    float *__restrict__ out, long long nrows, long long ncols,
+                                                    long long r0, int block_rows, int block_cols,
+                                                    long long scale_cols) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= nrows * ncols) return;
+    const long long r = i / ncols, j = i - r * ncols;
+    const uint32_t v = src[i];
+    const float f = fp8_e4m3fn(v);
+    out[i] = (v & 0x7fu) == 0x7fu ? f : f * scale[((r0 + r) / block_rows) * scale_cols + j / block_cols];
+}
+
+hipError_t launch_fp8_blocks(const uint8_t *src, const float *scale, float *out, long long nrows, long long ncols,
+                             long long r0, int block_rows, int block_cols, long long scale_cols, hipStream_t stream) {
+    const long long n = nrows * ncols;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_fp8_blocks, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, src, scale, out, nrows,
+                       ncols, r0, block_rows, block_cols, scale_cols);
+    return hipGetLastError();
+}
+
 }  // namespace pq

@@ -208,6 +208,49 @@ int qmatvec_supported(int type) {
     return 0;
 }
 
+// ---- the float-activation entries: outside this path (the reference's answer for a missing kernel)
+hipError_t qmatvec_launch_bf16f(const void *, size_t, const float *, float *, int, int, int, hipStream_t) {
+    return hipErrorInvalidDeviceFunction;
+}
+hipError_t qmatvec_launch(int, const void *, size_t, const float *, float *, int, int, hipStream_t) {
+    return hipErrorInvalidDeviceFunction;
+}
+hipError_t qmatvec_launch_batch(int, const void *, size_t, const float *, float *, int, int, int, hipStream_t) {
+    return hipErrorInvalidDeviceFunction;
+}
+hipError_t qmatvec_launch_batch_h(int, const void *, size_t, const float *, uint16_t *, size_t, float *, int, int, int,
+                                  hipStream_t) {
+    return hipErrorInvalidDeviceFunction;
+}
+int qmatvec_half_supported(int, const void *, size_t, int, int, int) { return 0; }
+hipError_t qmatvec_round_half(int, const float *, uint16_t *, long long, hipStream_t) {
+    return hipErrorInvalidDeviceFunction;
+}
+hipError_t qmatvec_launch_batch_hx(int, const void *, size_t, const uint16_t *, float *, int, int, int, hipStream_t) {
+    return hipErrorInvalidDeviceFunction;
+}
+int qmatvec_q8_0s_source_supported(int, int) { return 0; }
+hipError_t qmatvec_quantize_rows_q8_0(int, const void *, size_t, int, int, int8_t *, uint16_t *, hipStream_t) {
+    return hipErrorInvalidDeviceFunction;
+}
+hipError_t qmatvec_launch_q8_0s(const int8_t *, const uint16_t *, const qmatvec_q8 *, float *, int, int, hipStream_t) {
+    return hipErrorInvalidDeviceFunction;
+}
+int qmatvec_q8_lr_supported(int, int) { return 0; }
+hipError_t qmatvec_launch_q8_lr(int, const void *, size_t, const float *, int, int, float, float *, int, hipStream_t) {
+    return hipErrorInvalidDeviceFunction;
+}
+hipError_t qmatvec_launch_id(int, const void *, size_t, const int32_t *, int, int, const float *, float *, int, int, int,
+                             hipStream_t) {
+    return hipErrorInvalidDeviceFunction;
+}
+int qmatvec_id_batch_f_supported(int) { return 0; }
+hipError_t qmatvec_launch_id_batch_f(int, const void *, size_t, const float *, float *, int, int, int, int,
+                                     const int32_t *, const int32_t *, const int32_t *, const int32_t *, const int32_t *,
+                                     const int32_t *, hipStream_t) {
+    return hipErrorInvalidDeviceFunction;
+}
+
 void qmatvec_set_prefill(int on) { g_prefill = on && !getenv("QMATVEC_PREFILL_SPLIT_VARIANT"); }
 int qmatvec_prefill(void) { return g_prefill; }
 void qmatvec_set_prefill_fp32(int on) { g_prefill_fp32 = on; }

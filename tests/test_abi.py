@@ -96,3 +96,66 @@ def test_host_scalar_conversions(oracle):
         R.qz_fp32_to_bf16.restype = C.c_uint16
         R.qz_fp32_to_bf16.argtypes = [C.c_float]
         assert np.array_equal(got_bf, np.array([R.qz_fp32_to_bf16(C.c_float(v)) for v in xs], dtype=np.uint16))
+
+
+# every function of the reference's C headers for this path (src/qmatvec.h:17-199, src/quant_types.h:19-72,
+# src/quantize.h:21-45; qmatvec_q8_outputs is a header inline there and here)
+REFERENCE_SURFACE = (
+    "qmatvec_init qmatvec_free qmatvec_supported qmatvec_launch qmatvec_launch_bf16f qmatvec_launch_batch "
+    "qmatvec_launch_batch_h qmatvec_half_supported qmatvec_round_half qmatvec_launch_batch_hx qmatvec_set_prefill "
+    "qmatvec_prefill qmatvec_set_prefill_fp32 qmatvec_q8_0s_source_supported qmatvec_quantize_rows_q8_0 "
+    "qmatvec_launch_q8_0s qmatvec_q8_bytes qmatvec_q8_bind qmatvec_q8_supported qmatvec_quantize qmatvec_launch_q8 "
+    "qmatvec_launch_q8_pair qmatvec_q8_lr_supported qmatvec_launch_q8_lr qmatvec_q8_few_supported "
+    "qmatvec_launch_q8_multi qmatvec_launch_q8_multi_t qmatvec_launch_q8_batch qmatvec_launch_q8_id "
+    "qmatvec_launch_q8_id_pair qmatvec_launch_q8_id_x qmatvec_launch_id qmatvec_id_batch_tile "
+    "qmatvec_q8_id_batch_supported qmatvec_launch_q8_id_batch qmatvec_id_batch_f_supported "
+    "qmatvec_launch_id_batch_f qmatvec_set_out_scale qmatvec_drop_out_scales "
+    "qt_get_traits qt_row_size qt_to_float qt_vec_dot_q8k qt_fp16_to_fp32 qt_bf16_to_fp32 "
+    "qz_supported qz_quantize qz_quantize_im qz_quantize_fp8_blocks qz_fp8_e4m3_to_fp32 qz_row_q8_0 "
+    "qz_row_rocmfp4 qz_row_rocmfp4_fast qz_fp32_to_fp16 qz_fp32_to_bf16").split()
+
+
+def test_library_exports_the_reference_surface():
+    """an engine built against the reference's headers links: every function they declare is exported"""
+    lib = C.CDLL(LIB)
+    missing = [n for n in REFERENCE_SURFACE if not hasattr(lib, n)]
+    assert not missing, missing
+    declared = set(declared_functions())
+    assert not [n for n in REFERENCE_SURFACE if n not in declared]
+
+
+def test_float_path_entries_report_unsupported():
+    """the float-activation entries outside this path answer as the reference does for a missing kernel:
+    *_supported 0, launches hipErrorInvalidDeviceFunction (98), without touching their pointers"""
+    lib = C.CDLL(LIB)
+    assert lib.qmatvec_supported(12) == 0
+    assert lib.qmatvec_half_supported(1, None, C.c_size_t(0), 64, 256, 64) == 0
+    assert lib.qmatvec_q8_0s_source_supported(0, 256) == 0
+    assert lib.qmatvec_q8_lr_supported(12, 256) == 0
+    assert lib.qmatvec_id_batch_f_supported(12) == 0
+    assert lib.qmatvec_launch(12, None, C.c_size_t(0), None, None, 64, 256, None) == 98
+    assert lib.qmatvec_launch_batch(12, None, C.c_size_t(0), None, None, 64, 256, 4, None) == 98
+    assert lib.qmatvec_launch_id(12, None, C.c_size_t(0), None, 8, 0, None, None, 64, 256, 1, None) == 98
+
+
+def test_fp8_e4m3_decoder(oracle):
+    """qz_fp8_e4m3_to_fp32 over all 256 codes: the OCP e4m3fn closed form (bias 7, exponent field 0
+    subnormal m 2^-9, S.1111.111 NaN, no infinities), and the compiled reference where it is built"""
+    import numpy as np
+    L = C.CDLL(LIB)
+    L.qz_fp8_e4m3_to_fp32.restype = C.c_float
+    L.qz_fp8_e4m3_to_fp32.argtypes = [C.c_uint8]
+    got = np.array([L.qz_fp8_e4m3_to_fp32(v) for v in range(256)], np.float32)
+    for v in range(256):
+        e, m, s = (v >> 3) & 15, v & 7, -1.0 if v & 0x80 else 1.0
+        if v & 0x7F == 0x7F:
+            assert np.isnan(got[v]) and np.signbit(got[v]) == bool(v & 0x80)
+        else:
+            assert got[v] == s * (m * 2.0 ** -9 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7)), v
+    assert got[0x7E] == 448.0 and got[0x08] == 2.0 ** -6 and got[0x01] == 2.0 ** -9
+    if oracle.ref_available():
+        R = oracle.ref()
+        R.qz_fp8_e4m3_to_fp32.restype = C.c_float
+        R.qz_fp8_e4m3_to_fp32.argtypes = [C.c_uint8]
+        want = np.array([R.qz_fp8_e4m3_to_fp32(v) for v in range(256)], np.float32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
