@@ -1,6 +1,7 @@
-/* moe_ops.h -- C ABI of the mixture-of-experts glue around the expert matvecs (libpurhie_qmv.so, gfx950).
+/* moe_ops.h -- C ABI of the matvec inputs' producers (add + RMSNorm, SwiGLU, both quantizing their output) and
+ * of the mixture-of-experts glue around the expert matvecs (libpurhie_qmv.so, gfx950).
  *
- * Drop-in for the MoE part of the reference's src/gpu_ops.h: same names, argument meaning and error
+ * Drop-in for those parts of the reference's src/gpu_ops.h: same names, argument meaning and error
  * convention (hipError_t; hipErrorInvalidValue for bad arguments). All launches are asynchronous on `stream`;
  * every buffer is device memory owned by the caller. */
 #ifndef PURHIE_MOE_OPS_H
@@ -13,6 +14,14 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+/* replaces src/gpu_ops.h:20-25 (kernels src/gpu_ops.hip:17-100): for each of T rows of n values, x_out = x_in +
+ * add (add NULL: x_out is not written and x_in is normalized), then y = x_out / sqrt(mean(x_out^2) + eps) * w
+ * (w NULL: no gamma); x_out must not alias x_in when add is set. With q8, the T rows of y are also quantized
+ * into it as one flattened [T * n] vector in the same launch (n % 256 == 0, T * n <= q8->max_k). A row's
+ * result does not depend on T. */
+hipError_t gpu_add_rmsnorm(const float *x_in, const float *add, float *x_out, const float *w, float *y, int n, int T,
+                           float eps, const qmatvec_q8 *q8, hipStream_t stream);
 
 /* replaces src/gpu_ops.h:29 (kernel src/gpu_ops.hip:103-113): out = SiLU(g) * u = g / (1 + exp(-g)) * u for
  * n values, quantized into q8 in the same launch when q8 is not NULL (n % 32 == 0, n <= q8->max_k; the Q8_K

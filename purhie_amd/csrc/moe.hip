@@ -2,6 +2,8 @@
 // combine and SwiGLU with the activation quantizer fused in. The reference's gpu_ops.hip:103-330
 // (swiglu, moe_router + router_select, moe_combine, moe_group); the C ABI is include/moe_ops.h.
 //
+//   k_add_rmsnorm  x_out = x_in + add, y = RMSNorm(x_out) * w, and y quantized in the same launch (the producer of
+//                  most matvec inputs; k_add_rmsnorm_rows for many rows, the same bits).
 //   k_swiglu       out = SiLU(g) * u (g / (1 + exp(-g)) * u), and, with a qmatvec_q8, quantized in the same
 //                  launch (one 256-thread workgroup per 256-value block: q8dev.h).
 //   k_moe_router   a workgroup per token: softmax of the router logits (exp(l - max) / sum), the n_used
@@ -33,6 +35,89 @@ __global__ void __launch_bounds__(256) k_swiglu(const float *__restrict__ g, con
         out[i] = v;
     }
     if (quantize) q8_quantize_value(v, active, blockIdx.x, sh, o);  // (uniform)
+}
+
+// ---------------------------------------------------------------- add + RMSNorm, the matvec inputs' producer
+// x_out = x_in + add (add set), y = x_out / sqrt(mean(x_out^2) + eps) * w, and y quantized for the int8 matvecs
+// in the same launch (src/gpu_ops.hip:17-100). The sum of squares has one order in both kernels: thread t adds
+// the squares of values t, t + 256, ... in turn, a wave64 butterfly adds the 64 threads of a wave, and the four
+// wave sums are added as (w0 + w1) + (w2 + w3); a row's result is therefore the same whatever T is.
+__device__ __forceinline__ float norm_total(float ss, float *red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// one token's row in blocks: grid (ceil(n / 256), T); every workgroup sums its row's squares itself (a row is a
+// few KB, its re-reads hit the cache) and normalizes and quantizes its own 256 values, so the whole GPU works on
+// one token
+__global__ void __launch_bounds__(256) k_add_rmsnorm(const float *__restrict__ x_in, const float *__restrict__ add,
+                                                     float *__restrict__ x_out, const float *__restrict__ w,
+                                                     float *__restrict__ y, int n, float eps, Q8Ptrs o, int quantize) {
+    __shared__ float red[4];
+    __shared__ Q8Shared sh;
+    const long long row = (long long)blockIdx.y * n;
+    const float *xi = x_in + row, *ad = add ? add + row : nullptr;
+    const int t = threadIdx.x, i = blockIdx.x * 256 + t;
+    float ss = 0.0f;
+    for (int k = t; k < n; k += 256) {
+        const float v = ad ? xi[k] + ad[k] : xi[k];
+        ss += v * v;
+    }
+    const float inv = 1.0f / sqrtf(norm_total(ss, red) / (float)n + eps);
+    const bool active = i < n;
+    float v = 0.0f;
+    if (active) {
+        v = ad ? xi[i] + ad[i] : xi[i];
+        if (ad) x_out[row + i] = v;
+        v = v * inv * (w ? w[i] : 1.0f);
+        y[row + i] = v;
+    }
+    if (quantize) q8_quantize_value(v, active, (int)blockIdx.y * (n / 256) + (int)blockIdx.x, sh, o);  // (uniform)
+}
+
+// many rows (prefill): one workgroup per row, read once; thread t holds values t + 256 j (n <= 256 NORM_ROWS_V)
+constexpr int NORM_ROWS_V = 32;
+__global__ void __launch_bounds__(256) k_add_rmsnorm_rows(const float *__restrict__ x_in,
+                                                          const float *__restrict__ add, float *__restrict__ x_out,
+                                                          const float *__restrict__ w, float *__restrict__ y, int n,
+                                                          float eps, Q8Ptrs o, int quantize) {
+    __shared__ float red[4];
+    __shared__ Q8Shared sh;
+    const long long row = (long long)blockIdx.x * n;
+    const float *xi = x_in + row, *ad = add ? add + row : nullptr;
+    const int t = threadIdx.x, nb = (n + 255) / 256;
+    float x[NORM_ROWS_V];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NORM_ROWS_V; ++j) {
+        const int k = t + 256 * j;
+        x[j] = 0.0f;
+        if (j < nb && k < n) {
+            x[j] = ad ? xi[k] + ad[k] : xi[k];
+            ss += x[j] * x[j];
+        }
+    }
+    const float inv = 1.0f / sqrtf(norm_total(ss, red) / (float)n + eps);
+#pragma unroll
+    for (int j = 0; j < NORM_ROWS_V; ++j) {
+        if (j < nb) {  // (uniform)
+            const int k = t + 256 * j;
+            const bool active = k < n;
+            float v = 0.0f;
+            if (active) {
+                if (ad) x_out[row + k] = x[j];
+                v = x[j] * inv * (w ? w[k] : 1.0f);
+                y[row + k] = v;
+            }
+            if (quantize) {  // (uniform; n % 256 == 0 when quantizing)
+                if (j) __syncthreads();  // the previous block's reads of sh are done
+                q8_quantize_value(v, active, (int)blockIdx.x * nb + j, sh, o);
+            }
+        }
+    }
 }
 
 // sum / max over the 256 threads of a workgroup (4 waves), the result in every thread
@@ -224,6 +309,25 @@ hipError_t gpu_swiglu(const float *g, const float *u, float *out, int n, const q
         o = Q8Ptrs{q8->q0, q8->d0, q8->qK, q8->dK, q8->bsK, q8->s0};
     }
     hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, g, u, out, n, o, q8 ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t gpu_add_rmsnorm(const float *x_in, const float *add, float *x_out, const float *w, float *y, int n, int T,
+                           float eps, const qmatvec_q8 *q8, hipStream_t stream) {
+    if (!x_in || !y || n <= 0 || T < 0 || (add && (!x_out || x_out == x_in))) return hipErrorInvalidValue;
+    if (T == 0) return hipSuccess;
+    Q8Ptrs o{};
+    if (q8) {
+        if (n % 256 != 0 || (long long)T * n > q8->max_k) return hipErrorInvalidValue;
+        o = Q8Ptrs{q8->q0, q8->d0, q8->qK, q8->dK, q8->bsK, q8->s0};
+    }
+    // one token (or a few): its row in blocks over the whole GPU; many rows of at most 8192 values: a workgroup each
+    if (T >= 8 && n <= 256 * NORM_ROWS_V)
+        hipLaunchKernelGGL(k_add_rmsnorm_rows, dim3((unsigned)T), dim3(256), 0, stream, x_in, add, x_out, w, y, n, eps, o,
+                           q8 ? 1 : 0);
+    else
+        hipLaunchKernelGGL(k_add_rmsnorm, dim3((unsigned)((n + 255) / 256), (unsigned)T), dim3(256), 0, stream, x_in,
+                           add, x_out, w, y, n, eps, o, q8 ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -42,7 +42,14 @@ __device__ __forceinline__ void q8_quantize_value(float v, bool active, int b, Q
         if ((lane & 31) == 0) {
             const float d = am / 127.0f;
             o.d0[i >> 5] = __half2float(__float2half(d));
-            if (o.s0) o.s0[i >> 5] = __float_as_int(__half2float(__float2half(d * (float)s0)));
+            if (o.s0) {
+                // fp16(d * s) rounds the product to fp32 first, as the reference. The register barrier keeps the
+                // backend from folding multiply and conversion into one v_fma_mix rounding, which differs on the
+                // fp16 ties the fp32 rounding makes or breaks (seen at 1 block in ~2700).
+                float p = d * (float)s0;
+                __asm__ volatile("" : "+v"(p));
+                o.s0[i >> 5] = __float_as_int(__half2float(__float2half(p)));
+            }
         }
     }
     if (!o.qK) return;  // (uniform)

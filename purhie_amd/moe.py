@@ -1,5 +1,5 @@
-"""ctypes mirror of include/moe_ops.h (the MoE router, grouping, combine and fused SwiGLU + quantize of
-libpurhie_qmv.so), the reference's src/gpu_ops.h MoE entry points. Device buffers are torch tensors; every
+"""ctypes mirror of include/moe_ops.h (the fused add + RMSNorm + quantize and SwiGLU + quantize producers, and
+the MoE router, grouping and combine of libpurhie_qmv.so), the reference's src/gpu_ops.h entry points. Device buffers are torch tensors; every
 call runs the library's HIP kernels (no CPU path)."""
 import ctypes as C
 
@@ -17,6 +17,7 @@ def lib():
         vp, i32 = C.c_void_p, C.c_int
         pq8 = C.POINTER(Q.qmatvec_q8)
         for name, args in {
+            "gpu_add_rmsnorm": [vp, vp, vp, vp, vp, i32, i32, C.c_float, pq8, vp],
             "gpu_swiglu": [vp, vp, vp, i32, pq8, vp],
             "gpu_moe_router": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32],
             "gpu_moe_combine": [vp, vp, vp, vp, vp, i32, i32, i32, vp],
@@ -42,6 +43,18 @@ def max_tiles(T, n_used, n_expert, tile):
     """gpu_moe_max_tiles (include/moe_ops.h)"""
     n = T * n_used
     return min(n, n_expert + n // tile)
+
+
+def add_rmsnorm(x_in, y, n, T, eps, add=None, x_out=None, w=None, q8=None, stream=None):
+    Q._need(x_in, T * n * 4, "x_in")
+    Q._need(y, T * n * 4, "y")
+    for t_, what in ((add, "add"), (x_out, "x_out")):
+        if t_ is not None:
+            Q._need(t_, T * n * 4, what)
+    if w is not None:
+        Q._need(w, n * 4, "w")
+    _check("gpu_add_rmsnorm", lib().gpu_add_rmsnorm(_p(x_in), _p(add), _p(x_out), _p(w), _p(y), n, T, eps,
+                                                    None if q8 is None else q8.ref, stream))
 
 
 def swiglu(g, u, out, n, q8=None, stream=None):

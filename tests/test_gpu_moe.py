@@ -132,3 +132,57 @@ def test_swiglu_fused_quantize(M, oracle, n):
     out2 = torch.zeros(n, dtype=torch.float32, device="cuda")
     M.swiglu(dev(g), dev(u), out2, n)  # without quantization: the same values
     assert np.array_equal(host(out2).view(np.uint32), got.view(np.uint32))
+
+
+@pytest.mark.parametrize("n,T", [(2560, 1), (5120, 3), (2048, 16), (1024, 40), (9728, 9)])
+def test_add_rmsnorm_fused_quantize(M, oracle, n, T):
+    """gpu_add_rmsnorm (src/gpu_ops.hip:17-100): x_out = x_in + add bit for bit (one fp32 add), y within a few
+    ulps of the float64 RMSNorm of it, the fused quantization bit-identical to the oracle's quantizer on the y it
+    wrote (both formats), and each row the same bits as that row normalized alone (the one-row kernel against
+    the many-rows one)"""
+    import torch
+    from purhie_amd import qmatvec as Q
+    eps = 1e-6
+    x = synth.gaussian(990 + n + T, T * n).reshape(T, n)
+    a = synth.gaussian(991 + n + T, T * n).reshape(T, n) * np.float32(0.5)
+    w = (synth.gaussian(992 + n, n) * np.float32(0.1) + np.float32(1.0)).astype(np.float32)
+    y = torch.full((T, n), float("nan"), dtype=torch.float32, device="cuda")
+    xo = torch.full((T, n), float("nan"), dtype=torch.float32, device="cuda")
+    q = Q.Q8(T * n)
+    M.add_rmsnorm(dev(x), y, n, T, eps, add=dev(a), x_out=xo, w=dev(w), q8=q)
+    s = x + a
+    assert np.array_equal(host(xo).view(np.uint32), s.view(np.uint32))
+    got = host(y)
+    s64 = s.astype(np.float64)
+    want = s64 / np.sqrt((s64 * s64).mean(axis=1, keepdims=True) + eps) * w.astype(np.float64)
+    assert np.all(np.abs(got - want) <= 4e-7 * np.abs(want) + 1e-30), np.abs((got - want) / want).max()
+    v = {k: host(t) for k, t in q.views(T * n).items()}
+    a0, aK = oracle.quantize_act(got, kq=False), oracle.quantize_act(got, kq=True)
+    assert np.array_equal(v["q0"], a0["q"]) and np.array_equal(v["d0"].view(np.uint32), a0["d"].view(np.uint32))
+    assert np.array_equal(v["s0"], a0["s0"])
+    assert np.array_equal(v["qK"], aK["q"]) and np.array_equal(v["dK"].view(np.uint32), aK["d"].view(np.uint32))
+    assert np.array_equal(v["bsK"], aK["bs"])
+    for r in range(min(T, 3)):
+        y1 = torch.zeros(n, dtype=torch.float32, device="cuda")
+        x1 = torch.zeros(n, dtype=torch.float32, device="cuda")
+        M.add_rmsnorm(dev(x[r]), y1, n, 1, eps, add=dev(a[r]), x_out=x1, w=dev(w))
+        assert np.array_equal(host(y1).view(np.uint32), got[r].view(np.uint32)), r
+    # without add (x_out untouched) and without gamma
+    y2 = torch.zeros((T, n), dtype=torch.float32, device="cuda")
+    xo2 = torch.full((T, n), 7.0, dtype=torch.float32, device="cuda")
+    M.add_rmsnorm(dev(s), y2, n, T, eps, x_out=xo2)
+    want2 = s64 / np.sqrt((s64 * s64).mean(axis=1, keepdims=True) + eps)
+    assert np.all(np.abs(host(y2) - want2) <= 4e-7 * np.abs(want2) + 1e-30)
+    assert np.all(host(xo2) == 7.0)
+
+
+def test_add_rmsnorm_bad_arguments(M):
+    import torch
+    from purhie_amd import qmatvec as Q
+    L = M.lib()
+    x = torch.zeros(512, device="cuda")
+    q = Q.Q8(256)
+    p = lambda t: __import__("ctypes").c_void_p(t.data_ptr())
+    assert L.gpu_add_rmsnorm(p(x), p(x), p(x), None, p(x), 256, 1, 1e-6, None, None) == 1  # x_out aliases x_in
+    assert L.gpu_add_rmsnorm(p(x), None, None, None, p(x), 200, 1, 1e-6, q.ref, None) == 1  # n % 256
+    assert L.gpu_add_rmsnorm(p(x), None, None, None, p(x), 256, 2, 1e-6, q.ref, None) == 1  # T n > max_k

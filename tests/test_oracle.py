@@ -231,6 +231,15 @@ def test_q8_0_activation_closed_form(oracle):
     t[0] = 127.0
     t[1:5] = [0.5, 1.5, 2.5, -2.5]
     assert oracle.quantize_act(t, kq=False)["q"][:5].tolist() == [127, 0, 2, 2, -2]
+    # the sum term rounds twice (fp32 product, then fp16): d * -113 at amax 3.1137567 is exactly the fp16
+    # midpoint -2.7705078125 in fp32, so it goes to even (-2.76953125), where one rounding of the exact
+    # product (-2.77050789...) would give -2.771484375
+    am = np.float32(3.1137567)
+    t = np.zeros(32, np.float32)
+    t[0], t[1] = -am, np.float32(14) * am / np.float32(127)
+    a = oracle.quantize_act(t, kq=False)
+    assert a["q"][:2].tolist() == [-127, 14]
+    assert float(a["s0"][:1].view(np.float32)[0]) == -2.76953125
 
 
 def test_q8_k_activation_closed_form(oracle):
