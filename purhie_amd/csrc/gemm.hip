@@ -450,6 +450,7 @@ constexpr int GS_K = 64;                  // K per stage (two 32-blocks)
 constexpr int GS_ROW = GS_K + 8;          // halves per LDS row (16 bytes of padding: conflict-free b128 reads)
 constexpr int GS_N = 256;                 // weight rows per workgroup (one per thread when staging)
 constexpr int GS_T = 128;                 // tokens per workgroup
+constexpr int GS_T_MOE = 64;              // tokens per workgroup over MoE expert tiles and short prompts
 
 // the stage's two weight blocks of row n0 + t (thread t), decoded into the 64 halves of its LDS row
 template <int TYPE>
@@ -491,14 +492,18 @@ struct SplitStage {
     }
 };
 
-// workgroup tile 256 weight rows x 128 tokens; wave w computes rows 128 (w & 1) .. + 127 x tokens 64 (w >> 1) ..
-// + 63 (8 x 4 MFMA tiles): a wave reads 8 weight and 2 x 4 token fragments per 32-block for 64 MFMAs
-template <int TYPE>
+// workgroup tile 256 weight rows x TT tokens (128; 64 for MoE expert tiles, whose runs average a few dozen
+// entries, and for prompts of at most 64 tokens); wave w computes rows 128 (w & 1) .. + 127 x tokens TT / 2 (w >> 1) .. (8 x TT / 32 MFMA tiles): per
+// 32-block a wave reads 8 weight and 2 x TT / 32 token fragments for 16 TT / 32 MFMAs
+template <int TYPE, int TT>
 __global__ void __launch_bounds__(G_THREADS, 2) k_gemm_split(GemmArgs a) {
     using S = SplitStage<TYPE>;
+    constexpr int NJ = TT / 32;          // token tiles per wave
+    constexpr int TPR = G_THREADS / TT;  // staging threads per token row
+    constexpr int U4 = GS_K / TPR / 8;   // 16-byte pieces per thread and plane
     __shared__ __attribute__((aligned(16))) _Float16 sW[GS_N * GS_ROW];
-    __shared__ __attribute__((aligned(16))) _Float16 sH[GS_T * GS_ROW];
-    __shared__ __attribute__((aligned(16))) _Float16 sL[GS_T * GS_ROW];
+    __shared__ __attribute__((aligned(16))) _Float16 sH[TT * GS_ROW];
+    __shared__ __attribute__((aligned(16))) _Float16 sL[TT * GS_ROW];
     __shared__ uint32_t lut[256];
 
     int n0, e = 0;
@@ -513,22 +518,22 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm_split(GemmArgs a) {
         orow = a.out_rows + st;
         n0 = blockIdx.x * GS_N;
     } else {          // dense: grid (token tiles, row tiles); a row tile's token tiles are adjacent
-        tm = {nullptr, (int)blockIdx.x * GS_T, GS_T, a.zero_row};
+        tm = {nullptr, (int)blockIdx.x * TT, TT, a.zero_row};
         n0 = blockIdx.y * GS_N;
     }
     const uint8_t *W = a.W + (long long)e * a.N * a.row_bytes;
     init_fp4_lut(lut);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wn = (wave & 1) * 128, wt = (wave >> 1) * 64;
+    const int wn = (wave & 1) * 128, wt = (wave >> 1) * (TT / 2);
 
-    // token staging: thread t copies 32 halves (64 bytes) of hi and of lo of token row t / 2
-    const int xr = tid >> 1, xp = tid & 1;
-    const long long xoff = (long long)tm.row(xr) * a.K + 32 * xp;
+    // token staging: thread t copies 8 U4 halves of hi and of lo of token row t / TPR
+    const int xr = tid / TPR, xp = tid % TPR;
+    const long long xoff = (long long)tm.row(xr) * a.K + 8 * U4 * xp;
     const _Float16 *hsrc = a.xh + xoff, *lsrc = a.xl + xoff;
 
     typename S::Raw raw;
-    uint4 hv0, hv1, hv2, hv3, lv0, lv1, lv2, lv3;  // (scalars: an array here ends up in scratch)
+    uint4 hv0, hv1, hv2, hv3, lv0, lv1, lv2, lv3;  // (scalars: an array here ends up in scratch; U4 = 2 uses 0, 1)
 #define GSPLIT_ISSUE(k0)                                                \
     do {                                                                \
         S::load(W, a.row_bytes, a.N, n0, (k0), raw);                    \
@@ -536,33 +541,37 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm_split(GemmArgs a) {
         const uint4 *l4 = (const uint4 *)(lsrc + (k0));                 \
         hv0 = h4[0];                                                    \
         hv1 = h4[1];                                                    \
-        hv2 = h4[2];                                                    \
-        hv3 = h4[3];                                                    \
         lv0 = l4[0];                                                    \
         lv1 = l4[1];                                                    \
-        lv2 = l4[2];                                                    \
-        lv3 = l4[3];                                                    \
+        if (U4 == 4) {                                                  \
+            hv2 = h4[2];                                                \
+            hv3 = h4[3];                                                \
+            lv2 = l4[2];                                                \
+            lv3 = l4[3];                                                \
+        }                                                               \
     } while (0)
 
-    f4 acc[8][4];
+    f4 acc[8][NJ];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < NJ; ++j) acc[i][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
     GSPLIT_ISSUE(0);
     for (int k0 = 0; k0 < a.K; k0 += GS_K) {
         __syncthreads();  // the previous stage's LDS reads are done (and the table is written)
         S::store(raw, lut, sW);
-        uint4 *hd = (uint4 *)(sH + xr * GS_ROW + 32 * xp), *ld = (uint4 *)(sL + xr * GS_ROW + 32 * xp);
+        uint4 *hd = (uint4 *)(sH + xr * GS_ROW + 8 * U4 * xp), *ld = (uint4 *)(sL + xr * GS_ROW + 8 * U4 * xp);
         hd[0] = hv0;
         hd[1] = hv1;
-        hd[2] = hv2;
-        hd[3] = hv3;
         ld[0] = lv0;
         ld[1] = lv1;
-        ld[2] = lv2;
-        ld[3] = lv3;
+        if (U4 == 4) {
+            hd[2] = hv2;
+            hd[3] = hv3;
+            ld[2] = lv2;
+            ld[3] = lv3;
+        }
         __syncthreads();
         if (k0 + GS_K < a.K) GSPLIT_ISSUE(k0 + GS_K);  // next stage's global loads in flight during the MFMAs
 
@@ -570,9 +579,9 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm_split(GemmArgs a) {
 #pragma unroll
         for (int b = 0; b < GS_K / 32; ++b) {
             const int kk = b * 32 + 8 * (lane >> 4);
-            h8 fh[4], fl[4];
+            h8 fh[NJ], fl[NJ];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < NJ; ++j) {
                 fh[j] = *(const h8 *)(sH + (wt + 16 * j + (lane & 15)) * GS_ROW + kk);
                 fl[j] = *(const h8 *)(sL + (wt + 16 * j + (lane & 15)) * GS_ROW + kk);
             }
@@ -584,16 +593,16 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm_split(GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < NJ; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fh[j], acc[i][j], 0, 0, 0);
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < NJ; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fl[j], acc[i][j], 0, 0, 0);
             }
-            // the block's 16 fragment reads are issued before its 64 MFMAs (left alone, the scheduler moves each
-            // weight fragment's read next to its first use and waits for it there)
-            __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 64, 0);
+            // the block's fragment reads are issued before its MFMAs (left alone, the scheduler moves each weight
+            // fragment's read next to its first use and waits for it there)
+            __builtin_amdgcn_sched_group_barrier(0x100, 8 + 2 * NJ, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 16 * NJ, 0);
         }
         __builtin_amdgcn_s_setprio(0);
     }
@@ -602,7 +611,7 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm_split(GemmArgs a) {
     // store: lane holds rows 4 (lane / 16) .. + 3 of each 16 x 16 tile, token column lane % 16
     const float sc = a.es ? a.es[e] : a.osc;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
         const int tt = wt + 16 * j + (lane & 15);
         long long yrow;
         if (orow) {
@@ -628,6 +637,10 @@ bool gemm_split(int type) { return type == TY_FP4 || type == TY_FAST; }
 
 int gemm_split_k_multiple() { return GS_K; }
 
+int gemm_id_token_tile(int type) { return gemm_split(type) ? GS_T_MOE : GB_T; }
+
+int gemm_dense_token_tile(int type, int T) { return gemm_split(type) && T <= GS_T_MOE ? GS_T_MOE : GB_T; }
+
 int gemm_rows_per_wg(int type) { return gemm_split(type) ? GS_N : gemm_kquant(type) ? GEMM_KQ_ROWS : GB_N; }
 
 hipError_t launch_act_split(int type, const int8_t *q, const float *d, int T, int K, int rows, _Float16 *xh,
@@ -639,8 +652,14 @@ hipError_t launch_act_split(int type, const int8_t *q, const float *d, int T, in
 
 hipError_t launch_gemm_split(int type, const GemmArgs &a, dim3 grid, hipStream_t stream) {
     switch (type) {
-    case TY_FP4: hipLaunchKernelGGL(k_gemm_split<TY_FP4>, grid, dim3(G_THREADS), 0, stream, a); break;
-    case TY_FAST: hipLaunchKernelGGL(k_gemm_split<TY_FAST>, grid, dim3(G_THREADS), 0, stream, a); break;
+    case TY_FP4:
+        if (a.n_tiles || a.tt == GS_T_MOE) hipLaunchKernelGGL((k_gemm_split<TY_FP4, GS_T_MOE>), grid, dim3(G_THREADS), 0, stream, a);
+        else hipLaunchKernelGGL((k_gemm_split<TY_FP4, GS_T>), grid, dim3(G_THREADS), 0, stream, a);
+        break;
+    case TY_FAST:
+        if (a.n_tiles || a.tt == GS_T_MOE) hipLaunchKernelGGL((k_gemm_split<TY_FAST, GS_T_MOE>), grid, dim3(G_THREADS), 0, stream, a);
+        else hipLaunchKernelGGL((k_gemm_split<TY_FAST, GS_T>), grid, dim3(G_THREADS), 0, stream, a);
+        break;
     default: return hipErrorInvalidDeviceFunction;
     }
     return hipGetLastError();

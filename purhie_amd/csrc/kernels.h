@@ -84,11 +84,14 @@ struct GemmArgs {
     // MoE tiles (n_tiles null: dense)
     const int32_t *n_tiles, *tile_e, *tile_start, *tile_n, *in_rows, *out_rows;
     const float *es;        // per-expert output scales (null: osc)
+    int tt;                 // split GEMM, dense: tokens per workgroup (128, or 64 for short prompts)
 };
 
 int gemm_supported(int type);
 int gemm_k_multiple();
 int gemm_token_tile();
+int gemm_id_token_tile(int type);  // the largest MoE expert tile the type's GEMM takes
+int gemm_dense_token_tile(int type, int T);  // tokens per workgroup of the dense GEMM for T tokens
 hipError_t launch_act_f16(int type, const int8_t *q, const float *d, int T, int K, int Tpad, _Float16 *xh, float *dxp,
                           hipStream_t stream);
 hipError_t launch_gemm(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);

@@ -143,7 +143,7 @@ int gemm_k_mult(int type) {
 
 hipError_t gemm_dense(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, long long ldy, int N,
                       int K, int T, hipStream_t stream) {
-    const int BT = gemm_token_tile();
+    const int BT = gemm_dense_token_tile(type, T);
     const int Tpad = (T + BT - 1) / BT * BT;
     TokWs w;
     hipError_t e = tokens_prep(type, q, T, K, Tpad + 1, w, stream);
@@ -163,6 +163,7 @@ hipError_t gemm_dense(int type, const void *W, size_t row_bytes, const qmatvec_q
         a.T = T;
         a.zero_row = Tpad;
         a.osc = dense_scale(W);
+        a.tt = BT;
         const int RN = gemm_rows_per_wg(type);
         e = gemm_launch(type, a, dim3((unsigned)(Tpad / BT), (unsigned)((N + RN - 1) / RN)), stream);
     }
@@ -443,7 +444,9 @@ static bool id_gemm_ok(int type, int N, int K) {
 
 // the largest tile the expert-tiled launch takes: the GEMM reads each expert's weights once per this many
 // entries; the decode-order path takes the reference's 16 (src/qmatvec.cpp:612-615)
-int qmatvec_id_batch_tile(int type, int N, int K) { return id_gemm_ok(type, N, K) ? gemm_token_tile() : ID_DECODE_TILE; }
+int qmatvec_id_batch_tile(int type, int N, int K) {
+    return id_gemm_ok(type, N, K) ? gemm_id_token_tile(type) : ID_DECODE_TILE;
+}
 
 hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N,
                                       int K, int max_tiles, int tile, const int32_t *n_tiles, const int32_t *tile_e,

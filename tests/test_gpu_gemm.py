@@ -78,7 +78,8 @@ def test_gemm_ldy_and_split_invariance(Q, oracle, t):
     Q.lib().qmatvec_set_prefill(1)
     try:
         full = run_batch(Q, t, Wd, x, N, K, ldy=N + 13)
-        parts = np.concatenate([run_batch(Q, t, Wd, x[s:e], N, K) for s, e in ((0, 1), (1, 70), (70, 150))])
+        cuts = ((0, 1), (1, 65), (65, 70), (70, 150))  # 64-token workgroups up to 64 tokens, 128 above
+        parts = np.concatenate([run_batch(Q, t, Wd, x[s:e], N, K) for s, e in cuts])
     finally:
         Q.lib().qmatvec_set_prefill(0)
     assert np.array_equal(full.view(np.uint32), parts.view(np.uint32))
