@@ -8,7 +8,8 @@
 //                  launch (one 256-thread workgroup per 256-value block: q8dev.h).
 //   k_moe_router   a workgroup per token: softmax of the router logits (exp(l - max) / sum), the n_used
 //                  largest probabilities in descending order (equal values: the lower expert) by each expert's
-//                  rank, their weights divided by max(sum, 2^-14), and the shared-expert gate sigmoid(x . w_shexp).
+//                  rank among 64-bit (probability, ~index) keys, their weights divided by max(sum, 2^-14), and
+//                  the shared-expert gate sigmoid(x . w_shexp).
 //   k_moe_combine  out = sum_j w_j down_j in slot order (+ sg shared), rounded after every product and sum
 //                  (no contraction) as the reference's CPU add chain.
 //   k_moe_group    one 1024-thread workgroup: entries (token, slot) counted per expert in LDS, two exclusive
@@ -143,65 +144,90 @@ __global__ void __launch_bounds__(256) k_moe_router(const float *__restrict__ lo
                                                     const float *__restrict__ w_sh, int *__restrict__ ids,
                                                     float *__restrict__ wts, float *__restrict__ sg, int n_expert,
                                                     int n_used, int n, int ids_stride) {
-    __shared__ __attribute__((aligned(16))) float p[MOE_MAX_EXPERTS];
+    constexpr int PER = MOE_MAX_EXPERTS / 256;  // experts per thread: tid + 256 j
+    __shared__ unsigned long long key[MOE_MAX_EXPERTS];
     __shared__ float red[4];
     __shared__ float selw[MOE_MAX_USED];
+    __shared__ float wsum;
     const int t = blockIdx.x, tid = threadIdx.x;
     const float *l = logits + (long long)t * n_expert;
 
-    if (w_sh) {  // (uniform) the shared expert's gate
+    // the logits once into registers, and the shared expert's dot product, before any wait
+    float lv[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int e = tid + 256 * j;
+        lv[j] = e < n_expert ? l[e] : -INFINITY;
+    }
+    float dsum = 0.0f;
+    if (w_sh) {  // (uniform)
         const float *xt = x + (long long)t * n;
-        float dsum = 0.0f;
         for (int i = tid; i < n; i += 256) dsum = fmaf(xt[i], w_sh[i], dsum);
-        dsum = wg_sum(dsum, red);
-        if (tid == 0) sg[t] = 1.0f / (1.0f + expf(-dsum));
     }
 
-    float mx = -INFINITY;
-    for (int e = tid; e < n_expert; e += 256) mx = fmaxf(mx, l[e]);
+    float mx = lv[0];
+#pragma unroll
+    for (int j = 1; j < PER; ++j) mx = fmaxf(mx, lv[j]);
     mx = wg_max(mx, red);
     float sum = 0.0f;
-    for (int e = tid; e < n_expert; e += 256) {
-        const float v = expf(l[e] - mx);
-        p[e] = v;
-        sum += v;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int e = tid + 256 * j;
+        lv[j] = e < n_expert ? expf(lv[j] - mx) : 0.0f;
+        sum += lv[j];
     }
     sum = wg_sum(sum, red);
     const float inv = 1.0f / sum;
-    for (int e = tid; e < n_expert; e += 256) p[e] *= inv;
-    __syncthreads();
 
     // top n_used by rank: expert e's rank is the number of experts ahead of it, those with a larger probability
-    // or an equal one at a lower index (the order of the reference's rounds of argmax). Every thread ranks its
-    // experts against all of p at once (broadcast LDS reads), so no round waits on another. Ranks are distinct:
-    // the order is total once a NaN probability ranks below every number.
-    const int n4 = (n_expert + 3) & ~3;
-    for (int e = n_expert + tid; e < n4; e += 256) p[e] = -INFINITY;  // (ahead of nothing)
-    __syncthreads();
-    for (int e = tid; e < n_expert; e += 256) {
-        const float pe = p[e];
-        const float v = pe == pe ? pe : -2.0f;
-        int r = 0;
-        for (int f = 0; f < n4; f += 4) {
-            const float4 u = *(const float4 *)(p + f);
-            const float u0 = u.x == u.x ? u.x : -2.0f, u1 = u.y == u.y ? u.y : -2.0f;
-            const float u2 = u.z == u.z ? u.z : -2.0f, u3 = u.w == u.w ? u.w : -2.0f;
-            r += (u0 > v || (u0 == v && f < e)) + (u1 > v || (u1 == v && f + 1 < e)) +
-                 (u2 > v || (u2 == v && f + 2 < e)) + (u3 > v || (u3 == v && f + 3 < e));
+    // or an equal one at a lower index (the order of the reference's rounds of argmax). One 64-bit key per
+    // expert orders both at once: high word the probability's bits plus one (probabilities are >= 0, so their
+    // bits order as the values; a NaN gets 0 and ranks below every number), low word ~e. Keys are distinct, so
+    // the ranks are too.
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int e = tid + 256 * j;
+        if (e < n_expert) {
+            const float p = lv[j] * inv;
+            lv[j] = p;
+            const uint32_t hi = p == p ? __float_as_uint(p) + 1u : 0u;
+            key[e] = ((unsigned long long)hi << 32) | (uint32_t)~e;
         }
-        if (r < n_used) {
-            ids[(long long)t * ids_stride + r] = e;
-            selw[r] = pe;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int e = tid + 256 * j;
+        if (256 * j < n_expert) {  // (uniform)
+            if (e < n_expert) {
+                const unsigned long long k = key[e];
+                int r = 0;
+                int f = 0;
+                for (; f + 2 <= n_expert; f += 2) {
+                    const ulonglong2 u = *(const ulonglong2 *)(key + f);
+                    r += (u.x > k) + (u.y > k);
+                }
+                if (f < n_expert) r += key[f] > k;
+                if (r < n_used) {
+                    ids[(long long)t * ids_stride + r] = e;
+                    selw[r] = lv[j];
+                }
+            }
         }
     }
     if (tid == n_used && ids_stride > n_used) ids[(long long)t * ids_stride + n_used] = -1;  // the shared slot
+    if (w_sh) {  // (uniform) the shared expert's gate
+        dsum = wg_sum(dsum, red);
+        if (tid == 0) sg[t] = 1.0f / (1.0f + expf(-dsum));
+    }
     __syncthreads();
-    if (tid == 0) {
+    if (tid == 0) {  // the sum in slot order, as the reference's loop
         float ws = 0.0f;
         for (int r = 0; r < n_used; ++r) ws += selw[r];
-        ws = fmaxf(ws, 6.103515625e-5f);
-        for (int r = 0; r < n_used; ++r) wts[(long long)t * n_used + r] = selw[r] / ws;
+        wsum = fmaxf(ws, 6.103515625e-5f);
     }
+    __syncthreads();
+    if (tid < n_used) wts[(long long)t * n_used + tid] = selw[tid] / wsum;
 }
 
 __global__ void __launch_bounds__(256) k_moe_combine(const float *__restrict__ down, const float *__restrict__ wts,
