@@ -11,11 +11,13 @@
 #   src/quantize.cpp      weight encoders (qz_*); needs -ffp-contract=off (it #errors under fast math)
 #   src/quantize_iq.cpp   IQ encoders, referenced by quantize.cpp's row driver
 #   src/expert_cpu.cpp    CPU expert matvecs (scalar + AVX-512 VNNI, chosen at run time)
+#   src/gguf_mmap.cpp     the GGUF reader (gguf_*)
 
 REF ?= /root/reference
 ORACLE_DIR := $(dir $(lastword $(MAKEFILE_LIST)))
 OUT := $(ORACLE_DIR)_ref
-SRCS := $(REF)/src/quant_types.cpp $(REF)/src/quantize.cpp $(REF)/src/quantize_iq.cpp $(REF)/src/expert_cpu.cpp
+SRCS := $(REF)/src/quant_types.cpp $(REF)/src/quantize.cpp $(REF)/src/quantize_iq.cpp $(REF)/src/expert_cpu.cpp \
+        $(REF)/src/gguf_mmap.cpp
 CXXFLAGS := -std=c++17 -O2 -fPIC -ffp-contract=off -fno-fast-math -I$(REF)/src -w
 
 $(OUT)/libref.so: $(SRCS) $(lastword $(MAKEFILE_LIST))

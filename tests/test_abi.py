@@ -99,7 +99,8 @@ def test_host_scalar_conversions(oracle):
 
 
 # every function of the reference's C headers for this path (src/qmatvec.h:17-199, src/quant_types.h:19-72,
-# src/quantize.h:21-45; qmatvec_q8_outputs is a header inline there and here)
+# src/quantize.h:21-45, the producer and MoE part of src/gpu_ops.h, src/gguf_mmap.h:15-121; qmatvec_q8_outputs
+# and gpu_moe_max_tiles are header inlines there and here)
 REFERENCE_SURFACE = (
     "qmatvec_init qmatvec_free qmatvec_supported qmatvec_launch qmatvec_launch_bf16f qmatvec_launch_batch "
     "qmatvec_launch_batch_h qmatvec_half_supported qmatvec_round_half qmatvec_launch_batch_hx qmatvec_set_prefill "
@@ -112,7 +113,21 @@ REFERENCE_SURFACE = (
     "qmatvec_launch_id_batch_f qmatvec_set_out_scale qmatvec_drop_out_scales "
     "qt_get_traits qt_row_size qt_to_float qt_vec_dot_q8k qt_fp16_to_fp32 qt_bf16_to_fp32 "
     "qz_supported qz_quantize qz_quantize_im qz_quantize_fp8_blocks qz_fp8_e4m3_to_fp32 qz_row_q8_0 "
-    "qz_row_rocmfp4 qz_row_rocmfp4_fast qz_fp32_to_fp16 qz_fp32_to_bf16").split()
+    "qz_row_rocmfp4 qz_row_rocmfp4_fast qz_fp32_to_fp16 qz_fp32_to_bf16 "
+    # src/gpu_ops.h:20-29,36-48,76: the matvec inputs' producers and the MoE glue
+    "gpu_add_rmsnorm gpu_swiglu gpu_moe_router gpu_moe_combine gpu_moe_combine_scaled gpu_moe_group "
+    # src/gguf_mmap.h:15-121: the GGUF reader
+    "gguf_mmap_open gguf_mmap_close gguf_mmap_get_tensor gguf_n_tensors gguf_tensor_name gguf_tensor_type "
+    "gguf_tensor_ne gguf_tensor_dims gguf_tensor_block_size gguf_tensor_type_size gguf_tensor_row_size "
+    "gguf_tensor_offset gguf_tensor_nbytes gguf_tensor_nbytes_pad gguf_n_kv gguf_kv_key gguf_kv_type "
+    "gguf_kv_get_u8 gguf_kv_get_i8 gguf_kv_get_u16 gguf_kv_get_i16 gguf_kv_get_u32 gguf_kv_get_i32 "
+    "gguf_kv_get_f32 gguf_kv_get_u64 gguf_kv_get_i64 gguf_kv_get_f64 gguf_alignment gguf_data_offset "
+    "gguf_version gguf_arch gguf_vocab_name gguf_tokenizer_type gguf_pre_type gguf_vocab_size gguf_head_count "
+    "gguf_head_count_kv gguf_context_length gguf_embedding_length gguf_block_count gguf_arch_int gguf_arch_float "
+    "gguf_kv_str_val gguf_kv_get_string_array gguf_free_string_array gguf_kv_get_array gguf_find_kv "
+    "gguf_kv_get_added_tokens gguf_get_tensor_ptr gguf_map_base gguf_n_maps gguf_map_at gguf_remap "
+    "gguf_tensor_source gguf_tensor_split gguf_set_tensor_staged gguf_file_path gguf_file_identity "
+    "gguf_type_is_self_contained").split()
 
 
 def test_library_exports_the_reference_surface():
