@@ -396,26 +396,27 @@ hipError_t launch_gemm(int type, const GemmArgs &a, dim3 grid, hipStream_t strea
 }
 
 // ---------------------------------------------------------------- split-activation GEMM (ROCmFP4, FAST)
-// The activation value X = q dx (int8 q times its fp16-rounded block scale: at most 19 significant bits,
-// exact in fp32) is written as two fp16 planes, hi = fp16(X 2^s) and lo = fp16(X 2^s - hi), with a per-token
-// power of two 2^s that puts the row's largest |X| just under 2^14. hi + lo carries X to 2^-22 relative (the
-// lo rounding), products with the weight value CB * scale (exact in fp16) are exact in fp32, so the MFMAs
-// chain straight through K with no per-block epilogue: y = (sum_k W'[n][k] (hi + lo)[t][k]) 2^-s. The
-// matrix core does twice the multiplies of the per-block form, and the vector ALU only decodes weights.
+// The activation value X = q dx (int8 q times its fp16-rounded block scale: at most 19 significant bits) enters
+// the MFMAs as two fp16 planes, hi = fp16(X 2^s) and lo = fp16(X 2^s - hi), with a per-token power of two 2^s
+// that puts the row's largest |X| just under 2^14. hi + lo carries X to 2^-22 relative (the lo rounding),
+// products with the weight value CB * scale (exact in fp16) are exact in fp32, so the MFMAs chain straight
+// through K with no per-block epilogue: y = (sum_k W'[n][k] (hi + lo)[t][k]) 2^-s. The matrix core does twice
+// the multiplies of the per-block form. The planes are made in registers from the int8 values and the block's
+// scale ds = fp16(dx 2^s) (exact: an fp16 value times a power of two, inside the fp16 range): hi = q * ds and
+// lo = fma(q, ds, -hi), packed fp16 operations with one rounding each, which are the two roundings above.
 
-// one workgroup per token row (rows >= T, up to Tpad + 1, are zero): hi / lo planes in the GEMM's K order
-// (perm: position 2j <- value j, 2j + 1 <- value j + 16 of each 32-block) and ts[t] = 2^-s
+// one workgroup per token row (rows >= T, up to Tpad + 1, are zero): the int8 values in the GEMM's K order (perm:
+// position 2j <- value j, 2j + 1 <- value j + 16 of each 32-block), the block scales dx 2^s as fp16 and ts[t] = 2^-s
 __global__ void __launch_bounds__(256) k_act_split(const int8_t *__restrict__ q, const float *__restrict__ d, int T,
-                                                   int K, int perm, _Float16 *__restrict__ xh,
-                                                   _Float16 *__restrict__ xl, float *__restrict__ ts) {
+                                                   int K, int perm, int8_t *__restrict__ xq,
+                                                   _Float16 *__restrict__ xs, float *__restrict__ ts) {
     __shared__ float red[4];
     const int t = blockIdx.x, tid = threadIdx.x, nb = K / 32;
-    _Float16 *oh = xh + (long long)t * K, *ol = xl + (long long)t * K;
+    int8_t *oq = xq + (long long)t * K;
+    _Float16 *os = xs + (long long)t * nb;
     if (t >= T) {  // (uniform)
-        for (int k = tid; k < K; k += 256) {
-            oh[k] = (_Float16)0.0f;
-            ol[k] = (_Float16)0.0f;
-        }
+        for (int k = tid; k < K; k += 256) oq[k] = 0;
+        for (int b = tid; b < nb; b += 256) os[b] = (_Float16)0.0f;
         if (tid == 0) ts[t] = 0.0f;
         return;
     }
@@ -437,13 +438,9 @@ __global__ void __launch_bounds__(256) k_act_split(const int8_t *__restrict__ q,
     const int8_t *qt = q + (long long)t * K;
     for (int i = tid; i < K; i += 256) {
         const int b = i >> 5, j = i & 31;
-        const float x = (float)qt[i] * dt[b] * up;  // exact: 8 x 11 significant bits, times a power of two
-        const _Float16 h = (_Float16)x;
-        const _Float16 l = (_Float16)(x - (float)h);
-        const int pos = perm ? 32 * b + (j < 16 ? 2 * j : 2 * (j - 16) + 1) : i;
-        oh[pos] = h;
-        ol[pos] = l;
+        oq[perm ? 32 * b + (j < 16 ? 2 * j : 2 * (j - 16) + 1) : i] = qt[i];
     }
+    for (int b = tid; b < nb; b += 256) os[b] = (_Float16)(dt[b] * up);
 }
 
 constexpr int GS_K = 64;                  // K per stage (two 32-blocks)
@@ -500,10 +497,11 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm_split(GemmArgs a) {
     using S = SplitStage<TYPE>;
     constexpr int NJ = TT / 32;          // token tiles per wave
     constexpr int TPR = G_THREADS / TT;  // staging threads per token row
-    constexpr int U4 = GS_K / TPR / 8;   // 16-byte pieces per thread and plane
+    constexpr int BPT = GS_K / TPR;      // int8 values a staging thread copies (32 or 16: one 16-byte piece or two)
+    constexpr int QROW = GS_K + 16;      // bytes per LDS token row (16 of padding: conflict-free 8-byte reads)
     __shared__ __attribute__((aligned(16))) _Float16 sW[GS_N * GS_ROW];
-    __shared__ __attribute__((aligned(16))) _Float16 sH[TT * GS_ROW];
-    __shared__ __attribute__((aligned(16))) _Float16 sL[TT * GS_ROW];
+    __shared__ __attribute__((aligned(16))) int8_t sQ[TT * QROW];
+    __shared__ uint16_t sD[TT * 2];  // the stage's two block scales of each token row (fp16 bits)
     __shared__ uint32_t lut[256];
 
     int n0, e = 0;
@@ -527,28 +525,23 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm_split(GemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wn = (wave & 1) * 128, wt = (wave >> 1) * (TT / 2);
 
-    // token staging: thread t copies 8 U4 halves of hi and of lo of token row t / TPR
-    const int xr = tid / TPR, xp = tid % TPR;
-    const long long xoff = (long long)tm.row(xr) * a.K + 8 * U4 * xp;
-    const _Float16 *hsrc = a.xh + xoff, *lsrc = a.xl + xoff;
+    // token staging: thread t copies BPT int8 values of token row t / TPR, and the scale of their block (the
+    // thread whose values start a block)
+    const int xr = tid / TPR, xp = tid % TPR, xb = BPT * xp / 32;
+    const bool xlead = BPT * xp % 32 == 0;
+    const int8_t *qsrc = a.xq + (long long)tm.row(xr) * a.K + BPT * xp;
+    const uint16_t *ssrc = (const uint16_t *)a.xs + (long long)tm.row(xr) * (a.K / 32) + xb;
 
     typename S::Raw raw;
-    uint4 hv0, hv1, hv2, hv3, lv0, lv1, lv2, lv3;  // (scalars: an array here ends up in scratch; U4 = 2 uses 0, 1)
+    uint4 qv0, qv1;  // (qv1: BPT = 32 only)
+    uint32_t sv;
 #define GSPLIT_ISSUE(k0)                                                \
     do {                                                                \
         S::load(W, a.row_bytes, a.N, n0, (k0), raw);                    \
-        const uint4 *h4 = (const uint4 *)(hsrc + (k0));                 \
-        const uint4 *l4 = (const uint4 *)(lsrc + (k0));                 \
-        hv0 = h4[0];                                                    \
-        hv1 = h4[1];                                                    \
-        lv0 = l4[0];                                                    \
-        lv1 = l4[1];                                                    \
-        if (U4 == 4) {                                                  \
-            hv2 = h4[2];                                                \
-            hv3 = h4[3];                                                \
-            lv2 = l4[2];                                                \
-            lv3 = l4[3];                                                \
-        }                                                               \
+        const uint4 *q4 = (const uint4 *)(qsrc + (k0));                 \
+        qv0 = q4[0];                                                    \
+        if (BPT == 32) qv1 = q4[1];                                     \
+        sv = ssrc[(k0) / 32];                                           \
     } while (0)
 
     f4 acc[8][NJ];
@@ -561,17 +554,10 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm_split(GemmArgs a) {
     for (int k0 = 0; k0 < a.K; k0 += GS_K) {
         __syncthreads();  // the previous stage's LDS reads are done (and the table is written)
         S::store(raw, lut, sW);
-        uint4 *hd = (uint4 *)(sH + xr * GS_ROW + 8 * U4 * xp), *ld = (uint4 *)(sL + xr * GS_ROW + 8 * U4 * xp);
-        hd[0] = hv0;
-        hd[1] = hv1;
-        ld[0] = lv0;
-        ld[1] = lv1;
-        if (U4 == 4) {
-            hd[2] = hv2;
-            hd[3] = hv3;
-            ld[2] = lv2;
-            ld[3] = lv3;
-        }
+        uint4 *qd = (uint4 *)(sQ + xr * QROW + BPT * xp);
+        qd[0] = qv0;
+        if (BPT == 32) qd[1] = qv1;
+        if (xlead) sD[xr * 2 + xb] = (uint16_t)sv;
         __syncthreads();
         if (k0 + GS_K < a.K) GSPLIT_ISSUE(k0 + GS_K);  // next stage's global loads in flight during the MFMAs
 
@@ -579,30 +565,41 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm_split(GemmArgs a) {
 #pragma unroll
         for (int b = 0; b < GS_K / 32; ++b) {
             const int kk = b * 32 + 8 * (lane >> 4);
-            h8 fh[NJ], fl[NJ];
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                fh[j] = *(const h8 *)(sH + (wt + 16 * j + (lane & 15)) * GS_ROW + kk);
-                fl[j] = *(const h8 *)(sL + (wt + 16 * j + (lane & 15)) * GS_ROW + kk);
-            }
             h8 fa[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) fa[i] = *(const h8 *)(sW + (wn + 16 * i + (lane & 15)) * GS_ROW + kk);
-            // (the four hi products of a weight fragment first: a lo product then finds its accumulator's hi result
-            // ready)
+            uint2 qq[NJ];
+            uint32_t ds[NJ];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-#pragma unroll
-                for (int j = 0; j < NJ; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fh[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-                for (int j = 0; j < NJ; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fl[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < NJ; ++j) {
+                const int row = wt + 16 * j + (lane & 15);
+                qq[j] = *(const uint2 *)(sQ + row * QROW + kk);
+                ds[j] = sD[row * 2 + b];
             }
-            // the block's fragment reads are issued before its MFMAs (left alone, the scheduler moves each weight
-            // fragment's read next to its first use and waits for it there)
-            __builtin_amdgcn_sched_group_barrier(0x100, 8 + 2 * NJ, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 16 * NJ, 0);
+            // per token tile: its hi and lo fragments from 8 int8 values and the block scale, then its 16 MFMAs (the
+            // next tile's conversion overlaps them); each accumulator takes the block's hi product, then its lo one
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const h2 dd = __builtin_bit_cast(h2, ds[j] | (ds[j] << 16));
+                uint32_t qh[4], hv[4], lv[4];
+                i8x4_to_h4(qq[j].x, qh[0], qh[1]);
+                i8x4_to_h4(qq[j].y, qh[2], qh[3]);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const h2 x = __builtin_bit_cast(h2, qh[c]);
+                    const h2 h = x * dd;
+                    hv[c] = __builtin_bit_cast(uint32_t, h);
+                    lv[c] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(x, dd, -h));
+                }
+                const h8 fh = __builtin_bit_cast(h8, make_uint4(hv[0], hv[1], hv[2], hv[3]));
+                const h8 fl = __builtin_bit_cast(h8, make_uint4(lv[0], lv[1], lv[2], lv[3]));
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fh, acc[i][j], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fl, acc[i][j], 0, 0, 0);
+            }
         }
         __builtin_amdgcn_s_setprio(0);
     }
@@ -643,10 +640,10 @@ int gemm_dense_token_tile(int type, int T) { return gemm_split(type) && T <= GS_
 
 int gemm_rows_per_wg(int type) { return gemm_split(type) ? GS_N : gemm_kquant(type) ? GEMM_KQ_ROWS : GB_N; }
 
-hipError_t launch_act_split(int type, const int8_t *q, const float *d, int T, int K, int rows, _Float16 *xh,
-                            _Float16 *xl, float *ts, hipStream_t stream) {
+hipError_t launch_act_split(int type, const int8_t *q, const float *d, int T, int K, int rows, int8_t *xq,
+                            _Float16 *xs, float *ts, hipStream_t stream) {
     hipLaunchKernelGGL(k_act_split, dim3((unsigned)rows), dim3(256), 0, stream, q, d, T, K,
-                       (type == TY_FP4 || type == TY_FAST) ? 1 : 0, xh, xl, ts);
+                       (type == TY_FP4 || type == TY_FAST) ? 1 : 0, xq, xs, ts);
     return hipGetLastError();
 }
 

@@ -74,7 +74,8 @@ struct GemmArgs {
     long long row_bytes;
     const _Float16 *xh;     // token operand [rows][K] (pre-pass); split GEMM: the hi plane
     const float *dx;        // block scales [rows][K / 32] (per-block GEMM)
-    const _Float16 *xl;     // split GEMM: the lo plane [rows][K]
+    const int8_t *xq;       // split GEMM: int8 token rows in the GEMM's K order [rows][K]
+    const _Float16 *xs;     // split GEMM: their block scales dx 2^s [rows][K / 32]
     const float *ts;        // split GEMM: per-row output factor 2^-s
     const _Float16 *xb;     // K-quant GEMM: the token's 16-value group sums [rows][K / 16] (dx: dK [rows][K / 256])
     float *y;
@@ -99,8 +100,8 @@ hipError_t launch_gemm(int type, const GemmArgs &a, dim3 grid, hipStream_t strea
 bool gemm_split(int type);
 int gemm_split_k_multiple();
 int gemm_rows_per_wg(int type);  // weight rows per GEMM workgroup (token tiles: gemm_token_tile())
-hipError_t launch_act_split(int type, const int8_t *q, const float *d, int T, int K, int rows, _Float16 *xh,
-                            _Float16 *xl, float *ts, hipStream_t stream);
+hipError_t launch_act_split(int type, const int8_t *q, const float *d, int T, int K, int rows, int8_t *xq,
+                            _Float16 *xs, float *ts, hipStream_t stream);
 hipError_t launch_gemm_split(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);
 // the K-quant GEMM (Q4_K, Q6_K): pre-pass of the Q8_K activation (`rows` rows, T real) and the kernel
 bool gemm_kquant(int type);

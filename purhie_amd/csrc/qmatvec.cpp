@@ -96,12 +96,14 @@ constexpr int ID_DECODE_TILE = 16;
 size_t align16z(size_t n) { return (n + 15) & ~(size_t)15; }
 
 // The GEMM's token operand in a stream-ordered allocation (freed on the same stream after the GEMM): for
-// ROCmFP4 / FAST the split planes hi, lo (fp16) and the per-row factors; for Q8_0 the int8 rows as fp16 and
+// ROCmFP4 / FAST the int8 rows in the GEMM's K order, their block scales times the row's power of two (fp16) and
+// the per-row factors; for Q8_0 the int8 rows as fp16 and
 // their block scales; for Q4_K / Q6_K the Q8_K rows as fp16, their group sums as fp16 and dK. `rows` rows are
 // converted (the first T from q, the rest zero: padding and the zero row MoE tiles point past their entries).
 struct TokWs {
     void *mem = nullptr;
-    _Float16 *xh = nullptr, *xl = nullptr, *xb = nullptr;
+    _Float16 *xh = nullptr, *xb = nullptr, *xs = nullptr;
+    int8_t *xq = nullptr;
     float *dx = nullptr, *ts = nullptr;
 };
 
@@ -117,12 +119,13 @@ hipError_t tokens_prep(int type, const qmatvec_q8 *q, int T, int K, int rows, To
         return launch_act_q8k(q->qK, q->dK, q->bsK, T, K, rows, w.xh, w.xb, w.dx, stream);
     }
     if (gemm_split(type)) {
-        hipError_t e = hipMallocAsync(&w.mem, 2 * plane + (size_t)rows * 4, stream);
+        const size_t vals = align16z((size_t)rows * K), scales = align16z((size_t)rows * (K / 32) * 2);
+        hipError_t e = hipMallocAsync(&w.mem, vals + scales + (size_t)rows * 4, stream);
         if (e != hipSuccess) return e;
-        w.xh = (_Float16 *)w.mem;
-        w.xl = (_Float16 *)((char *)w.mem + plane);
-        w.ts = (float *)((char *)w.mem + 2 * plane);
-        return launch_act_split(type, q->q0, q->d0, T, K, rows, w.xh, w.xl, w.ts, stream);
+        w.xq = (int8_t *)w.mem;
+        w.xs = (_Float16 *)((char *)w.mem + vals);
+        w.ts = (float *)((char *)w.mem + vals + scales);
+        return launch_act_split(type, q->q0, q->d0, T, K, rows, w.xq, w.xs, w.ts, stream);
     }
     hipError_t e = hipMallocAsync(&w.mem, plane + (size_t)rows * (K / 32) * 4, stream);
     if (e != hipSuccess) return e;
@@ -153,7 +156,8 @@ hipError_t gemm_dense(int type, const void *W, size_t row_bytes, const qmatvec_q
         a.row_bytes = (long long)row_bytes;
         a.xh = w.xh;
         a.dx = w.dx;
-        a.xl = w.xl;
+        a.xq = w.xq;
+        a.xs = w.xs;
         a.xb = w.xb;
         a.ts = w.ts;
         a.y = y;
@@ -494,7 +498,8 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
         a.row_bytes = (long long)row_bytes;
         a.xh = w.xh;
         a.dx = w.dx;
-        a.xl = w.xl;
+        a.xq = w.xq;
+        a.xs = w.xs;
         a.xb = w.xb;
         a.ts = w.ts;
         a.y = y;
