@@ -651,8 +651,9 @@ static hipError_t tile_id(const MvIdArgs &a, hipStream_t stream) {
     // sums on from the previous one, which keeps every row as aligned as the first when K % VALS == 0)
     const uint8_t *W[4] = {a.W[0], a.Wx[0], a.nmat > 1 ? a.W[1] : nullptr, a.nmat > 1 ? a.Wx[1] : nullptr};
     if (!tile_takes<TYPE>(a.K, 1, W, 4, a.row_bytes, a.q, a.d, a.bs)) return hipErrorNotSupported;
-    const long long blocks = a.n_tiles ? (long long)a.tile * a.max_tiles : (long long)a.n_used * a.nmat * a.T;
-    switch (tile_threads(a.K / Tu<TYPE>::VALS, (long long)a.N * blocks)) {
+    // (expert-indexed launches keep whole 256-thread tiles: every workgroup first reads its entry's expert id and
+    // stages its activation, and smaller tiles measured slower, e.g. config 4's expert down matvec 7.5 vs 6.0 us)
+    switch (tile_threads(a.K / Tu<TYPE>::VALS, 1ll << 40)) {
     case 64: return tile_id_thr<TYPE, 64>(a, stream);
     case 128: return tile_id_thr<TYPE, 128>(a, stream);
     default: return tile_id_thr<TYPE, 256>(a, stream);
