@@ -30,6 +30,7 @@ enum qt_type {
     QT_F16 = 1,
     QT_Q8_0 = 8,
     QT_Q4_K = 12,
+    QT_Q5_K = 13,
     QT_Q6_K = 14,
     QT_BF16 = 30,
     QT_Q4_0_ROCMFP4 = 100,

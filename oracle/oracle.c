@@ -94,7 +94,7 @@ int orc_block_size(int t) {
     switch (t) {
     case ORC_F32: case ORC_F16: case ORC_BF16: return 1;
     case ORC_Q8_0: case ORC_FP4: case ORC_FAST: return 32;
-    case ORC_Q4_K: case ORC_Q6_K: return 256;
+    case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: return 256;
     default: return 0;
     }
 }
@@ -107,6 +107,7 @@ int orc_type_size(int t) {
     case ORC_FP4: return 18;
     case ORC_FAST: return 17;
     case ORC_Q4_K: return 144;
+    case ORC_Q5_K: return 176;
     case ORC_Q6_K: return 210;
     default: return 0;
     }
@@ -133,6 +134,14 @@ static inline void k4_scale_min(int j, const uint8_t *q, int *sc, int *mn) {
 static inline int k4_level(const uint8_t *blk, int v) {
     const uint8_t b = blk[16 + 32 * (v >> 6) + (v & 31)];
     return (v & 32) ? (b >> 4) : (b & 0xf);
+}
+
+/* Q5_K level (0..31) of value v of a super-block (src/quant_types.cpp:290-314): Q4_K's nibble from ql (bytes
+ * 48..175) plus bit 2c (low nibble) or 2c + 1 (high nibble) of qh byte v % 32 (bytes 16..47) as bit 4 */
+static inline int k5_level(const uint8_t *blk, int v) {
+    const int c = v >> 6, hi = (v >> 5) & 1, l = v & 31;
+    const uint8_t b = blk[48 + 32 * c + l];
+    return (hi ? (b >> 4) : (b & 0xf)) | (((blk[16 + l] >> (2 * c + hi)) & 1) << 4);
 }
 
 /* Q6_K raw level (0..63) of value v of a super-block (src/quant_types.cpp:319-344): half h = v/128,
@@ -174,6 +183,20 @@ int orc_to_float(int t, const void *src, float *y, int64_t n) {
                 const float d2 = d * (float)sc, m2 = dmin * (float)mn;
                 for (int l = 0; l < 32; ++l) *y++ = d1 * (float)(b[16 + 32 * c + l] & 0xf) - m1;
                 for (int l = 0; l < 32; ++l) *y++ = d2 * (float)(b[16 + 32 * c + l] >> 4) - m2;
+            }
+        }
+        return 0;
+    case ORC_Q5_K:
+        for (int64_t i = 0; i < n / 256; ++i, b += 176) {
+            const float d = rd16(b), dmin = rd16(b + 2);
+            for (int c = 0; c < 4; ++c) {
+                int sc, mn;
+                k4_scale_min(2 * c, b + 4, &sc, &mn);
+                const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+                k4_scale_min(2 * c + 1, b + 4, &sc, &mn);
+                const float d2 = d * (float)sc, m2 = dmin * (float)mn;
+                for (int l = 0; l < 32; ++l) *y++ = d1 * (float)k5_level(b, 64 * c + l) - m1;
+                for (int l = 0; l < 32; ++l) *y++ = d2 * (float)k5_level(b, 64 * c + 32 + l) - m2;
             }
         }
         return 0;
@@ -307,56 +330,86 @@ static float qkx2(int n, int nmax, const float *x, const float *w, uint8_t *L, f
     return scale;
 }
 
-/* Q4_K (src/quantize.cpp:246-325): eight sub-block searches (weights av_x + |x|, rmin -1, 20 steps),
- * 6-bit scales / mins relative to the largest, fp16 d = max_scale / 63 and dmin = max_min / 63, then the
- * levels re-derived from the packed scales. */
+/* The K-quant super-block of Q4_K / Q5_K (src/quantize.cpp:246-307, kq_super_block): eight sub-block searches
+ * (weights av_x + |x|; Q4_K nmax 15, rmin -1, 20 steps; Q5_K nmax 31, rmin -0.5, 15 steps), 6-bit scales / mins
+ * relative to the largest packed into 12 bytes, fp16 d = max_scale / 63 and dmin = max_min / 63, then the levels
+ * re-derived from the packed scales, clamped to [0, nmax]. */
+static void kq_block(const float *x, int nmax, float rmin, int nstep, uint8_t *L, uint8_t *scl, uint16_t *hd,
+                     uint16_t *hm) {
+    uint8_t Laux[32];
+    float w[32], mins[8], scales[8];
+    float max_scale = 0, max_min = 0;
+    for (int j = 0; j < 8; ++j) {
+        float s2 = 0;
+        for (int l = 0; l < 32; ++l) s2 += x[32 * j + l] * x[32 * j + l];
+        const float av = sqrtf(s2 / 32);
+        for (int l = 0; l < 32; ++l) w[l] = av + fabsf(x[32 * j + l]);
+        scales[j] = qkx2(32, nmax, x + 32 * j, w, L + 32 * j, &mins[j], Laux, rmin, 0.1f, nstep);
+        if (scales[j] > max_scale) max_scale = scales[j];
+        if (mins[j] > max_min) max_min = mins[j];
+    }
+    const float inv_s = max_scale > 0 ? 63.f / max_scale : 0.f;
+    const float inv_m = max_min > 0 ? 63.f / max_min : 0.f;
+    memset(scl, 0, 12);
+    for (int j = 0; j < 8; ++j) {
+        uint8_t ls = (uint8_t)nint(inv_s * scales[j]);
+        uint8_t lm = (uint8_t)nint(inv_m * mins[j]);
+        if (ls > 63) ls = 63;
+        if (lm > 63) lm = 63;
+        if (j < 4) {
+            scl[j] = ls;
+            scl[j + 4] = lm;
+        } else {
+            scl[j + 4] = (uint8_t)((ls & 0xf) | ((lm & 0xf) << 4));
+            scl[j - 4] |= (uint8_t)((ls >> 4) << 6);
+            scl[j] |= (uint8_t)((lm >> 4) << 6);
+        }
+    }
+    *hd = orc_f32_to_f16(max_scale / 63.f);
+    *hm = orc_f32_to_f16(max_min / 63.f);
+    const float fd = orc_f16_to_f32(*hd), fm = orc_f16_to_f32(*hm);
+    for (int j = 0; j < 8; ++j) {
+        int sc, mn;
+        k4_scale_min(j, scl, &sc, &mn);
+        const float d = fd * (float)sc;
+        if (d == 0.0f) continue;
+        const float dm = fm * (float)mn;
+        for (int i = 0; i < 32; ++i) L[32 * j + i] = (uint8_t)clampi(nint((x[32 * j + i] + dm) / d), 0, nmax);
+    }
+}
+
+/* Q4_K (src/quantize.cpp:309-325): d, dmin, scales, then chunk c's 32 bytes hold values 64 c + l (low nibble)
+ * and 64 c + 32 + l (high nibble) */
 static void enc_q4_k(const float *x, uint8_t *out, int64_t k) {
     for (int64_t b = 0; b < k / 256; ++b, x += 256, out += 144) {
-        uint8_t L[256], Laux[32];
-        float w[32], mins[8], scales[8];
-        float max_scale = 0, max_min = 0;
-        for (int j = 0; j < 8; ++j) {
-            float s2 = 0;
-            for (int l = 0; l < 32; ++l) s2 += x[32 * j + l] * x[32 * j + l];
-            const float av = sqrtf(s2 / 32);
-            for (int l = 0; l < 32; ++l) w[l] = av + fabsf(x[32 * j + l]);
-            scales[j] = qkx2(32, 15, x + 32 * j, w, L + 32 * j, &mins[j], Laux, -1.0f, 0.1f, 20);
-            if (scales[j] > max_scale) max_scale = scales[j];
-            if (mins[j] > max_min) max_min = mins[j];
-        }
-        const float inv_s = max_scale > 0 ? 63.f / max_scale : 0.f;
-        const float inv_m = max_min > 0 ? 63.f / max_min : 0.f;
-        uint8_t *scl = out + 4;
-        memset(scl, 0, 12);
-        for (int j = 0; j < 8; ++j) {
-            uint8_t ls = (uint8_t)nint(inv_s * scales[j]);
-            uint8_t lm = (uint8_t)nint(inv_m * mins[j]);
-            if (ls > 63) ls = 63;
-            if (lm > 63) lm = 63;
-            if (j < 4) {
-                scl[j] = ls;
-                scl[j + 4] = lm;
-            } else {
-                scl[j + 4] = (uint8_t)((ls & 0xf) | ((lm & 0xf) << 4));
-                scl[j - 4] |= (uint8_t)((ls >> 4) << 6);
-                scl[j] |= (uint8_t)((lm >> 4) << 6);
-            }
-        }
-        const uint16_t hd = orc_f32_to_f16(max_scale / 63.f), hm = orc_f32_to_f16(max_min / 63.f);
+        uint8_t L[256];
+        uint16_t hd, hm;
+        kq_block(x, 15, -1.0f, 20, L, out + 4, &hd, &hm);
         memcpy(out, &hd, 2);
         memcpy(out + 2, &hm, 2);
-        const float fd = orc_f16_to_f32(hd), fm = orc_f16_to_f32(hm);
-        for (int j = 0; j < 8; ++j) {
-            int sc, mn;
-            k4_scale_min(j, scl, &sc, &mn);
-            const float d = fd * (float)sc;
-            if (d == 0.0f) continue;
-            const float dm = fm * (float)mn;
-            for (int i = 0; i < 32; ++i) L[32 * j + i] = (uint8_t)clampi(nint((x[32 * j + i] + dm) / d), 0, 15);
-        }
         uint8_t *q = out + 16;
         for (int c = 0; c < 4; ++c)
             for (int l = 0; l < 32; ++l) q[32 * c + l] = (uint8_t)(L[64 * c + l] | (L[64 * c + 32 + l] << 4));
+    }
+}
+
+/* Q5_K (src/quantize.cpp:327-358): as Q4_K with 5-bit levels; the low 4 bits as Q4_K's nibbles (ql, bytes
+ * 48..175), bit 4 of value 64 c + l in qh byte l bit 2 c, of value 64 c + 32 + l in bit 2 c + 1 (bytes 16..47) */
+static void enc_q5_k(const float *x, uint8_t *out, int64_t k) {
+    for (int64_t b = 0; b < k / 256; ++b, x += 256, out += 176) {
+        uint8_t L[256];
+        uint16_t hd, hm;
+        kq_block(x, 31, -0.5f, 15, L, out + 4, &hd, &hm);
+        memcpy(out, &hd, 2);
+        memcpy(out + 2, &hm, 2);
+        uint8_t *qh = out + 16, *ql = out + 48;
+        memset(qh, 0, 32);
+        for (int c = 0; c < 4; ++c)
+            for (int l = 0; l < 32; ++l) {
+                const int l1 = L[64 * c + l], l2 = L[64 * c + 32 + l];
+                qh[l] |= (uint8_t)(((l1 >> 4) << (2 * c)) | ((l2 >> 4) << (2 * c + 1)));
+                ql[32 * c + l] = (uint8_t)((l1 & 0xf) | ((l2 & 0xf) << 4));
+            }
     }
 }
 
@@ -578,6 +631,7 @@ static void enc_row(int t, const float *x, uint8_t *y, int64_t k) {
     case ORC_F16: for (int64_t i = 0; i < k; ++i) { const uint16_t h = orc_f32_to_f16(x[i]); memcpy(y + 2 * i, &h, 2); } break;
     case ORC_Q8_0: enc_q8_0(x, y, k); break;
     case ORC_Q4_K: enc_q4_k(x, y, k); break;
+    case ORC_Q5_K: enc_q5_k(x, y, k); break;
     case ORC_Q6_K: enc_q6_k(x, y, k); break;
     case ORC_FP4: enc_fp4(x, y, k); break;
     case ORC_FAST: enc_fast(x, y, k); break;
@@ -707,7 +761,7 @@ void orc_quantize_q8_k(const float *x, int64_t k, int8_t *qK, float *dK, int32_t
 
 int orc_group_size(int t) {
     switch (t) {
-    case ORC_Q8_0: case ORC_FAST: case ORC_Q4_K: return 32;
+    case ORC_Q8_0: case ORC_FAST: case ORC_Q4_K: case ORC_Q5_K: return 32;
     case ORC_FP4: case ORC_Q6_K: return 16;
     default: return 0;
     }
@@ -729,6 +783,7 @@ static inline int raw_level(int t, const uint8_t *row, int v) {
         return k_cb[j < 16 ? (b[j] & 0xf) : (b[j - 16] >> 4)];
     }
     case ORC_Q4_K: return k4_level(row + 144 * (v >> 8), v & 255);
+    case ORC_Q5_K: return k5_level(row + 176 * (v >> 8), v & 255);
     case ORC_Q6_K: return k6_level(row + 210 * (v >> 8), v & 255);
     }
     return 0;
@@ -756,6 +811,7 @@ int orc_block_dots(int t, const void *W, size_t rb, int N, int K, const int8_t *
  *   FP4   (e0 * dx) * s0 + (e1 * dx) * s1            src/matvec_q.hip:1310-1327 (P4ROCmFP4::block)
  *   FAST  (e * dx) * (s0 + s1)                       src/matvec_q.hip:1492-1502, src/expert_cpu.cpp:50-63
  *   Q4_K  per 8 lanes of 16 bytes: (d * dx) * isum - (dmin * dx) * msum     src/matvec_q.hip:1752-1789
+ *   Q5_K  the same with 5-bit levels (qh bit 2c / 2c + 1 as bit 4)           src/matvec_q.hip:1752-1789,1928-1930
  *   Q6_K  per 8 lanes of 16 bytes: (d * dx) * (isum - 32 * offs)            src/matvec_q.hip:1716-1750 */
 static float row_q8(int t, const uint8_t *row, int K, const int8_t *q, const float *d, const int32_t *bs,
                     double *mag) {
@@ -792,18 +848,20 @@ static float row_q8(int t, const uint8_t *row, int K, const int8_t *q, const flo
             acc += term;
             m += fabs((double)term);
         }
-    } else if (t == ORC_Q4_K) {
+    } else if (t == ORC_Q4_K || t == ORC_Q5_K) {
+        const int q5 = t == ORC_Q5_K, BY = q5 ? 176 : 144;
         for (int ib = 0; ib < K / 256; ++ib) {
-            const uint8_t *b = row + 144 * ib;
+            const uint8_t *b = row + BY * ib;
             const int8_t *xb = q + 256 * ib;
             const float dw = rd16(b), dm = rd16(b + 2), dx = d[ib];
-            for (int s = 0; s < 8; ++s) {      /* lane s: qs bytes 16 s .. 16 s + 15 */
+            for (int s = 0; s < 8; ++s) {      /* lane s: 16 bytes of chunk s / 2 */
                 const int c = s >> 1, l = (s & 1) * 16;
                 int slo = 0, shi = 0;
                 for (int i = 0; i < 16; ++i) {
-                    const uint8_t v = b[16 + 32 * c + l + i];
-                    slo += (v & 0xf) * xb[64 * c + l + i];
-                    shi += (v >> 4) * xb[64 * c + 32 + l + i];
+                    const int vlo = q5 ? k5_level(b, 64 * c + l + i) : k4_level(b, 64 * c + l + i);
+                    const int vhi = q5 ? k5_level(b, 64 * c + 32 + l + i) : k4_level(b, 64 * c + 32 + l + i);
+                    slo += vlo * xb[64 * c + l + i];
+                    shi += vhi * xb[64 * c + 32 + l + i];
                 }
                 int sc1, m1, sc2, m2, sm, mm;
                 k4_scale_min(2 * c, b + 4, &sc1, &m1);
@@ -859,7 +917,7 @@ typedef struct {
 
 static void mv_span(void *p, int64_t r0, int64_t r1) {
     mv_ctx *c = (mv_ctx *)p;
-    const int kq = c->t == ORC_Q4_K || c->t == ORC_Q6_K;
+    const int kq = c->t == ORC_Q4_K || c->t == ORC_Q5_K || c->t == ORC_Q6_K;
     float *wf = c->ref ? (float *)malloc((size_t)c->K * 4) : NULL;
     for (int64_t n = r0; n < r1; ++n) {
         const uint8_t *row = c->W + (size_t)n * c->rb;

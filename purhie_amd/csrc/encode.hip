@@ -1,8 +1,8 @@
-// encode.hip -- the weight encoders on the GPU: fp32 rows -> GGUF blocks (Q8_0, Q4_K, Q6_K, ROCmFP4,
+// encode.hip -- the weight encoders on the GPU: fp32 rows -> GGUF blocks (Q8_0, Q4_K, Q5_K, Q6_K, ROCmFP4,
 // ROCmFP4_FAST) and F32 / F16 / BF16 rows, bit-identical to the reference's CPU encoders (src/quantize.cpp:
-// 28-64, 161-330, 362-476, 975-1109), which reproduce ggml's _ref quantizers and ROCmFPX's rocmfp4.c.
+// 28-64, 161-358, 362-476, 975-1109), which reproduce ggml's _ref quantizers and ROCmFPX's rocmfp4.c.
 //
-// One thread per block (Q8_0, ROCmFP4, FAST: 32 values) or super-block (Q4_K, Q6_K: 256 values). The
+// One thread per block (Q8_0, ROCmFP4, FAST: 32 values) or super-block (K-quants: 256 values). The
 // searches are the reference's, step for step, in single precision: this file is compiled without
 // floating-point contraction (a fused multiply-add rounds a sum of squares differently and can pick
 // another scale on a tie), divisions and square roots are IEEE-rounded (hipcc's default), and nothing is
@@ -74,12 +74,14 @@ __device__ void enc_q8_0_block(const float *x, uint8_t *out) {
     for (int j = 0; j < 32; ++j) out[2 + j] = (uint8_t)(int8_t)roundf(x[j] * id);
 }
 
-// ---------------------------------------------------------------- Q4_K (src/quantize.cpp:169-325)
+// ---------------------------------------------------------------- Q4_K / Q5_K (src/quantize.cpp:169-358)
 
-// the asymmetric scale / min search of one 32-value sub-block: returns the scale, *neg_min = -min
-__device__ float make_qkx2(const float *x, const float *w, uint8_t *L, float *neg_min) {
-    constexpr int n = 32, nmax = 15, nstep = 20;
-    constexpr float rmin = -1.0f, rdelta = 0.1f;
+// the asymmetric scale / min search of one 32-value sub-block: returns the scale, *neg_min = -min (Q4_K: nmax
+// 15, rmin -1, 20 steps; Q5_K: nmax 31, rmin -0.5, 15 steps)
+template <int nmax, int nstep>
+__device__ float make_qkx2(const float *x, const float *w, uint8_t *L, float *neg_min, float rmin) {
+    constexpr int n = 32;
+    constexpr float rdelta = 0.1f;
     uint8_t Laux[32];
     float lo = x[0], hi = x[0];
     float sw = w[0];
@@ -140,8 +142,9 @@ __device__ float make_qkx2(const float *x, const float *w, uint8_t *L, float *ne
     return scale;
 }
 
-__device__ void enc_q4_k_block(const float *x, uint8_t *out) {
-    uint8_t L[256];
+// the super-block's levels L (0..nmax), its packed scales and mins (bytes 4..15) and d, dmin (bytes 0..3)
+template <int nmax, int nstep>
+__device__ void enc_kq_levels(const float *x, uint8_t *out, uint8_t *L, float rmin) {
     float w[32], mins[8], scales[8];
     float max_scale = 0, max_min = 0;
     for (int j = 0; j < 8; ++j) {
@@ -149,7 +152,7 @@ __device__ void enc_q4_k_block(const float *x, uint8_t *out) {
         for (int l = 0; l < 32; ++l) s2 += x[32 * j + l] * x[32 * j + l];
         const float av = sqrtf(s2 / 32);
         for (int l = 0; l < 32; ++l) w[l] = av + fabsf(x[32 * j + l]);
-        scales[j] = make_qkx2(x + 32 * j, w, L + 32 * j, &mins[j]);
+        scales[j] = make_qkx2<nmax, nstep>(x + 32 * j, w, L + 32 * j, &mins[j], rmin);
         if (scales[j] > max_scale) max_scale = scales[j];
         if (mins[j] > max_min) max_min = mins[j];
     }
@@ -190,11 +193,31 @@ __device__ void enc_q4_k_block(const float *x, uint8_t *out) {
         const float d = fd * (float)sc;
         if (d == 0.0f) continue;
         const float dm = fm * (float)mn;
-        for (int i = 0; i < 32; ++i) L[32 * j + i] = (uint8_t)clampi(nearest((x[32 * j + i] + dm) / d), 0, 15);
+        for (int i = 0; i < 32; ++i) L[32 * j + i] = (uint8_t)clampi(nearest((x[32 * j + i] + dm) / d), 0, nmax);
     }
+}
+
+__device__ void enc_q4_k_block(const float *x, uint8_t *out) {
+    uint8_t L[256];
+    enc_kq_levels<15, 20>(x, out, L, -1.0f);
     uint8_t *q = out + 16;
     for (int c = 0; c < 4; ++c)
         for (int l = 0; l < 32; ++l) q[32 * c + l] = (uint8_t)(L[64 * c + l] | (L[64 * c + 32 + l] << 4));
+}
+
+// Q5_K: the low 4 bits as Q4_K's nibbles (bytes 48..175), bit 4 of value 64 c + l in qh byte l bit 2 c, of value
+// 64 c + 32 + l in bit 2 c + 1 (bytes 16..47)
+__device__ void enc_q5_k_block(const float *x, uint8_t *out) {
+    uint8_t L[256];
+    enc_kq_levels<31, 15>(x, out, L, -0.5f);
+    uint8_t *qh = out + 16, *ql = out + 48;
+    for (int l = 0; l < 32; ++l) {
+        uint32_t h = 0;
+        for (int c = 0; c < 4; ++c) h |= (uint32_t)((L[64 * c + l] >> 4) << (2 * c)) | ((L[64 * c + 32 + l] >> 4) << (2 * c + 1));
+        qh[l] = (uint8_t)h;
+    }
+    for (int c = 0; c < 4; ++c)
+        for (int l = 0; l < 32; ++l) ql[32 * c + l] = (uint8_t)((L[64 * c + l] & 0xf) | ((L[64 * c + 32 + l] & 0xf) << 4));
 }
 
 // ---------------------------------------------------------------- Q6_K (src/quantize.cpp:362-476)
@@ -413,8 +436,13 @@ __device__ void enc_fast_block(const float *x, uint8_t *out) {
 template <int TYPE>
 __global__ void __launch_bounds__(256) k_encode(const float *__restrict__ x, uint8_t *__restrict__ y, long long nrows,
                                                 long long ncols, long long row_bytes) {
-    constexpr int VALS = (TYPE == TY_Q4_K || TYPE == TY_Q6_K) ? 256 : 32;
-    constexpr int BYTES = TYPE == TY_Q8_0 ? 34 : TYPE == TY_Q4_K ? 144 : TYPE == TY_Q6_K ? 210 : TYPE == TY_FP4 ? 18 : 17;
+    constexpr int VALS = (TYPE == TY_Q4_K || TYPE == TY_Q5_K || TYPE == TY_Q6_K) ? 256 : 32;
+    constexpr int BYTES = TYPE == TY_Q8_0   ? 34
+                          : TYPE == TY_Q4_K ? 144
+                          : TYPE == TY_Q5_K ? 176
+                          : TYPE == TY_Q6_K ? 210
+                          : TYPE == TY_FP4  ? 18
+                                            : 17;
     const long long per_row = ncols / VALS;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nrows * per_row) return;
@@ -423,6 +451,7 @@ __global__ void __launch_bounds__(256) k_encode(const float *__restrict__ x, uin
     uint8_t *dst = y + r * row_bytes + b * BYTES;
     if (TYPE == TY_Q8_0) enc_q8_0_block(src, dst);
     else if (TYPE == TY_Q4_K) enc_q4_k_block(src, dst);
+    else if (TYPE == TY_Q5_K) enc_q5_k_block(src, dst);
     else if (TYPE == TY_Q6_K) enc_q6_k_block(src, dst);
     else if (TYPE == TY_FP4) enc_fp4_block(src, dst);
     else enc_fast_block(src, dst);
@@ -441,7 +470,7 @@ int encode_block_values(int type) {
     switch (type) {
     case 0: case 1: case 30: return 1;
     case TY_Q8_0: case TY_FP4: case TY_FAST: return 32;
-    case TY_Q4_K: case TY_Q6_K: return 256;
+    case TY_Q4_K: case TY_Q5_K: case TY_Q6_K: return 256;
     }
     return 0;
 }
@@ -459,6 +488,7 @@ hipError_t launch_encode(int type, const float *x, uint8_t *y, long long nrows, 
     case 30: hipLaunchKernelGGL(k_encode_float, grid, dim3(256), 0, stream, x, y, n, 2); break;
     case TY_Q8_0: hipLaunchKernelGGL(k_encode<TY_Q8_0>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes); break;
     case TY_Q4_K: hipLaunchKernelGGL(k_encode<TY_Q4_K>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes); break;
+    case TY_Q5_K: hipLaunchKernelGGL(k_encode<TY_Q5_K>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes); break;
     case TY_Q6_K: hipLaunchKernelGGL(k_encode<TY_Q6_K>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes); break;
     case TY_FP4: hipLaunchKernelGGL(k_encode<TY_FP4>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes); break;
     case TY_FAST: hipLaunchKernelGGL(k_encode<TY_FAST>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes); break;

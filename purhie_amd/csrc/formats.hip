@@ -52,6 +52,20 @@ __global__ void k_dequant(int type, const uint8_t *__restrict__ src, float *__re
         for (int l = 0; l < 32; ++l) o[l] = d1 * (float)((j & 1) ? (q[l] >> 4) : (q[l] & 0xf)) - m1;
         break;
     }
+    case TY_Q5_K: {  // Q4_K's nibble plus bit 2 (j / 2) + (j & 1) of qh byte l as bit 4 (src/quant_types.cpp:290-314)
+        const uint8_t *b = src + (g >> 3) * 176;
+        const int j = (int)(g & 7);
+        const uint32_t sc3[3] = {*(const uint32_t *)(b + 4), *(const uint32_t *)(b + 8), *(const uint32_t *)(b + 12)};
+        int sc, mn;
+        k4_scale_min(sc3, j, sc, mn);
+        const float d1 = rd16(b) * (float)sc, m1 = rd16(b + 2) * (float)mn;
+        const uint8_t *q = b + 48 + 32 * (j >> 1);
+        for (int l = 0; l < 32; ++l) {
+            const int lv = ((j & 1) ? (q[l] >> 4) : (q[l] & 0xf)) | (((b[16 + l] >> j) & 1) << 4);
+            o[l] = d1 * (float)lv - m1;
+        }
+        break;
+    }
     case TY_Q6_K: {
         const uint8_t *b = src + (g >> 3) * 210;
         const int part = (int)(g & 7);  // values 32 part .. 32 part + 31
@@ -91,6 +105,7 @@ namespace {
 
 void to_float_sync_q8_0(const void *s, float *d, int64_t n) { (void)qt_to_float(TY_Q8_0, s, d, n); }
 void to_float_sync_q4_k(const void *s, float *d, int64_t n) { (void)qt_to_float(TY_Q4_K, s, d, n); }
+void to_float_sync_q5_k(const void *s, float *d, int64_t n) { (void)qt_to_float(TY_Q5_K, s, d, n); }
 void to_float_sync_q6_k(const void *s, float *d, int64_t n) { (void)qt_to_float(TY_Q6_K, s, d, n); }
 void to_float_sync_fp4(const void *s, float *d, int64_t n) { (void)qt_to_float(QT_Q4_0_ROCMFP4, s, d, n); }
 void to_float_sync_fast(const void *s, float *d, int64_t n) { (void)qt_to_float(QT_Q4_0_ROCMFP4_FAST, s, d, n); }
@@ -104,6 +119,7 @@ const qt_traits k_traits[] = {
     {QT_F16, "f16", 1, 2, to_float_sync_f16, 1},
     {TY_Q8_0, "q8_0", 32, 34, to_float_sync_q8_0, 1},
     {TY_Q4_K, "q4_K", 256, 144, to_float_sync_q4_k, 1},
+    {TY_Q5_K, "q5_K", 256, 176, to_float_sync_q5_k, 1},
     {TY_Q6_K, "q6_K", 256, 210, to_float_sync_q6_k, 1},
     {QT_BF16, "bf16", 1, 2, to_float_sync_bf16, 1},
     {QT_Q4_0_ROCMFP4, "q4_0_rocmfp4", 32, 18, to_float_sync_fp4, 1},
@@ -135,7 +151,7 @@ size_t qt_row_size(int type, int64_t ne0) {
     return (size_t)(ne0 / t->blck_size) * (size_t)t->type_size;
 }
 
-int qt_vec_dot_q8k(int type) { return type == TY_Q4_K || type == TY_Q6_K; }
+int qt_vec_dot_q8k(int type) { return type == TY_Q4_K || type == TY_Q5_K || type == TY_Q6_K; }
 
 float qt_fp16_to_fp32(uint16_t h) {
     const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;

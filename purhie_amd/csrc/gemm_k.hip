@@ -1,4 +1,4 @@
-// gemm_k.hip -- the prefill GEMM Y[t][n] = sum_k W[n][k] X[t][k] for the K-quant formats (Q4_K, Q6_K) on
+// gemm_k.hip -- the prefill GEMM Y[t][n] = sum_k W[n][k] X[t][k] for the K-quant formats (Q4_K, Q5_K, Q6_K) on
 // gfx950 MFMA, dense and over MoE expert tiles. Replaces the reference's K-quant WMMA GEMM (matmul_wmma_q4_K /
 // _q6_K and their _id forms: wmma_q8k, WStageK, src/matvec_q.hip:2975-3348), which reads Q8_K activations
 // and applies d_x (d_w isum - dmin msum) to exact integer tile sums.
@@ -121,6 +121,56 @@ struct KStage<TY_Q4_K> {
     }
 };
 
+// Q5_K (176-byte super-block, 16-byte aligned: Q4_K's header, qh[32] @16, qs[128] @48): as Q4_K, with bit j of qh
+// byte l as bit 4 of sub-block j's value l. sc q reaches 63 * 31 = 1953, past the 1024-value window of
+// scaled_nibbles, so the low nibble and the high bit go through it apart (sc q_lo <= 945, sc 16 <= 1008) and are
+// added in fp16 (exact: integers below 2048).
+template <>
+struct KStage<TY_Q5_K> {
+    static constexpr int PLANES = 1, BB = 176;
+    struct Raw {
+        uint4 h, h0, h1, q0, q1;
+    };
+    __device__ static void load(const uint8_t *W, long long rb, int N, int n0, int s, int c, Raw &r) {
+        const int row = n0 + (threadIdx.x >> 1);
+        const int rr = row < N ? row : N - 1;
+        const uint8_t *b = W + (long long)rr * rb + (long long)s * BB;
+        r.h = *(const uint4 *)b;
+        r.h0 = *(const uint4 *)(b + 16);
+        r.h1 = *(const uint4 *)(b + 32);
+        r.q0 = *(const uint4 *)(b + 48 + 32 * c);
+        r.q1 = *(const uint4 *)(b + 64 + 32 * c);
+    }
+    __device__ static void store(const Raw &r, int c, _Float16 *sW, _Float16 *sG, float2 *sD) {
+        const int row = threadIdx.x >> 1, p = threadIdx.x & 1, j = 2 * c + p;
+        const uint32_t s3[3] = {r.h.y, r.h.z, r.h.w};
+        int sc0, mn0, sc1, mn1;
+        k4_scale_min(s3, 2 * c, sc0, mn0);
+        k4_scale_min(s3, 2 * c + 1, sc1, mn1);
+        const uint32_t sc = (uint32_t)(p ? sc1 : sc0);
+        const _Float16 mn = (_Float16)(float)(p ? mn1 : mn0);
+        const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        const uint32_t qh[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+        uint32_t o[16];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            uint32_t a01, a23, b01, b23;
+            scaled_nibbles((q[k] >> (4 * p)) & 0x0f0f0f0fu, sc, a01, a23);
+            scaled_nibbles(((qh[k] >> j) & 0x01010101u) << 4, sc, b01, b23);
+            o[2 * k] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a01) + __builtin_bit_cast(h2, b01));
+            o[2 * k + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a23) + __builtin_bit_cast(h2, b23));
+        }
+        uint4 *d4 = (uint4 *)(sW + row * GK_ROW + 32 * p);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) d4[m] = make_uint4(o[4 * m], o[4 * m + 1], o[4 * m + 2], o[4 * m + 3]);
+        h2 mm;
+        mm.x = mn;
+        mm.y = mn;
+        *(h2 *)(sG + row * GK_G + 4 * c + 2 * p) = mm;
+        if (p == 0) sD[row] = make_float2(h2f(r.h.x & 0xffffu), h2f(r.h.x >> 16));
+    }
+};
+
 // Q6_K (210-byte super-block, 2-byte aligned: ql[128], qh[64] @128, sc[16] @192, d @208). Values 128 h + 32 i + l
 // (h = 0, 1; i = 0..3; l < 32): ql byte 64 h + 32 (i & 1) + l, nibble i >> 1; qh byte 128 + 32 h + l, bits 2 i;
 // scale sc[(128 h + 32 i + l) / 16]. Stage c is h = c >> 1, i = 2 (c & 1) + p for thread parity p. The runs of
@@ -185,7 +235,7 @@ struct KStage<TY_Q6_K> {
 template <int TYPE>
 __global__ void __launch_bounds__(GK_THREADS, 2) k_gemm_kq(GemmArgs a) {
     using S = KStage<TYPE>;
-    constexpr bool MINS = TYPE == TY_Q4_K;
+    constexpr bool MINS = TYPE == TY_Q4_K || TYPE == TY_Q5_K;
     constexpr int PL = S::PLANES;
     __shared__ __attribute__((aligned(16))) _Float16 sW[PL * GK_N * GK_ROW];
     __shared__ __attribute__((aligned(16))) _Float16 sX[GK_T * GK_ROW];
@@ -342,7 +392,7 @@ __global__ void __launch_bounds__(GK_THREADS, 2) k_gemm_kq(GemmArgs a) {
 
 // ---------------------------------------------------------------- host launchers
 
-bool gemm_kquant(int type) { return type == TY_Q4_K || type == TY_Q6_K; }
+bool gemm_kquant(int type) { return type == TY_Q4_K || type == TY_Q5_K || type == TY_Q6_K; }
 
 hipError_t launch_act_q8k(const int8_t *q, const float *dK, const int32_t *bs, int T, int K, int rows, _Float16 *xh,
                           _Float16 *xb, float *xd, hipStream_t stream) {
@@ -353,6 +403,7 @@ hipError_t launch_act_q8k(const int8_t *q, const float *dK, const int32_t *bs, i
 hipError_t launch_gemm_kquant(int type, const GemmArgs &a, dim3 grid, hipStream_t stream) {
     switch (type) {
     case TY_Q4_K: hipLaunchKernelGGL(k_gemm_kq<TY_Q4_K>, grid, dim3(GK_THREADS), 0, stream, a); break;
+    case TY_Q5_K: hipLaunchKernelGGL(k_gemm_kq<TY_Q5_K>, grid, dim3(GK_THREADS), 0, stream, a); break;
     case TY_Q6_K: hipLaunchKernelGGL(k_gemm_kq<TY_Q6_K>, grid, dim3(GK_THREADS), 0, stream, a); break;
     default: return hipErrorInvalidDeviceFunction;
     }

@@ -220,21 +220,24 @@ struct Mv<TY_FAST> {
 // and 64 c + 32 + l + 0..15 (high nibbles, sub-block 2c + 1), l = 16 (s & 1); plus the block header
 // (d, dmin, the 12 scale bytes). The lane with quarter s also applies sub-block s's min through the Q8_K
 // group sums 2 s, 2 s + 1 (reference src/matvec_q.hip:1752-1789). A lane's quarter s is fixed (L % 8 == 0).
-template <>
-struct Mv<TY_Q4_K> {
+// Q5_K (176 bytes, 16-aligned) has qh (bytes 16..47) before qs (48..175): the lane also loads qh bytes
+// 16 (s & 1) .. + 15, whose bit 2 c (low nibbles) and 2 c + 1 (high nibbles) are the levels' bit 4.
+template <bool Q5>
+struct MvKq {
     static constexpr int ACT_BLK = 256;
     static constexpr bool KQ = true;
     __host__ __device__ static int tasks(int K) { return K / 256 * 8; }
-    static constexpr int LDIV = 8, W_UNIT = 144, X_UNIT = 256, D_UNIT = 1, B_UNIT = 16;
+    static constexpr int LDIV = 8, W_UNIT = Q5 ? 176 : 144, X_UNIT = 256, D_UNIT = 1, B_UNIT = 16;
     static constexpr int U = 6;  // 8 dwords each
     // 6-bit scales of sub-blocks 2c, 2c + 1 and the min of sub-block s from the scale dwords y, z, w
     // (bytes 4..15 of the block), gathered with v_perm_b32 using the lane's selectors:
     //   scales: (perm(w, y, p) & pmask) | ((perm(w, y, q) >> 6) & 0x0303) << 4
     //   min:    ((perm(w, z, m) >> msh) & mmask) | ((perm(w, z, n) >> 6) & 3) << 4
     struct Lane {
-        uint32_t p, pmask, q, m, msh, mmask, n;
+        uint32_t p, pmask, q, m, msh, mmask, n, hsh;
         __device__ Lane(int gl) {
             const int s = gl & 7, c = s >> 1;
+            hsh = (uint32_t)(2 * c);
             if (c < 2) {  // sub-blocks 2c, 2c + 1 < 4: scale = byte j & 63 (y)
                 p = (uint32_t)(2 * c) | (uint32_t)(2 * c + 1) << 8 | 0x0c0c0000u;
                 pmask = 0x3f3fu;
@@ -259,7 +262,7 @@ struct Mv<TY_Q4_K> {
             }
         }
     };
-    __device__ static long long wbase(int gl) { return 144LL * (gl >> 3); }
+    __device__ static long long wbase(int gl) { return (long long)W_UNIT * (gl >> 3); }
     __device__ static int xoff(int gl) {
         const int s = gl & 7;
         return 256 * (gl >> 3) + 64 * (s >> 1) + 16 * (s & 1);
@@ -267,12 +270,13 @@ struct Mv<TY_Q4_K> {
     __device__ static int doff(int gl) { return gl >> 3; }
     __device__ static int boff(int gl) { return 16 * (gl >> 3) + 2 * (gl & 7); }
     struct Raw {
-        u32x4 h, qs;
+        u32x4 h, qs, qh;
     };
-    // the task's block header and its quarter s of qs; p = the block header of the lane's current task
+    // the task's block header and its quarter s of qs (and of qh); p = the block header of the lane's current task
     __device__ static void load(const uint8_t *p, Raw &r, int s) {
         r.h = ld128_nt(p);
-        r.qs = ld128_nt(p + 16 + 16 * s);
+        r.qs = ld128_nt(p + (Q5 ? 48 : 16) + 16 * s);
+        if (Q5) r.qh = ld128_nt(p + 16 + 16 * (s & 1));
     }
     template <int NT>
     __device__ static void compute(const Raw &r, const Lane &o, const Act<NT> &x, int xo, int dof, int bo,
@@ -287,8 +291,14 @@ struct Mv<TY_Q4_K> {
         int lo[4], hi[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            lo[k] = (int)(q[k] & 0x0f0f0f0fu);
-            hi[k] = (int)((q[k] >> 4) & 0x0f0f0f0fu);
+            uint32_t l4 = q[k] & 0x0f0f0f0fu, h4 = (q[k] >> 4) & 0x0f0f0f0fu;
+            if (Q5) {
+                const uint32_t qh = k == 0 ? r.qh.x : k == 1 ? r.qh.y : k == 2 ? r.qh.z : r.qh.w;
+                l4 |= ((qh >> o.hsh) & 0x01010101u) << 4;
+                h4 |= ((qh >> (o.hsh + 1)) & 0x01010101u) << 4;
+            }
+            lo[k] = (int)l4;
+            hi[k] = (int)h4;
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
@@ -311,6 +321,10 @@ struct Mv<TY_Q4_K> {
         }
     }
 };
+template <>
+struct Mv<TY_Q4_K> : MvKq<false> {};
+template <>
+struct Mv<TY_Q5_K> : MvKq<true> {};
 
 // Q6_K: a task is one of the 8 quarters s of a 210-byte super-block (2-aligned): half h = s / 4, ql bytes
 // 64 h + r .. + 15 (r = 16 (s & 3)) and qh bytes 128 + 32 h + (r & 31) .. + 15, loaded as realigned
@@ -400,7 +414,7 @@ struct Mv<TY_Q6_K> {
 template <int TYPE>
 __device__ __forceinline__ void load_task(const uint8_t *p, typename Mv<TYPE>::Raw &r, const typename Mv<TYPE>::Lane &o,
                                           int gl) {
-    if constexpr (TYPE == TY_Q4_K) Mv<TYPE>::load(p, r, gl & 7);
+    if constexpr (TYPE == TY_Q4_K || TYPE == TY_Q5_K) Mv<TYPE>::load(p, r, gl & 7);
     else if constexpr (TYPE == TY_Q6_K) Mv<TYPE>::load(p, r, o);
     else Mv<TYPE>::load(p, r);
 }
@@ -522,12 +536,14 @@ __global__ void k_block_dots(const uint8_t *W, long long rb, const int8_t *q, in
             const uint32_t nib = v < 16 ? (b[v] & 0xfu) : (b[v - 16] >> 4);
             s += cb_value(nib) * xg[j];
         }
-    } else if (TYPE == TY_Q4_K) {
-        const uint8_t *b = row + 144 * (g >> 3);
-        const int j = g & 7;  // sub-block: chunk j / 2, high nibbles for odd j
+    } else if (TYPE == TY_Q4_K || TYPE == TY_Q5_K) {
+        const bool q5 = TYPE == TY_Q5_K;
+        const uint8_t *b = row + (q5 ? 176 : 144) * (g >> 3);
+        const int j = g & 7;  // sub-block: chunk j / 2, high nibbles for odd j (Q5_K: bit j of qh byte i2 as bit 4)
         for (int i2 = 0; i2 < 32; ++i2) {
-            const uint8_t v = b[16 + 32 * (j >> 1) + i2];
-            s += (int)((j & 1) ? (v >> 4) : (v & 0xf)) * xg[i2];
+            const uint8_t v = b[(q5 ? 48 : 16) + 32 * (j >> 1) + i2];
+            const int hb = q5 ? ((b[16 + i2] >> j) & 1) << 4 : 0;
+            s += ((int)((j & 1) ? (v >> 4) : (v & 0xf)) | hb) * xg[i2];
         }
     } else {  // Q6_K group of 16
         const uint8_t *b = row + 210 * (g >> 4);
@@ -550,6 +566,7 @@ int matvec_lanes(int type, int K, long long rows) {
     case TY_FP4: nt = Mv<TY_FP4>::tasks(K); U = Mv<TY_FP4>::U; break;
     case TY_FAST: nt = Mv<TY_FAST>::tasks(K); U = Mv<TY_FAST>::U; break;
     case TY_Q4_K: nt = Mv<TY_Q4_K>::tasks(K); U = Mv<TY_Q4_K>::U; break;
+    case TY_Q5_K: nt = Mv<TY_Q5_K>::tasks(K); U = Mv<TY_Q5_K>::U; break;
     case TY_Q6_K: nt = Mv<TY_Q6_K>::tasks(K); U = Mv<TY_Q6_K>::U; break;
     default: return 0;
     }
@@ -611,6 +628,7 @@ hipError_t launch_matvec(int type, const MvArgs &a, hipStream_t stream) {
     case TY_FP4: return launch_nt<TY_FP4>(a, stream);
     case TY_FAST: return launch_nt<TY_FAST>(a, stream);
     case TY_Q4_K: return launch_nt<TY_Q4_K>(a, stream);
+    case TY_Q5_K: return launch_nt<TY_Q5_K>(a, stream);
     case TY_Q6_K: return launch_nt<TY_Q6_K>(a, stream);
     }
     return hipErrorInvalidDeviceFunction;
@@ -647,6 +665,7 @@ hipError_t launch_matvec_id(int type, const MvIdArgs &a, hipStream_t stream) {
     case TY_FP4: return launch_id_t<TY_FP4>(a, stream);
     case TY_FAST: return launch_id_t<TY_FAST>(a, stream);
     case TY_Q4_K: return launch_id_t<TY_Q4_K>(a, stream);
+    case TY_Q5_K: return launch_id_t<TY_Q5_K>(a, stream);
     case TY_Q6_K: return launch_id_t<TY_Q6_K>(a, stream);
     }
     return hipErrorInvalidDeviceFunction;
@@ -662,6 +681,7 @@ hipError_t launch_block_dots(int type, const uint8_t *W, long long rb, const int
     case TY_FP4: hipLaunchKernelGGL(k_block_dots<TY_FP4>, grid, dim3(256), 0, stream, W, rb, q, out, N, K); break;
     case TY_FAST: hipLaunchKernelGGL(k_block_dots<TY_FAST>, grid, dim3(256), 0, stream, W, rb, q, out, N, K); break;
     case TY_Q4_K: hipLaunchKernelGGL(k_block_dots<TY_Q4_K>, grid, dim3(256), 0, stream, W, rb, q, out, N, K); break;
+    case TY_Q5_K: hipLaunchKernelGGL(k_block_dots<TY_Q5_K>, grid, dim3(256), 0, stream, W, rb, q, out, N, K); break;
     case TY_Q6_K: hipLaunchKernelGGL(k_block_dots<TY_Q6_K>, grid, dim3(256), 0, stream, W, rb, q, out, N, K); break;
     default: return hipErrorInvalidDeviceFunction;
     }

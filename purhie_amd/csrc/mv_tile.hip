@@ -3,7 +3,7 @@
 // Replaces the reference's matvec_q8_<type> / matvec_q8t_<type> / matvec_q8_id_<type> (src/matvec_q.hip:
 // 1403-1965) for the shapes it covers (K a whole number of units, at most 256 units a row); the per-wave
 // kernels of matvec.hip take the rest. The unit a lane owns (values of one row):
-//   Q4_K: one 144-byte super-block (256)    Q6_K: one 210-byte super-block (256)
+//   Q4_K / Q5_K: one 144 / 176-byte super-block (256)    Q6_K: one 210-byte super-block (256)
 //   ROCmFP4: eight 18-byte blocks (256)     ROCmFP4_FAST: eight 17-byte blocks (256)
 //   Q8_0: four 34-byte blocks (128)
 // so a scale decode serves a whole block and the integer work per byte is small.
@@ -110,10 +110,13 @@ struct Tu;
 // (reference src/quant_types.cpp:193-201): scale j < 4 = y byte j & 63, j >= 4 = (w byte & 15) | (y byte
 // >> 6) << 4; min j < 4 = z byte j & 63, j >= 4 = (w byte >> 4) | (z byte >> 6) << 4 (y, z, w = dwords
 // 1..3). Per super-block: d dx isum - dmin dx msum, isum = sum_j sc_j dot_j, msum = sum_j m_j sum32_j
-// (reference src/matvec_q.hip:1752-1789).
-template <>
-struct Tu<TY_Q4_K> {
-    static constexpr int VALS = 256, BYTES = 144, NDW = 36, ACT = 256, SUMS = 32, LEAD = 0;
+// (reference src/matvec_q.hip:1752-1789). Q5_K (176 bytes) puts qh (32 bytes) between the scales and qs: the
+// level's bit 4 is bit 2 c (low nibble) or 2 c + 1 (high nibble) of qh byte l (reference src/matvec_q.hip:
+// 1752-1789 with Q5, 1928-1930).
+template <bool Q5>
+struct TuKq {
+    static constexpr int VALS = 256, BYTES = Q5 ? 176 : 144, NDW = BYTES / 4, ACT = 256, SUMS = 32, LEAD = 0;
+    static constexpr int QS = Q5 ? 12 : 4;  // first dword of qs
     static constexpr bool LUT = false;
     __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read16(p, w, aux); }
     template <int NT>
@@ -129,9 +132,15 @@ struct Tu<TY_Q4_K> {
             int lo[8], hi[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                const uint32_t q = w[4 + 8 * c + k];
-                lo[k] = (int)(q & 0x0f0f0f0fu);
-                hi[k] = (int)((q >> 4) & 0x0f0f0f0fu);
+                const uint32_t q = w[QS + 8 * c + k];
+                uint32_t l4 = q & 0x0f0f0f0fu, h4 = (q >> 4) & 0x0f0f0f0fu;
+                if (Q5) {
+                    const uint32_t qh = w[4 + k];
+                    l4 |= ((qh >> (2 * c)) & 0x01010101u) << 4;
+                    h4 |= ((qh >> (2 * c + 1)) & 0x01010101u) << 4;
+                }
+                lo[k] = (int)l4;
+                hi[k] = (int)h4;
             }
             const int sa = (int)((sc[c >> 1] >> (16 * (c & 1))) & 0xffu);
             const int sb = (int)((sc[c >> 1] >> (16 * (c & 1) + 8)) & 0xffu);
@@ -160,6 +169,10 @@ struct Tu<TY_Q4_K> {
         }
     }
 };
+template <>
+struct Tu<TY_Q4_K> : TuKq<false> {};
+template <>
+struct Tu<TY_Q5_K> : TuKq<true> {};
 
 // Q6_K super-block (210 bytes, 2-aligned): ql (bytes 0..127), qh (128..191), 16 int8 scales (192..207),
 // d (208..209). Read as 53 dwords from the 4-aligned address at or below it and realigned. For half h,
@@ -629,6 +642,7 @@ hipError_t launch_matvec_tile(int type, const MvArgs &a, hipStream_t stream) {
     case TY_FP4: return tile_dense_t<TY_FP4>(a, stream);
     case TY_FAST: return tile_dense_t<TY_FAST>(a, stream);
     case TY_Q4_K: return tile_dense_t<TY_Q4_K>(a, stream);
+    case TY_Q5_K: return tile_dense_t<TY_Q5_K>(a, stream);
     case TY_Q6_K: return tile_dense_t<TY_Q6_K>(a, stream);
     }
     return hipErrorNotSupported;
@@ -666,6 +680,7 @@ hipError_t launch_matvec_id_tile(int type, const MvIdArgs &a, hipStream_t stream
     case TY_FP4: return tile_id<TY_FP4>(a, stream);
     case TY_FAST: return tile_id<TY_FAST>(a, stream);
     case TY_Q4_K: return tile_id<TY_Q4_K>(a, stream);
+    case TY_Q5_K: return tile_id<TY_Q5_K>(a, stream);
     case TY_Q6_K: return tile_id<TY_Q6_K>(a, stream);
     }
     return hipErrorNotSupported;

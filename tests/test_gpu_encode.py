@@ -10,7 +10,7 @@ import pytest
 from purhie_amd import synth
 
 pytestmark = pytest.mark.gpu
-TYPES = (8, 12, 14, 100, 101)
+TYPES = (8, 12, 13, 14, 100, 101)
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
@@ -60,7 +60,7 @@ def test_encode_device_matches_oracle(Q, oracle, t):
     assert np.array_equal(y.cpu().numpy().reshape(N, -1), oracle.quantize(t, x))
 
 
-@pytest.mark.parametrize("src_t,dst_t", [(1, 100), (30, 12), (8, 101), (100, 8), (12, 14)])
+@pytest.mark.parametrize("src_t,dst_t", [(1, 100), (30, 12), (8, 101), (100, 8), (12, 14), (14, 13)])
 def test_reencode_from_other_type(Q, oracle, src_t, dst_t):
     K = 512
     x = synth.gaussian(720 + src_t, 8 * K, 0, 0.02).reshape(8, K)
