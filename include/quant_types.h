@@ -32,6 +32,7 @@ enum qt_type {
     QT_Q4_K = 12,
     QT_Q5_K = 13,
     QT_Q6_K = 14,
+    QT_IQ4_XS = 23,
     QT_BF16 = 30,
     QT_Q4_0_ROCMFP4 = 100,
     QT_Q4_0_ROCMFP4_FAST = 101,

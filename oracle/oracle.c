@@ -94,7 +94,7 @@ int orc_block_size(int t) {
     switch (t) {
     case ORC_F32: case ORC_F16: case ORC_BF16: return 1;
     case ORC_Q8_0: case ORC_FP4: case ORC_FAST: return 32;
-    case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: return 256;
+    case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_IQ4_XS: return 256;
     default: return 0;
     }
 }
@@ -109,6 +109,7 @@ int orc_type_size(int t) {
     case ORC_Q4_K: return 144;
     case ORC_Q5_K: return 176;
     case ORC_Q6_K: return 210;
+    case ORC_IQ4_XS: return 136;
     default: return 0;
     }
 }
@@ -142,6 +143,21 @@ static inline int k5_level(const uint8_t *blk, int v) {
     const int c = v >> 6, hi = (v >> 5) & 1, l = v & 31;
     const uint8_t b = blk[48 + 32 * c + l];
     return (hi ? (b >> 4) : (b & 0xf)) | (((blk[16 + l] >> (2 * c + hi)) & 1) << 4);
+}
+
+/* IQ4_XS (src/quant_types.cpp:111-125): ggml's non-linear 4-bit levels, a nibble indexing kvalues_iq4nl;
+ * super-block d (fp16 @0), the 6-bit sub-block scales as scales_h (2 bits each, u16 @2) and scales_l (4 bits,
+ * two a byte, @4), qs[128] @8: sub-block j's bytes 8 + 16 j .. + 15 hold values 32 j + i (low nibble) and
+ * 32 j + 16 + i (high nibble) */
+static const int8_t k_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+static inline int iq4xs_scale(const uint8_t *blk, int j) {  /* ls - 32, in -32 .. 31 */
+    const int sh = blk[2] | (blk[3] << 8);
+    return (((blk[4 + j / 2] >> (4 * (j & 1))) & 0xf) | (((sh >> (2 * j)) & 3) << 4)) - 32;
+}
+static inline int iq4xs_level(const uint8_t *blk, int v) {  /* the codebook value of value v (0..255) */
+    const int j = v >> 5, i = v & 31;
+    const uint8_t b = blk[8 + 16 * j + (i & 15)];
+    return k_iq4nl[i < 16 ? (b & 0xf) : (b >> 4)];
 }
 
 /* Q6_K raw level (0..63) of value v of a super-block (src/quant_types.cpp:319-344): half h = v/128,
@@ -207,6 +223,15 @@ int orc_to_float(int t, const void *src, float *y, int64_t n) {
             for (int v = 0; v < 256; ++v) {
                 const int q = k6_level(b, v) - 32;
                 y[v] = d * (float)sc[v >> 4] * (float)q;   /* (d * sc) * q, src/quant_types.cpp:337-340 */
+            }
+        }
+        return 0;
+    case ORC_IQ4_XS:
+        for (int64_t i = 0; i < n / 256; ++i, b += 136, y += 256) {
+            const float d = rd16(b);
+            for (int v = 0; v < 256; ++v) {
+                const float dl = d * (float)iq4xs_scale(b, v >> 5);   /* d * (ls - 32), then * value */
+                y[v] = dl * (float)iq4xs_level(b, v);
             }
         }
         return 0;
@@ -625,6 +650,103 @@ static void enc_fast(const float *x, uint8_t *out, int64_t k) {
     }
 }
 
+/* ggml's best_index_int8 over the sorted codebook: the nearest value, the lower one on a tie
+ * (src/quantize.cpp:838-849) */
+static int iq4_index(float x) {
+    if (x <= k_iq4nl[0]) return 0;
+    if (x >= k_iq4nl[15]) return 15;
+    int lo = 0, hi = 15;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) / 2;
+        if (x < k_iq4nl[mid]) hi = mid;
+        else lo = mid;
+    }
+    return x - k_iq4nl[hi - 1] < k_iq4nl[hi] - x ? hi - 1 : hi;
+}
+
+/* IQ4_XS (src/quantize.cpp:851-958, 960-974; ggml's quantize_row_iq4_nl_impl without importance weights, 7
+ * retries): per 32-value sub-block, weights x^2, a first scale from the signed largest value (d = -max / -127),
+ * the least-squares scale of its levels, then 15 candidate inverse scales (itry - 127) / max, keeping the one
+ * whose sumqx^2 / sumq2 is largest; the sub-block scales are quantized to 6 bits against d = -max_scale / 32 (the
+ * fp32 d, not its fp16 rounding) and each value re-indexed with its sub-block's d * l */
+static void enc_iq4_xs(const float *x, uint8_t *out, int64_t k) {
+    for (int64_t b = 0; b < k / 256; ++b, x += 256, out += 136) {
+        uint8_t L[256];
+        float scales[8];
+        float max_scale = 0, amax_scale = 0;
+        memset(L, 0, sizeof L);
+        for (int ib = 0; ib < 8; ++ib) {
+            const float *xb = x + 32 * ib;
+            float w[32];
+            for (int j = 0; j < 32; ++j) w[j] = xb[j] * xb[j];
+            float amax = 0, mx = 0;
+            for (int j = 0; j < 32; ++j) {
+                const float ax = fabsf(xb[j]);
+                if (ax > amax) {
+                    amax = ax;
+                    mx = xb[j];
+                }
+            }
+            if (amax < 1e-15f) {
+                scales[ib] = 0;
+                continue;
+            }
+            float d = -mx / (float)k_iq4nl[0];
+            float id = 1 / d;
+            float sumqx = 0, sumq2 = 0;
+            for (int j = 0; j < 32; ++j) {
+                const int l = iq4_index(id * xb[j]);
+                L[32 * ib + j] = (uint8_t)l;
+                const float q = (float)k_iq4nl[l];
+                sumqx += w[j] * q * xb[j];
+                sumq2 += w[j] * q * q;
+            }
+            d = sumq2 > 0 ? sumqx / sumq2 : 0.f;
+            float best = d * sumqx;
+            for (int itry = -7; itry <= 7; ++itry) {
+                id = ((float)itry + (float)k_iq4nl[0]) / mx;
+                sumqx = sumq2 = 0;
+                for (int j = 0; j < 32; ++j) {
+                    const int l = iq4_index(id * xb[j]);
+                    const float q = (float)k_iq4nl[l];
+                    sumqx += w[j] * q * xb[j];
+                    sumq2 += w[j] * q * q;
+                }
+                if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
+                    d = sumqx / sumq2;
+                    best = d * sumqx;
+                }
+            }
+            scales[ib] = d;
+            if (fabsf(d) > amax_scale) {
+                amax_scale = fabsf(d);
+                max_scale = d;
+            }
+        }
+        const float d = -max_scale / 32;
+        const uint16_t dh = orc_f32_to_f16(d);
+        const float id = d != 0.0f ? 1 / d : 0.f;
+        uint16_t sh = 0;
+        uint8_t sl[4] = {0, 0, 0, 0};
+        for (int ib = 0; ib < 8; ++ib) {
+            int l = nint(id * scales[ib]);
+            l = l < -32 ? -32 : l > 31 ? 31 : l;
+            const float dl = d * (float)l;
+            const float idl = dl != 0.0f ? 1 / dl : 0.f;
+            for (int j = 0; j < 32; ++j) L[32 * ib + j] = (uint8_t)iq4_index(idl * x[32 * ib + j]);
+            l += 32;
+            if (ib % 2 == 0) sl[ib / 2] = (uint8_t)(l & 0xf);
+            else sl[ib / 2] |= (uint8_t)((l & 0xf) << 4);
+            sh |= (uint16_t)((l >> 4) << (2 * ib));
+        }
+        memcpy(out, &dh, 2);
+        memcpy(out + 2, &sh, 2);
+        memcpy(out + 4, sl, 4);
+        for (int i = 0; i < 8; ++i)
+            for (int j = 0; j < 16; ++j) out[8 + 16 * i + j] = (uint8_t)(L[32 * i + j] | (L[32 * i + 16 + j] << 4));
+    }
+}
+
 static void enc_row(int t, const float *x, uint8_t *y, int64_t k) {
     switch (t) {
     case ORC_F32: memcpy(y, x, (size_t)k * 4); break;
@@ -632,6 +754,7 @@ static void enc_row(int t, const float *x, uint8_t *y, int64_t k) {
     case ORC_Q8_0: enc_q8_0(x, y, k); break;
     case ORC_Q4_K: enc_q4_k(x, y, k); break;
     case ORC_Q5_K: enc_q5_k(x, y, k); break;
+    case ORC_IQ4_XS: enc_iq4_xs(x, y, k); break;
     case ORC_Q6_K: enc_q6_k(x, y, k); break;
     case ORC_FP4: enc_fp4(x, y, k); break;
     case ORC_FAST: enc_fast(x, y, k); break;
@@ -761,7 +884,7 @@ void orc_quantize_q8_k(const float *x, int64_t k, int8_t *qK, float *dK, int32_t
 
 int orc_group_size(int t) {
     switch (t) {
-    case ORC_Q8_0: case ORC_FAST: case ORC_Q4_K: case ORC_Q5_K: return 32;
+    case ORC_Q8_0: case ORC_FAST: case ORC_Q4_K: case ORC_Q5_K: case ORC_IQ4_XS: return 32;
     case ORC_FP4: case ORC_Q6_K: return 16;
     default: return 0;
     }
@@ -784,6 +907,7 @@ static inline int raw_level(int t, const uint8_t *row, int v) {
     }
     case ORC_Q4_K: return k4_level(row + 144 * (v >> 8), v & 255);
     case ORC_Q5_K: return k5_level(row + 176 * (v >> 8), v & 255);
+    case ORC_IQ4_XS: return iq4xs_level(row + 136 * (v >> 8), v & 255);
     case ORC_Q6_K: return k6_level(row + 210 * (v >> 8), v & 255);
     }
     return 0;
@@ -812,7 +936,8 @@ int orc_block_dots(int t, const void *W, size_t rb, int N, int K, const int8_t *
  *   FAST  (e * dx) * (s0 + s1)                       src/matvec_q.hip:1492-1502, src/expert_cpu.cpp:50-63
  *   Q4_K  per 8 lanes of 16 bytes: (d * dx) * isum - (dmin * dx) * msum     src/matvec_q.hip:1752-1789
  *   Q5_K  the same with 5-bit levels (qh bit 2c / 2c + 1 as bit 4)           src/matvec_q.hip:1752-1789,1928-1930
- *   Q6_K  per 8 lanes of 16 bytes: (d * dx) * (isum - 32 * offs)            src/matvec_q.hip:1716-1750 */
+ *   Q6_K  per 8 lanes of 16 bytes: (d * dx) * (isum - 32 * offs)            src/matvec_q.hip:1716-1750
+ *   IQ4_XS per 8 lanes of a 32-value sub-block: (d * dx) * ((ls - 32) * dot)  src/matvec_q.hip:1788-1810 */
 static float row_q8(int t, const uint8_t *row, int K, const int8_t *q, const float *d, const int32_t *bs,
                     double *mag) {
     float acc = 0.0f;
@@ -874,6 +999,19 @@ static float row_q8(int t, const uint8_t *row, int K, const int8_t *q, const flo
                 m += fabs((double)ta) + fabs((double)tb);
             }
         }
+    } else if (t == ORC_IQ4_XS) {
+        for (int ib = 0; ib < K / 256; ++ib) {
+            const uint8_t *b = row + 136 * ib;
+            const int8_t *xb = q + 256 * ib;
+            const float dw = rd16(b), dx = d[ib];
+            for (int s = 0; s < 8; ++s) {
+                int dot = 0;
+                for (int i = 0; i < 32; ++i) dot += iq4xs_level(b, 32 * s + i) * xb[32 * s + i];
+                const float term = dw * dx * (float)(iq4xs_scale(b, s) * dot);
+                acc += term;
+                m += fabs((double)term);
+            }
+        }
     } else if (t == ORC_Q6_K) {
         for (int ib = 0; ib < K / 256; ++ib) {
             const uint8_t *b = row + 210 * ib;
@@ -917,7 +1055,7 @@ typedef struct {
 
 static void mv_span(void *p, int64_t r0, int64_t r1) {
     mv_ctx *c = (mv_ctx *)p;
-    const int kq = c->t == ORC_Q4_K || c->t == ORC_Q5_K || c->t == ORC_Q6_K;
+    const int kq = c->t == ORC_Q4_K || c->t == ORC_Q5_K || c->t == ORC_Q6_K || c->t == ORC_IQ4_XS;
     float *wf = c->ref ? (float *)malloc((size_t)c->K * 4) : NULL;
     for (int64_t n = r0; n < r1; ++n) {
         const uint8_t *row = c->W + (size_t)n * c->rb;

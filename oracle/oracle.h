@@ -33,7 +33,7 @@ extern "C" {
 #endif
 
 /* ggml type ids of the path */
-enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14, ORC_BF16 = 30,
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14, ORC_IQ4_XS = 23, ORC_BF16 = 30,
        ORC_FP4 = 100, ORC_FAST = 101 };
 
 /* ---- scalars */

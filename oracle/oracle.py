@@ -13,11 +13,11 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liboracle.so")
 REF_PATH = os.path.join(_HERE, "_ref", "libref.so")
 
-Q8_0, Q4_K, Q5_K, Q6_K, FP4, FAST, F32, F16, BF16 = 8, 12, 13, 14, 100, 101, 0, 1, 30
-KQ = (Q4_K, Q5_K, Q6_K)
-BLOCK = {Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, FP4: 32, FAST: 32, F32: 1, F16: 1, BF16: 1}
-BYTES = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, FP4: 18, FAST: 17, F32: 4, F16: 2, BF16: 2}
-GROUP = {Q8_0: 32, FP4: 16, FAST: 32, Q4_K: 32, Q5_K: 32, Q6_K: 16}
+Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS, FP4, FAST, F32, F16, BF16 = 8, 12, 13, 14, 23, 100, 101, 0, 1, 30
+KQ = (Q4_K, Q5_K, Q6_K, IQ4_XS)
+BLOCK = {Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ4_XS: 256, FP4: 32, FAST: 32, F32: 1, F16: 1, BF16: 1}
+BYTES = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136, FP4: 18, FAST: 17, F32: 4, F16: 2, BF16: 2}
+GROUP = {Q8_0: 32, FP4: 16, FAST: 32, Q4_K: 32, Q5_K: 32, Q6_K: 16, IQ4_XS: 32}
 
 _lib = None
 _ref = None

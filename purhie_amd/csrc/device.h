@@ -53,6 +53,21 @@ __device__ __forceinline__ int fp4x4_hi(uint32_t w) {
 // four codes, one per byte (0..15)
 __device__ __forceinline__ int fp4x4(uint32_t n) { return fp4x4_lo(n); }
 
+// Four IQ4_NL / IQ4_XS indices (one per byte, 0..15) -> their int8 levels, ggml's kvalues_iq4nl {-127, -104, -83,
+// -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113}: the low 3 bits look up both halves of the table with
+// v_perm_b32, bit 3 picks the half per byte (as fp4_pick).
+__device__ __forceinline__ int iq4nl4(uint32_t n) {
+    const uint32_t sel = n & 0x07070707u, upper = (n & 0x08080808u) >> 1;
+    const uint32_t a = __builtin_amdgcn_perm(0xf6eaddcfu, 0xbfad9881u, sel);  // indices 0..7
+    const uint32_t b = __builtin_amdgcn_perm(0x71594535u, 0x26190d01u, sel);  // indices 8..15
+    return (int)__builtin_amdgcn_perm(b, a, 0x03020100u | upper);
+}
+
+// IQ4_XS sub-block j's scale ls - 32 from scales_h (16 bits) and scales_l (4 bytes as a dword)
+__device__ __forceinline__ int iq4xs_scale(uint32_t sh, uint32_t sl, int j) {
+    return (int)(((sl >> (4 * j)) & 0xfu) | (((sh >> (2 * j)) & 3u) << 4)) - 32;
+}
+
 // the dword starting `off` bytes (0..3, run-time) into the 8 bytes {hi:lo}
 __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t off) {
     return __builtin_amdgcn_alignbyte(hi, lo, off);

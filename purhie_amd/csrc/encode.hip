@@ -1,6 +1,7 @@
-// encode.hip -- the weight encoders on the GPU: fp32 rows -> GGUF blocks (Q8_0, Q4_K, Q5_K, Q6_K, ROCmFP4,
-// ROCmFP4_FAST) and F32 / F16 / BF16 rows, bit-identical to the reference's CPU encoders (src/quantize.cpp:
-// 28-64, 161-358, 362-476, 975-1109), which reproduce ggml's _ref quantizers and ROCmFPX's rocmfp4.c.
+// encode.hip -- the weight encoders on the GPU: fp32 rows -> GGUF blocks (Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS,
+// ROCmFP4, ROCmFP4_FAST) and F32 / F16 / BF16 rows, bit-identical to the reference's CPU encoders
+// (src/quantize.cpp:28-64, 161-358, 362-476, 851-974, 975-1109), which reproduce ggml's _ref quantizers and
+// ROCmFPX's rocmfp4.c.
 //
 // One thread per block (Q8_0, ROCmFP4, FAST: 32 values) or super-block (K-quants: 256 values). The
 // searches are the reference's, step for step, in single precision: this file is compiled without
@@ -430,17 +431,111 @@ __device__ void enc_fast_block(const float *x, uint8_t *out) {
     out[16] = e;
 }
 
+// ---------------------------------------------------------------- IQ4_XS (src/quantize.cpp:851-974)
+
+__constant__ int8_t k_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+// the nearest codebook value's index, the lower one on a tie (ggml's best_index_int8 over the sorted table)
+__device__ int iq4_index(float x) {
+    if (x <= (float)k_iq4nl[0]) return 0;
+    if (x >= (float)k_iq4nl[15]) return 15;
+    int lo = 0, hi = 15;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (x < (float)k_iq4nl[mid]) hi = mid;
+        else lo = mid;
+    }
+    return x - (float)k_iq4nl[hi - 1] < (float)k_iq4nl[hi] - x ? hi - 1 : hi;
+}
+
+// ggml's quantize_row_iq4_nl_impl for one 256-value super-block, no importance weights, 7 retries: per 32-value
+// sub-block, weights x^2, a first scale from the signed largest value, its least-squares refinement, then 15
+// candidate inverse scales (itry - 127) / max keeping the largest sumqx^2 / sumq2; the sub-block scales quantized
+// to 6 bits against d = -max_scale / 32 (fp32; its fp16 rounding is only stored) and every value re-indexed
+__device__ void enc_iq4_xs_block(const float *x, uint8_t *out) {
+    uint8_t L[256];
+    float scales[8];
+    float max_scale = 0, amax_scale = 0;
+    for (int i = 0; i < 256; ++i) L[i] = 0;
+    for (int ib = 0; ib < 8; ++ib) {
+        const float *xb = x + 32 * ib;
+        float amax = 0, mx = 0;
+        for (int j = 0; j < 32; ++j) {
+            const float ax = fabsf(xb[j]);
+            if (ax > amax) {
+                amax = ax;
+                mx = xb[j];
+            }
+        }
+        if (amax < 1e-15f) {
+            scales[ib] = 0;
+            continue;
+        }
+        float d = -mx / (float)k_iq4nl[0];
+        float id = 1 / d;
+        float sumqx = 0, sumq2 = 0;
+        for (int j = 0; j < 32; ++j) {
+            const int l = iq4_index(id * xb[j]);
+            L[32 * ib + j] = (uint8_t)l;
+            const float q = (float)k_iq4nl[l], w = xb[j] * xb[j];
+            sumqx += w * q * xb[j];
+            sumq2 += w * q * q;
+        }
+        d = sumq2 > 0 ? sumqx / sumq2 : 0.f;
+        float best = d * sumqx;
+        for (int itry = -7; itry <= 7; ++itry) {
+            id = ((float)itry + (float)k_iq4nl[0]) / mx;
+            sumqx = sumq2 = 0;
+            for (int j = 0; j < 32; ++j) {
+                const float q = (float)k_iq4nl[iq4_index(id * xb[j])], w = xb[j] * xb[j];
+                sumqx += w * q * xb[j];
+                sumq2 += w * q * q;
+            }
+            if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
+                d = sumqx / sumq2;
+                best = d * sumqx;
+            }
+        }
+        scales[ib] = d;
+        if (fabsf(d) > amax_scale) {
+            amax_scale = fabsf(d);
+            max_scale = d;
+        }
+    }
+    const float d = -max_scale / 32;
+    const uint16_t dh = f32_to_f16_bits(d);
+    const float id = d != 0.0f ? 1 / d : 0.f;
+    uint32_t sh = 0, sl = 0;
+    for (int ib = 0; ib < 8; ++ib) {
+        const int l = clampi(nearest(id * scales[ib]), -32, 31);
+        const float dl = d * (float)l;
+        const float idl = dl != 0.0f ? 1 / dl : 0.f;
+        for (int j = 0; j < 32; ++j) L[32 * ib + j] = (uint8_t)iq4_index(idl * x[32 * ib + j]);
+        const uint32_t u = (uint32_t)(l + 32);
+        sl |= (u & 0xfu) << (4 * ib);
+        sh |= (u >> 4) << (2 * ib);
+    }
+    out[0] = (uint8_t)dh;
+    out[1] = (uint8_t)(dh >> 8);
+    out[2] = (uint8_t)sh;
+    out[3] = (uint8_t)(sh >> 8);
+    for (int i = 0; i < 4; ++i) out[4 + i] = (uint8_t)(sl >> (8 * i));
+    for (int i = 0; i < 8; ++i)
+        for (int j = 0; j < 16; ++j) out[8 + 16 * i + j] = (uint8_t)(L[32 * i + j] | (L[32 * i + 16 + j] << 4));
+}
+
 // ---------------------------------------------------------------- kernels
 
 // one thread per block of `vals` values: block i of row r at x + r * ncols + i * vals
 template <int TYPE>
 __global__ void __launch_bounds__(256) k_encode(const float *__restrict__ x, uint8_t *__restrict__ y, long long nrows,
                                                 long long ncols, long long row_bytes) {
-    constexpr int VALS = (TYPE == TY_Q4_K || TYPE == TY_Q5_K || TYPE == TY_Q6_K) ? 256 : 32;
+    constexpr int VALS = (TYPE == TY_Q4_K || TYPE == TY_Q5_K || TYPE == TY_Q6_K || TYPE == TY_IQ4_XS) ? 256 : 32;
     constexpr int BYTES = TYPE == TY_Q8_0   ? 34
                           : TYPE == TY_Q4_K ? 144
                           : TYPE == TY_Q5_K ? 176
                           : TYPE == TY_Q6_K ? 210
+                          : TYPE == TY_IQ4_XS ? 136
                           : TYPE == TY_FP4  ? 18
                                             : 17;
     const long long per_row = ncols / VALS;
@@ -452,6 +547,7 @@ __global__ void __launch_bounds__(256) k_encode(const float *__restrict__ x, uin
     if (TYPE == TY_Q8_0) enc_q8_0_block(src, dst);
     else if (TYPE == TY_Q4_K) enc_q4_k_block(src, dst);
     else if (TYPE == TY_Q5_K) enc_q5_k_block(src, dst);
+    else if (TYPE == TY_IQ4_XS) enc_iq4_xs_block(src, dst);
     else if (TYPE == TY_Q6_K) enc_q6_k_block(src, dst);
     else if (TYPE == TY_FP4) enc_fp4_block(src, dst);
     else enc_fast_block(src, dst);
@@ -470,7 +566,7 @@ int encode_block_values(int type) {
     switch (type) {
     case 0: case 1: case 30: return 1;
     case TY_Q8_0: case TY_FP4: case TY_FAST: return 32;
-    case TY_Q4_K: case TY_Q5_K: case TY_Q6_K: return 256;
+    case TY_Q4_K: case TY_Q5_K: case TY_Q6_K: case TY_IQ4_XS: return 256;
     }
     return 0;
 }
@@ -489,6 +585,9 @@ hipError_t launch_encode(int type, const float *x, uint8_t *y, long long nrows, 
     case TY_Q8_0: hipLaunchKernelGGL(k_encode<TY_Q8_0>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes); break;
     case TY_Q4_K: hipLaunchKernelGGL(k_encode<TY_Q4_K>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes); break;
     case TY_Q5_K: hipLaunchKernelGGL(k_encode<TY_Q5_K>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes); break;
+    case TY_IQ4_XS:
+        hipLaunchKernelGGL(k_encode<TY_IQ4_XS>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes);
+        break;
     case TY_Q6_K: hipLaunchKernelGGL(k_encode<TY_Q6_K>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes); break;
     case TY_FP4: hipLaunchKernelGGL(k_encode<TY_FP4>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes); break;
     case TY_FAST: hipLaunchKernelGGL(k_encode<TY_FAST>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes); break;

@@ -66,6 +66,18 @@ __global__ void k_dequant(int type, const uint8_t *__restrict__ src, float *__re
         }
         break;
     }
+    case TY_IQ4_XS: {  // (d * (ls - 32)) * level (src/quant_types.cpp:111-125)
+        const uint8_t *b = src + (g >> 3) * 136;
+        const int j = (int)(g & 7);
+        const uint32_t sh = (uint32_t)b[2] | ((uint32_t)b[3] << 8), sl = *(const uint32_t *)(b + 4);
+        const float dl = rd16(b) * (float)iq4xs_scale(sh, sl, j);
+        const uint8_t *q = b + 8 + 16 * j;
+        for (int i = 0; i < 16; ++i) {
+            o[i] = dl * (float)(int8_t)(iq4nl4(q[i] & 0xfu) & 0xff);
+            o[i + 16] = dl * (float)(int8_t)(iq4nl4(q[i] >> 4) & 0xff);
+        }
+        break;
+    }
     case TY_Q6_K: {
         const uint8_t *b = src + (g >> 3) * 210;
         const int part = (int)(g & 7);  // values 32 part .. 32 part + 31
@@ -107,6 +119,7 @@ void to_float_sync_q8_0(const void *s, float *d, int64_t n) { (void)qt_to_float(
 void to_float_sync_q4_k(const void *s, float *d, int64_t n) { (void)qt_to_float(TY_Q4_K, s, d, n); }
 void to_float_sync_q5_k(const void *s, float *d, int64_t n) { (void)qt_to_float(TY_Q5_K, s, d, n); }
 void to_float_sync_q6_k(const void *s, float *d, int64_t n) { (void)qt_to_float(TY_Q6_K, s, d, n); }
+void to_float_sync_iq4_xs(const void *s, float *d, int64_t n) { (void)qt_to_float(TY_IQ4_XS, s, d, n); }
 void to_float_sync_fp4(const void *s, float *d, int64_t n) { (void)qt_to_float(QT_Q4_0_ROCMFP4, s, d, n); }
 void to_float_sync_fast(const void *s, float *d, int64_t n) { (void)qt_to_float(QT_Q4_0_ROCMFP4_FAST, s, d, n); }
 void to_float_sync_f32(const void *s, float *d, int64_t n) { (void)qt_to_float(QT_F32, s, d, n); }
@@ -121,6 +134,7 @@ const qt_traits k_traits[] = {
     {TY_Q4_K, "q4_K", 256, 144, to_float_sync_q4_k, 1},
     {TY_Q5_K, "q5_K", 256, 176, to_float_sync_q5_k, 1},
     {TY_Q6_K, "q6_K", 256, 210, to_float_sync_q6_k, 1},
+    {TY_IQ4_XS, "iq4_xs", 256, 136, to_float_sync_iq4_xs, 1},
     {QT_BF16, "bf16", 1, 2, to_float_sync_bf16, 1},
     {QT_Q4_0_ROCMFP4, "q4_0_rocmfp4", 32, 18, to_float_sync_fp4, 1},
     {QT_Q4_0_ROCMFP4_FAST, "q4_0_rocmfp4_fast", 32, 17, to_float_sync_fast, 1},
@@ -151,7 +165,7 @@ size_t qt_row_size(int type, int64_t ne0) {
     return (size_t)(ne0 / t->blck_size) * (size_t)t->type_size;
 }
 
-int qt_vec_dot_q8k(int type) { return type == TY_Q4_K || type == TY_Q5_K || type == TY_Q6_K; }
+int qt_vec_dot_q8k(int type) { return type == TY_Q4_K || type == TY_Q5_K || type == TY_Q6_K || type == TY_IQ4_XS; }
 
 float qt_fp16_to_fp32(uint16_t h) {
     const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;

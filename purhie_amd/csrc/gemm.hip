@@ -369,7 +369,8 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm(GemmArgs a) {
 // ---------------------------------------------------------------- host launchers
 
 int gemm_supported(int type) {
-    return type == TY_FP4 || type == TY_FAST || type == TY_Q8_0 || type == TY_Q4_K || type == TY_Q5_K || type == TY_Q6_K;
+    return type == TY_FP4 || type == TY_FAST || type == TY_Q8_0 || type == TY_Q4_K || type == TY_Q5_K || type == TY_Q6_K ||
+           type == TY_IQ4_XS;
 }
 
 int gemm_k_multiple() { return GB_K; }

@@ -1,4 +1,5 @@
-// gemm_k.hip -- the prefill GEMM Y[t][n] = sum_k W[n][k] X[t][k] for the K-quant formats (Q4_K, Q5_K, Q6_K) on
+// gemm_k.hip -- the prefill GEMM Y[t][n] = sum_k W[n][k] X[t][k] for the K-quant formats (Q4_K, Q5_K, Q6_K) and
+// IQ4_XS on
 // gfx950 MFMA, dense and over MoE expert tiles. Replaces the reference's K-quant WMMA GEMM (matmul_wmma_q4_K /
 // _q6_K and their _id forms: wmma_q8k, WStageK, src/matvec_q.hip:2975-3348), which reads Q8_K activations
 // and applies d_x (d_w isum - dmin msum) to exact integer tile sums.
@@ -168,6 +169,57 @@ struct KStage<TY_Q5_K> {
         mm.y = mn;
         *(h2 *)(sG + row * GK_G + 4 * c + 2 * p) = mm;
         if (p == 0) sD[row] = make_float2(h2f(r.h.x & 0xffffu), h2f(r.h.x >> 16));
+    }
+};
+
+// IQ4_XS (136-byte super-block, 8-byte aligned: d, scales_h, scales_l, qs[128] @8): thread parity p takes
+// sub-block j = 2 c + p, whose 16 qs bytes hold values 32 j + i (low nibbles) and 32 j + 16 + i (high). The
+// integer weight (ls - 32) * level reaches 32 * 127 = 4064, past fp16's exact integers: written as Q6_K's two
+// planes, the even part and the low bit.
+template <>
+struct KStage<TY_IQ4_XS> {
+    static constexpr int PLANES = 2, BB = 136;
+    struct Raw {
+        uint2 h, q0, q1;
+    };
+    __device__ static void load(const uint8_t *W, long long rb, int N, int n0, int s, int c, Raw &r) {
+        const int row = n0 + (threadIdx.x >> 1), p = threadIdx.x & 1;
+        const int rr = row < N ? row : N - 1;
+        const uint8_t *b = W + (long long)rr * rb + (long long)s * BB;
+        r.h = *(const uint2 *)b;
+        r.q0 = *(const uint2 *)(b + 8 + 16 * (2 * c + p));
+        r.q1 = *(const uint2 *)(b + 16 + 16 * (2 * c + p));
+    }
+    __device__ static void store(const Raw &r, int c, _Float16 *sW, _Float16 *, float2 *sD) {
+        const int row = threadIdx.x >> 1, p = threadIdx.x & 1;
+        const int ls = iq4xs_scale(r.h.x >> 16, r.h.y, 2 * c + p);
+        const uint32_t q[4] = {r.q0.x, r.q0.y, r.q1.x, r.q1.y};
+        uint32_t hi[16], lo[16];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {  // low nibbles: values 0..15; high nibbles: 16..31
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t v = (uint32_t)iq4nl4((q[k] >> (4 * half)) & 0x0f0f0f0fu);
+                _Float16 vh[4], vl[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int P = ls * (int)(int8_t)((v >> (8 * e)) & 0xffu);
+                    vh[e] = (_Float16)(float)(P & ~1);  // even, |.| <= 4064: exact
+                    vl[e] = (_Float16)(float)(P & 1);
+                }
+                hi[8 * half + 2 * k] = __builtin_bit_cast(uint32_t, h2{vh[0], vh[1]});
+                hi[8 * half + 2 * k + 1] = __builtin_bit_cast(uint32_t, h2{vh[2], vh[3]});
+                lo[8 * half + 2 * k] = __builtin_bit_cast(uint32_t, h2{vl[0], vl[1]});
+                lo[8 * half + 2 * k + 1] = __builtin_bit_cast(uint32_t, h2{vl[2], vl[3]});
+            }
+        }
+        uint4 *dh = (uint4 *)(sW + row * GK_ROW + 32 * p), *dl = (uint4 *)(sW + (GK_N + row) * GK_ROW + 32 * p);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            dh[m] = make_uint4(hi[4 * m], hi[4 * m + 1], hi[4 * m + 2], hi[4 * m + 3]);
+            dl[m] = make_uint4(lo[4 * m], lo[4 * m + 1], lo[4 * m + 2], lo[4 * m + 3]);
+        }
+        if (p == 0) sD[row] = make_float2(h2f(r.h.x & 0xffffu), 0.0f);
     }
 };
 
@@ -392,7 +444,7 @@ __global__ void __launch_bounds__(GK_THREADS, 2) k_gemm_kq(GemmArgs a) {
 
 // ---------------------------------------------------------------- host launchers
 
-bool gemm_kquant(int type) { return type == TY_Q4_K || type == TY_Q5_K || type == TY_Q6_K; }
+bool gemm_kquant(int type) { return type == TY_Q4_K || type == TY_Q5_K || type == TY_Q6_K || type == TY_IQ4_XS; }
 
 hipError_t launch_act_q8k(const int8_t *q, const float *dK, const int32_t *bs, int T, int K, int rows, _Float16 *xh,
                           _Float16 *xb, float *xd, hipStream_t stream) {
@@ -404,6 +456,7 @@ hipError_t launch_gemm_kquant(int type, const GemmArgs &a, dim3 grid, hipStream_
     switch (type) {
     case TY_Q4_K: hipLaunchKernelGGL(k_gemm_kq<TY_Q4_K>, grid, dim3(GK_THREADS), 0, stream, a); break;
     case TY_Q5_K: hipLaunchKernelGGL(k_gemm_kq<TY_Q5_K>, grid, dim3(GK_THREADS), 0, stream, a); break;
+    case TY_IQ4_XS: hipLaunchKernelGGL(k_gemm_kq<TY_IQ4_XS>, grid, dim3(GK_THREADS), 0, stream, a); break;
     case TY_Q6_K: hipLaunchKernelGGL(k_gemm_kq<TY_Q6_K>, grid, dim3(GK_THREADS), 0, stream, a); break;
     default: return hipErrorInvalidDeviceFunction;
     }

@@ -323,6 +323,61 @@ struct MvKq {
 };
 template <>
 struct Mv<TY_Q4_K> : MvKq<false> {};
+
+// IQ4_XS: a task is one of the 8 sub-blocks s of a 136-byte super-block (8-aligned): its 16 qs bytes (8 + 16 s,
+// low nibbles values 32 s + 0..15, high 32 s + 16..31, levels kvalues_iq4nl) and the header (d, scales_h,
+// scales_l); per task d dx ((ls_s - 32) dot) (reference src/matvec_q.hip:1788-1810).
+template <>
+struct Mv<TY_IQ4_XS> {
+    static constexpr int ACT_BLK = 256;
+    static constexpr bool KQ = true;
+    __host__ __device__ static int tasks(int K) { return K / 256 * 8; }
+    static constexpr int LDIV = 8, W_UNIT = 136, X_UNIT = 256, D_UNIT = 1, B_UNIT = 0;
+    static constexpr int U = 6;  // 6 dwords each
+    struct Lane {
+        int s;
+        __device__ Lane(int gl) : s(gl & 7) {}
+    };
+    __device__ static long long wbase(int gl) { return 136LL * (gl >> 3); }
+    __device__ static int xoff(int gl) { return 256 * (gl >> 3) + 32 * (gl & 7); }
+    __device__ static int doff(int gl) { return gl >> 3; }
+    __device__ static int boff(int) { return 0; }
+    struct Raw {
+        uint32_t h0, h1, q[4];
+    };
+    __device__ static void load(const uint8_t *p, Raw &r, int s) {
+        r.h0 = ld32_nt(p);
+        r.h1 = ld32_nt(p + 4);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) r.q[k] = ld32_nt(p + 8 + 16 * s + 4 * k);
+    }
+    template <int NT>
+    __device__ static void compute(const Raw &r, const Lane &o, const Act<NT> &x, int xo, int dof, int, float acc[NT],
+                                   bool v) {
+        int lo[4], hi[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            lo[k] = iq4nl4(r.q[k] & 0x0f0f0f0fu);
+            hi[k] = iq4nl4((r.q[k] >> 4) & 0x0f0f0f0fu);
+        }
+        const int ls = iq4xs_scale(r.h0 >> 16, r.h1, o.s);
+        const float dw = h2f(r.h0 & 0xffffu);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int8_t *xb = x.q[t] + xo;
+            const int4 xl = *(const int4 *)xb, xh = *(const int4 *)(xb + 16);
+            int s = dot4(lo[0], xl.x, 0);
+            s = dot4(lo[1], xl.y, s);
+            s = dot4(lo[2], xl.z, s);
+            s = dot4(lo[3], xl.w, s);
+            s = dot4(hi[0], xh.x, s);
+            s = dot4(hi[1], xh.y, s);
+            s = dot4(hi[2], xh.z, s);
+            s = dot4(hi[3], xh.w, s);
+            acc[t] = __builtin_fmaf(v ? dw * x.d[t][dof] : 0.0f, (float)(ls * s), acc[t]);
+        }
+    }
+};
 template <>
 struct Mv<TY_Q5_K> : MvKq<true> {};
 
@@ -414,7 +469,7 @@ struct Mv<TY_Q6_K> {
 template <int TYPE>
 __device__ __forceinline__ void load_task(const uint8_t *p, typename Mv<TYPE>::Raw &r, const typename Mv<TYPE>::Lane &o,
                                           int gl) {
-    if constexpr (TYPE == TY_Q4_K || TYPE == TY_Q5_K) Mv<TYPE>::load(p, r, gl & 7);
+    if constexpr (TYPE == TY_Q4_K || TYPE == TY_Q5_K || TYPE == TY_IQ4_XS) Mv<TYPE>::load(p, r, gl & 7);
     else if constexpr (TYPE == TY_Q6_K) Mv<TYPE>::load(p, r, o);
     else Mv<TYPE>::load(p, r);
 }
@@ -536,6 +591,12 @@ __global__ void k_block_dots(const uint8_t *W, long long rb, const int8_t *q, in
             const uint32_t nib = v < 16 ? (b[v] & 0xfu) : (b[v - 16] >> 4);
             s += cb_value(nib) * xg[j];
         }
+    } else if (TYPE == TY_IQ4_XS) {
+        const uint8_t *b = row + 136 * (g >> 3) + 8 + 16 * (g & 7);
+        for (int i2 = 0; i2 < 16; ++i2) {
+            s += (int)(int8_t)(iq4nl4(b[i2] & 0xfu) & 0xff) * xg[i2];
+            s += (int)(int8_t)(iq4nl4(b[i2] >> 4) & 0xff) * xg[16 + i2];
+        }
     } else if (TYPE == TY_Q4_K || TYPE == TY_Q5_K) {
         const bool q5 = TYPE == TY_Q5_K;
         const uint8_t *b = row + (q5 ? 176 : 144) * (g >> 3);
@@ -567,6 +628,7 @@ int matvec_lanes(int type, int K, long long rows) {
     case TY_FAST: nt = Mv<TY_FAST>::tasks(K); U = Mv<TY_FAST>::U; break;
     case TY_Q4_K: nt = Mv<TY_Q4_K>::tasks(K); U = Mv<TY_Q4_K>::U; break;
     case TY_Q5_K: nt = Mv<TY_Q5_K>::tasks(K); U = Mv<TY_Q5_K>::U; break;
+    case TY_IQ4_XS: nt = Mv<TY_IQ4_XS>::tasks(K); U = Mv<TY_IQ4_XS>::U; break;
     case TY_Q6_K: nt = Mv<TY_Q6_K>::tasks(K); U = Mv<TY_Q6_K>::U; break;
     default: return 0;
     }
@@ -629,6 +691,7 @@ hipError_t launch_matvec(int type, const MvArgs &a, hipStream_t stream) {
     case TY_FAST: return launch_nt<TY_FAST>(a, stream);
     case TY_Q4_K: return launch_nt<TY_Q4_K>(a, stream);
     case TY_Q5_K: return launch_nt<TY_Q5_K>(a, stream);
+    case TY_IQ4_XS: return launch_nt<TY_IQ4_XS>(a, stream);
     case TY_Q6_K: return launch_nt<TY_Q6_K>(a, stream);
     }
     return hipErrorInvalidDeviceFunction;
@@ -666,6 +729,7 @@ hipError_t launch_matvec_id(int type, const MvIdArgs &a, hipStream_t stream) {
     case TY_FAST: return launch_id_t<TY_FAST>(a, stream);
     case TY_Q4_K: return launch_id_t<TY_Q4_K>(a, stream);
     case TY_Q5_K: return launch_id_t<TY_Q5_K>(a, stream);
+    case TY_IQ4_XS: return launch_id_t<TY_IQ4_XS>(a, stream);
     case TY_Q6_K: return launch_id_t<TY_Q6_K>(a, stream);
     }
     return hipErrorInvalidDeviceFunction;
@@ -682,6 +746,9 @@ hipError_t launch_block_dots(int type, const uint8_t *W, long long rb, const int
     case TY_FAST: hipLaunchKernelGGL(k_block_dots<TY_FAST>, grid, dim3(256), 0, stream, W, rb, q, out, N, K); break;
     case TY_Q4_K: hipLaunchKernelGGL(k_block_dots<TY_Q4_K>, grid, dim3(256), 0, stream, W, rb, q, out, N, K); break;
     case TY_Q5_K: hipLaunchKernelGGL(k_block_dots<TY_Q5_K>, grid, dim3(256), 0, stream, W, rb, q, out, N, K); break;
+    case TY_IQ4_XS:
+        hipLaunchKernelGGL(k_block_dots<TY_IQ4_XS>, grid, dim3(256), 0, stream, W, rb, q, out, N, K);
+        break;
     case TY_Q6_K: hipLaunchKernelGGL(k_block_dots<TY_Q6_K>, grid, dim3(256), 0, stream, W, rb, q, out, N, K); break;
     default: return hipErrorInvalidDeviceFunction;
     }

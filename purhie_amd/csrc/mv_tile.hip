@@ -4,6 +4,7 @@
 // 1403-1965) for the shapes it covers (K a whole number of units, at most 256 units a row); the per-wave
 // kernels of matvec.hip take the rest. The unit a lane owns (values of one row):
 //   Q4_K / Q5_K: one 144 / 176-byte super-block (256)    Q6_K: one 210-byte super-block (256)
+//   IQ4_XS: one 136-byte super-block (256)
 //   ROCmFP4: eight 18-byte blocks (256)     ROCmFP4_FAST: eight 17-byte blocks (256)
 //   Q8_0: four 34-byte blocks (128)
 // so a scale decode serves a whole block and the integer work per byte is small.
@@ -290,6 +291,43 @@ struct Tu<TY_FP4> {
                 acc[t] += __builtin_fmaf(e1 * dx, (float)s1, e0 * dx * (float)s0);
             }
         }
+    }
+};
+
+// IQ4_XS (type 23): one 136-byte super-block (8-aligned): d (fp16) and scales_h (dword 0), scales_l (dword 1),
+// qs (dwords 2..33; sub-block j's 16 bytes hold values 32 j + i in the low nibbles, 32 j + 16 + i in the high),
+// a nibble indexing kvalues_iq4nl. Per super-block (d dx) * isum, isum = sum_j (ls_j - 32) dot_j (reference
+// src/matvec_q.hip:1788-1810 forms one float term per sub-block).
+template <>
+struct Tu<TY_IQ4_XS> {
+    static constexpr int VALS = 256, BYTES = 136, NDW = 34, ACT = 256, SUMS = 0, LEAD = 8;
+    static constexpr bool LUT = false;
+    __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read8(p, w, aux); }
+    template <int NT>
+    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT]) {
+        const uint32_t sh = w[0] >> 16, sl = w[1];
+        int isum[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) isum[t] = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            int lo[4], hi[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t q = w[2 + 4 * j + k];
+                lo[k] = iq4nl4(q & 0x0f0f0f0fu);
+                hi[k] = iq4nl4((q >> 4) & 0x0f0f0f0fu);
+            }
+            const int ls = iq4xs_scale(sh, sl, j);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const int4 *xv = (const int4 *)(x.x + t * x.xt + 32 * j);
+                isum[t] += ls * (dot4x(lo, xv[0]) + dot4x(hi, xv[1]));
+            }
+        }
+        const float dw = h2f(w[0] & 0xffffu);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = (dw * x.d[t * x.nd]) * (float)isum[t];
     }
 };
 
@@ -643,6 +681,7 @@ hipError_t launch_matvec_tile(int type, const MvArgs &a, hipStream_t stream) {
     case TY_FAST: return tile_dense_t<TY_FAST>(a, stream);
     case TY_Q4_K: return tile_dense_t<TY_Q4_K>(a, stream);
     case TY_Q5_K: return tile_dense_t<TY_Q5_K>(a, stream);
+    case TY_IQ4_XS: return tile_dense_t<TY_IQ4_XS>(a, stream);
     case TY_Q6_K: return tile_dense_t<TY_Q6_K>(a, stream);
     }
     return hipErrorNotSupported;
@@ -681,6 +720,7 @@ hipError_t launch_matvec_id_tile(int type, const MvIdArgs &a, hipStream_t stream
     case TY_FAST: return tile_id<TY_FAST>(a, stream);
     case TY_Q4_K: return tile_id<TY_Q4_K>(a, stream);
     case TY_Q5_K: return tile_id<TY_Q5_K>(a, stream);
+    case TY_IQ4_XS: return tile_id<TY_IQ4_XS>(a, stream);
     case TY_Q6_K: return tile_id<TY_Q6_K>(a, stream);
     }
     return hipErrorNotSupported;

@@ -18,9 +18,10 @@ using namespace pq;
 namespace {
 
 bool is_int8_type(int t) {
-    return t == TY_Q8_0 || t == TY_Q4_K || t == TY_Q5_K || t == TY_Q6_K || t == TY_FP4 || t == TY_FAST;
+    return t == TY_Q8_0 || t == TY_Q4_K || t == TY_Q5_K || t == TY_Q6_K || t == TY_IQ4_XS || t == TY_FP4 ||
+           t == TY_FAST;
 }
-bool reads_q8k(int t) { return t == TY_Q4_K || t == TY_Q5_K || t == TY_Q6_K; }
+bool reads_q8k(int t) { return t == TY_Q4_K || t == TY_Q5_K || t == TY_Q6_K || t == TY_IQ4_XS; }
 int act_blk(int t) { return reads_q8k(t) ? 256 : 32; }
 
 // required K multiple of each int8 kernel (src/qmatvec.cpp:423-429)
@@ -28,13 +29,13 @@ int k_multiple(int t) {
     switch (t) {
     case TY_Q8_0: case TY_FP4: return 64;
     case TY_FAST: return 128;
-    case TY_Q4_K: case TY_Q5_K: case TY_Q6_K: return 256;
+    case TY_Q4_K: case TY_Q5_K: case TY_Q6_K: case TY_IQ4_XS: return 256;
     }
     return 0;
 }
 
 // weight base alignment the kernels' loads need (Q4_K: 16-byte loads of 16-aligned blocks)
-uintptr_t w_align(int t) { return t == TY_Q4_K || t == TY_Q5_K ? 16 : 4; }
+uintptr_t w_align(int t) { return t == TY_Q4_K || t == TY_Q5_K ? 16 : t == TY_IQ4_XS ? 8 : 4; }
 
 int g_inited = 0;
 std::atomic<int> g_prefill{0};

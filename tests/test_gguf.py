@@ -23,13 +23,13 @@ def rand_bytes(seed, n):
 
 def tensors_for(seed):
     # (name, type, ne, data): the five matvec types, float types, a 3-D expert stack, a type the matvecs do not
-    # take (IQ4_XS, 23), a 1-D vector
+    # take (Q3_K, 11), a 1-D vector
     spec = [("blk.0.ffn_gate.weight", 12, (512, 6)), ("blk.0.ffn_down.weight", 14, (256, 3)),
             ("blk.0.attn_q.weight", 8, (64, 5)), ("blk.0.ffn_up_exps.weight", 100, (64, 3, 4)),
             ("blk.0.ffn_gate_exps.weight", 101, (128, 2, 2)), ("blk.0.attn_norm.weight", 0, (33,)),
-            ("token_embd.weight", 1, (16, 7)), ("output.weight", 30, (8, 3)), ("blk.1.iq4.weight", 23, (256, 2))]
+            ("token_embd.weight", 1, (16, 7)), ("output.weight", 30, (8, 3)), ("blk.1.q3k.weight", 11, (256, 2))]
     geo = {12: (256, 144), 14: (256, 210), 8: (32, 34), 100: (32, 18), 101: (32, 17), 0: (1, 4), 1: (1, 2),
-           30: (1, 2), 23: (256, 136)}
+           30: (1, 2), 11: (256, 110)}
     out = []
     for i, (name, t, ne) in enumerate(spec):
         b, s = geo[t]
@@ -297,7 +297,7 @@ def test_bind_weight_and_hbm_bytes(files):
         rc, w = m.bind_weight("blk.0.ffn_up_exps.weight")  # 3-D: experts stacked as rows
         assert rc == 0 and (w.type, w.N, w.K, w.row_bytes) == (100, 12, 64, 36)
         assert m.bind_weight("blk.0.attn_norm.weight")[0] == 0  # F32 vector: one row
-        assert m.bind_weight("blk.1.iq4.weight")[0] == -1       # a type the matvecs do not take
+        assert m.bind_weight("blk.1.q3k.weight")[0] == -1       # a type the matvecs do not take
         assert m.bind_weight("absent.weight")[0] == 1
         sizes = [len(d) for _, _, _, d in tensors]
         want = 0

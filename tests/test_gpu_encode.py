@@ -10,7 +10,7 @@ import pytest
 from purhie_amd import synth
 
 pytestmark = pytest.mark.gpu
-TYPES = (8, 12, 13, 14, 100, 101)
+TYPES = (8, 12, 13, 14, 23, 100, 101)
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 

@@ -9,7 +9,7 @@ from purhie_amd import synth
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
-GEMM_TYPES = (100, 101, 8, 12, 13, 14)
+GEMM_TYPES = (100, 101, 8, 12, 13, 14, 23)
 
 
 @pytest.fixture(scope="module")
@@ -51,7 +51,7 @@ def run_batch(Q, t, Wd, x, N, K, ldy=None):
 
 def check_tokens(oracle, t, W, N, K, x, got):
     for i in range(x.shape[0]):
-        a = oracle.quantize_act(x[i], t in (12, 13, 14))
+        a = oracle.quantize_act(x[i], t in (12, 13, 14, 23))
         want, ref, mag = oracle.matvec(t, W, N, K, a)
         err = np.abs(got[i] - want) / (mag + 1e-30)
         assert err.max() <= TOL, f"token {i}: max rel err {err.max():.3g}"
@@ -87,7 +87,8 @@ def test_gemm_ldy_and_split_invariance(Q, oracle, t):
 
 
 @pytest.mark.parametrize("t,N,K", [(100, 768, 2048), (100, 2048, 768), (8, 512, 1024), (101, 256, 1024),
-                                   (12, 768, 2048), (13, 512, 1024), (14, 2048, 768), (12, 200, 512)])
+                                   (12, 768, 2048), (13, 512, 1024), (14, 2048, 768), (23, 512, 1024),
+                                   (12, 200, 512)])
 def test_moe_tiled_gemm(Q, oracle, t, N, K):
     """expert tiles from the grouping (config 4 shapes, and K-quant experts): entry i of tile k multiplies input
     row in_rows[i] by expert tile_e[k] into output row out_rows[i]"""
@@ -114,7 +115,7 @@ def test_moe_tiled_gemm(Q, oracle, t, N, K):
     got = host(y)
     rb = W.shape[1]
     for tt in range(T):
-        a = oracle.quantize_act(x[tt], t in (12, 13, 14))
+        a = oracle.quantize_act(x[tt], t in (12, 13, 14, 23))
         for j in range(n_used):
             want, _, mag = oracle.matvec(t, W.reshape(E, N, rb)[ids[tt, j]], N, K, a)
             assert np.all(np.abs(got[tt * n_used + j] - want) <= TOL * mag)

@@ -13,7 +13,7 @@ import pytest
 
 from purhie_amd import synth
 
-TYPES_ENC = (8, 100, 101, 12, 13, 14)  # Q8_0, ROCmFP4, FAST, Q4_K, Q5_K, Q6_K
+TYPES_ENC = (8, 100, 101, 12, 13, 14, 23)  # Q8_0, ROCmFP4, FAST, Q4_K, Q5_K, Q6_K, IQ4_XS
 
 
 def families():
@@ -68,9 +68,9 @@ def test_decoders_match_reference_on_random_bytes(ref, t):
     k = 1024
     rb = ref.row_size(t, k)
     raw = (synth.splitmix64(100 + t, 64 * rb) & np.uint64(0xFF)).astype(np.uint8).reshape(64, rb)
-    if t in (8, 12, 13, 14):  # keep the fp16 scales finite: random bytes can be NaN / Inf halves
-        bs = {8: 34, 12: 144, 13: 176, 14: 210}[t]
-        offs = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208]}[t]
+    if t in (8, 12, 13, 14, 23):  # keep the fp16 scales finite: random bytes can be NaN / Inf halves
+        bs = {8: 34, 12: 144, 13: 176, 14: 210, 23: 136}[t]
+        offs = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 23: [0]}[t]
         v = raw.reshape(-1, bs)
         for o in offs:
             v[:, o + 1] &= 0x3B  # exponent < 15: |value| < 1
@@ -274,7 +274,7 @@ def test_block_dots_brute_force(oracle, t):
     N, K = 8, 512
     W = oracle.quantize(t, synth.gaussian(30 + t, N * K, 0, 0.02).reshape(N, K))
     x = synth.gaussian(40 + t, K)
-    kq = t in (12, 13, 14)
+    kq = t in (12, 13, 14, 23)
     a = oracle.quantize_act(x, kq)
     dots = oracle.block_dots(t, W, N, K, a["q"])
     G = oracle.GROUP[t]
@@ -296,6 +296,12 @@ def test_block_dots_brute_force(oracle, t):
                 w = v % 256
                 byte = b[16 + 32 * (w // 64) + w % 32]
                 lv[n, v] = (byte >> 4) if (w % 64) >= 32 else (byte & 15)
+            elif t == 23:  # IQ4_XS: kvalues_iq4nl[nibble], sub-block j's bytes 8 + 16 j, low nibbles first
+                b = row[136 * (v // 256):]
+                w = v % 256
+                byte = b[8 + 16 * (w // 32) + (w % 16)]
+                nib = (byte & 15) if (w % 32) < 16 else (byte >> 4)
+                lv[n, v] = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113][nib]
             elif t == 13:  # Q5_K: Q4_K's nibble from ql (byte 48 on) and qh byte w % 32, bit 2 chunk + high half
                 b = row[176 * (v // 256):]
                 w = v % 256
@@ -326,7 +332,7 @@ def test_matvec_float_order_within_tolerance(oracle, t):
     reference's criterion (tests/matvec_verify.cpp:8,142)"""
     N, K = 64, 2048
     W = oracle.quantize(t, synth.gaussian(50 + t, N * K, 0, 0.02).reshape(N, K))
-    a = oracle.quantize_act(synth.gaussian(60 + t, K), t in (12, 13, 14))
+    a = oracle.quantize_act(synth.gaussian(60 + t, K), t in (12, 13, 14, 23))
     y, r, mag = oracle.matvec(t, W, N, K, a)
     assert np.all(np.abs(y - r) <= 1e-5 * mag)
 
