@@ -175,9 +175,9 @@ hipError_t qmatvec_launch_id_batch_f(int type, const void *W, size_t row_bytes, 
                                      const int32_t *out_rows, hipStream_t stream);
 
 /* No counterpart in the reference: a test hook for the parity tests. The integer dot of every weight
- * scale group (Q8_0 / FAST / Q4_K / Q5_K / IQ4_XS: 32 values, ROCmFP4 / Q6_K: 16) of every row against the
- * quantized activation, computed by the same device decoders as the matvec kernels: out[N][K / group]. Q4_K /
- * Q5_K / Q6_K dot the raw levels (0..15 / 0..31 / 0..63), IQ4_XS the table levels (-127..113). */
+ * scale group (Q8_0 / FAST / MXFP4 / Q4_K / Q5_K / IQ4_XS: 32 values, ROCmFP4 / NVFP4 / Q6_K: 16) of every row
+ * against the quantized activation, computed by the same device decoders as the matvec kernels: out[N][K / group].
+ * Q4_K / Q5_K / Q6_K dot the raw levels (0..15 / 0..31 / 0..63), IQ4_XS the table levels (-127..113). */
 hipError_t qmatvec_debug_block_dots(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, int32_t *out,
                                     int N, int K, hipStream_t stream);
 

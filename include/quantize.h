@@ -1,8 +1,8 @@
 /* quantize.h -- the weight encoders of libpurhie_qmv.so (gfx950), the drop-in for the reference's
  * src/quantize.h (aardbeiplantje/PURHIE) for the path's types: rows of any type quant_types.h decodes are
- * encoded as F32, F16, BF16, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS, Q4_0_ROCMFP4 or Q4_0_ROCMFP4_FAST, bit-identical to the
- * reference's CPU encoders (ggml's _ref quantizers and ROCmFPX's exhaustive UE4M3 scale search). The
- * encoding runs on the GPU; the host entry points copy the rows there and back. */
+ * encoded as F32, F16, BF16, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS, MXFP4, NVFP4, Q4_0_ROCMFP4 or Q4_0_ROCMFP4_FAST,
+ * bit-identical to the reference's CPU encoders (ggml's _ref quantizers and ROCmFPX's exhaustive UE4M3 scale
+ * search). The encoding runs on the GPU; the host entry points copy the rows there and back. */
 #ifndef PURHIE_QUANTIZE_H
 #define PURHIE_QUANTIZE_H
 

@@ -86,6 +86,17 @@ float orc_ue4m3_fp4common(uint8_t e) {
 /* Signed FP4 codebook at half scale, sign in bit 3 (src/quant_types.cpp:349) */
 static const int8_t k_cb[16] = {0, 1, 2, 3, 4, 6, 8, 10, 0, -1, -2, -3, -4, -6, -8, -10};
 
+/* E2M1 at half scale, MXFP4's and NVFP4's codebook (src/quant_types.cpp:387): the same magnitudes with 12 on
+ * top (E2M1's 6 doubled) */
+static const int8_t k_e2m1[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+
+/* E8M0 exponent byte -> 2^(e - 128), the half-scale value (src/quant_types.cpp:390-395): e = 0, 1 are the
+ * subnormals 2^-128, 2^-127 */
+float orc_e8m0_half(uint8_t e) { return ldexpf(1.0f, (int)e - 128); }
+
+/* NVFP4's scale byte: UE4M3 at half scale with the sign bit cleared (src/quant_types.cpp:409-416) */
+static inline float nv_scale(uint8_t e) { return orc_ue4m3_half((uint8_t)(e & 0x7f)); }
+
 static inline float rd16(const uint8_t *p) { uint16_t h; memcpy(&h, p, 2); return orc_f16_to_f32(h); }
 
 /* ================================================================ formats */
@@ -93,7 +104,8 @@ static inline float rd16(const uint8_t *p) { uint16_t h; memcpy(&h, p, 2); retur
 int orc_block_size(int t) {
     switch (t) {
     case ORC_F32: case ORC_F16: case ORC_BF16: return 1;
-    case ORC_Q8_0: case ORC_FP4: case ORC_FAST: return 32;
+    case ORC_Q8_0: case ORC_FP4: case ORC_FAST: case ORC_MXFP4: return 32;
+    case ORC_NVFP4: return 64;
     case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_IQ4_XS: return 256;
     default: return 0;
     }
@@ -105,7 +117,8 @@ int orc_type_size(int t) {
     case ORC_F16: case ORC_BF16: return 2;
     case ORC_Q8_0: return 34;
     case ORC_FP4: return 18;
-    case ORC_FAST: return 17;
+    case ORC_FAST: case ORC_MXFP4: return 17;
+    case ORC_NVFP4: return 36;
     case ORC_Q4_K: return 144;
     case ORC_Q5_K: return 176;
     case ORC_Q6_K: return 210;
@@ -250,6 +263,26 @@ int orc_to_float(int t, const void *src, float *y, int64_t n) {
             for (int j = 0; j < 16; ++j) {
                 y[j] = (float)k_cb[b[j] & 0xf] * d;
                 y[j + 16] = (float)k_cb[b[j] >> 4] * d;
+            }
+        }
+        return 0;
+    case ORC_MXFP4:   /* e, then the FAST value bytes (src/quant_types.cpp:397-407) */
+        for (int64_t i = 0; i < n / 32; ++i, b += 17, y += 32) {
+            const float d = orc_e8m0_half(b[0]);
+            for (int j = 0; j < 16; ++j) {
+                y[j] = (float)k_e2m1[b[1 + j] & 0xf] * d;
+                y[j + 16] = (float)k_e2m1[b[1 + j] >> 4] * d;
+            }
+        }
+        return 0;
+    case ORC_NVFP4:   /* four scales, then four 8-byte sub-blocks of 16 values (src/quant_types.cpp:409-422) */
+        for (int64_t i = 0; i < n / 64; ++i, b += 36) {
+            for (int s = 0; s < 4; ++s, y += 16) {
+                const float d = nv_scale(b[s]);
+                for (int j = 0; j < 8; ++j) {
+                    y[j] = (float)k_e2m1[b[4 + 8 * s + j] & 0xf] * d;
+                    y[j + 8] = (float)k_e2m1[b[4 + 8 * s + j] >> 4] * d;
+                }
             }
         }
         return 0;
@@ -747,6 +780,72 @@ static void enc_iq4_xs(const float *x, uint8_t *out, int64_t k) {
     }
 }
 
+/* ggml's best_index_mxfp4: the codebook entry whose value times e is nearest x, the first on a tie
+ * (src/quantize.cpp:697-709) */
+static uint8_t e2m1_index(float x, float e) {
+    int best = 0;
+    float best_err = fabsf((float)k_e2m1[0] * e - x);
+    for (int i = 1; i < 16; ++i) {
+        const float err = fabsf((float)k_e2m1[i] * e - x);
+        if (err < best_err) { best = i; best_err = err; }
+    }
+    return (uint8_t)best;
+}
+
+/* MXFP4 (src/quantize.cpp:711-729): e = floor(log2(amax)) - 2 + 127 (log2f; the float converted as the
+ * reference's x86 build does, through int32), d = 2^(e - 128), each value's nearest E2M1 level */
+static void enc_mxfp4(const float *x, uint8_t *out, int64_t k) {
+    for (int64_t i = 0; i < k / 32; ++i, x += 32, out += 17) {
+        float amax = 0.0f;
+        for (int j = 0; j < 32; ++j)
+            if (amax < fabsf(x[j])) amax = fabsf(x[j]);
+        const uint8_t e = amax > 0.0f ? (uint8_t)(int32_t)(floorf(log2f(amax)) - 2 + 127) : 0;
+        const float d = orc_e8m0_half(e);
+        out[0] = e;
+        for (int j = 0; j < 16; ++j) out[1 + j] = (uint8_t)(e2m1_index(x[j], d) | (e2m1_index(x[16 + j], d) << 4));
+    }
+}
+
+/* ggml_fp32_to_ue4m3 (src/quantize.cpp:670-694): round to nearest on the fp32 bits (the bit below the 3
+ * mantissa bits decides), clamped to 448 and the largest code 0x7E, subnormals m * 2^-9 by x * 512 + 0.5 */
+static uint8_t f32_to_ue4m3(float x) {
+    if (!(x > 0.0f)) return 0;
+    if (x > 448.0f) x = 448.0f;
+    uint32_t bits;
+    memcpy(&bits, &x, 4);
+    int e = (int)((bits >> 23) & 0xff) - 127 + 7;
+    if (e <= 0) {
+        int m = (int)(x * 512.0f + 0.5f);
+        if (m > 7) m = 7;
+        return m < 1 ? 0 : (uint8_t)m;
+    }
+    if (e >= 15) return 0x7e;
+    int m = (int)((bits >> 20) & 7) + (int)((bits >> 19) & 1);
+    if (m > 7) {
+        m = 0;
+        if (++e >= 15) return 0x7e;
+    }
+    return (uint8_t)((e << 3) | m);
+}
+
+/* NVFP4 (src/quantize.cpp:731-750): per 16 values the UE4M3 code of amax / 6, its half-scale value d, each
+ * value's nearest E2M1 level */
+static void enc_nvfp4(const float *x, uint8_t *out, int64_t k) {
+    for (int64_t i = 0; i < k / 64; ++i, x += 64, out += 36) {
+        for (int s = 0; s < 4; ++s) {
+            const float *xb = x + 16 * s;
+            float amax = 0.0f;
+            for (int j = 0; j < 16; ++j)
+                if (amax < fabsf(xb[j])) amax = fabsf(xb[j]);
+            const uint8_t ue = f32_to_ue4m3(amax / 6.0f);
+            const float d = orc_ue4m3_half(ue);
+            out[s] = ue;
+            for (int j = 0; j < 8; ++j)
+                out[4 + 8 * s + j] = (uint8_t)(e2m1_index(xb[j], d) | (e2m1_index(xb[8 + j], d) << 4));
+        }
+    }
+}
+
 static void enc_row(int t, const float *x, uint8_t *y, int64_t k) {
     switch (t) {
     case ORC_F32: memcpy(y, x, (size_t)k * 4); break;
@@ -758,6 +857,8 @@ static void enc_row(int t, const float *x, uint8_t *y, int64_t k) {
     case ORC_Q6_K: enc_q6_k(x, y, k); break;
     case ORC_FP4: enc_fp4(x, y, k); break;
     case ORC_FAST: enc_fast(x, y, k); break;
+    case ORC_MXFP4: enc_mxfp4(x, y, k); break;
+    case ORC_NVFP4: enc_nvfp4(x, y, k); break;
     }
 }
 
@@ -884,8 +985,8 @@ void orc_quantize_q8_k(const float *x, int64_t k, int8_t *qK, float *dK, int32_t
 
 int orc_group_size(int t) {
     switch (t) {
-    case ORC_Q8_0: case ORC_FAST: case ORC_Q4_K: case ORC_Q5_K: case ORC_IQ4_XS: return 32;
-    case ORC_FP4: case ORC_Q6_K: return 16;
+    case ORC_Q8_0: case ORC_FAST: case ORC_Q4_K: case ORC_Q5_K: case ORC_IQ4_XS: case ORC_MXFP4: return 32;
+    case ORC_FP4: case ORC_Q6_K: case ORC_NVFP4: return 16;
     default: return 0;
     }
 }
@@ -904,6 +1005,15 @@ static inline int raw_level(int t, const uint8_t *row, int v) {
         const uint8_t *b = row + 17 * (v >> 5);
         const int j = v & 31;
         return k_cb[j < 16 ? (b[j] & 0xf) : (b[j - 16] >> 4)];
+    }
+    case ORC_MXFP4: {
+        const uint8_t *b = row + 17 * (v >> 5) + 1;
+        const int j = v & 31;
+        return k_e2m1[j < 16 ? (b[j] & 0xf) : (b[j - 16] >> 4)];
+    }
+    case ORC_NVFP4: {
+        const uint8_t q = row[36 * (v >> 6) + 4 + 8 * ((v >> 4) & 3) + (v & 7)];
+        return k_e2m1[(v & 8) ? q >> 4 : q & 0xf];
     }
     case ORC_Q4_K: return k4_level(row + 144 * (v >> 8), v & 255);
     case ORC_Q5_K: return k5_level(row + 176 * (v >> 8), v & 255);
@@ -934,6 +1044,9 @@ int orc_block_dots(int t, const void *W, size_t rb, int N, int K, const int8_t *
  *   Q8_0  (e * dx) * s                               src/matvec_q.hip:1566-1573, src/expert_cpu.cpp:223-229
  *   FP4   (e0 * dx) * s0 + (e1 * dx) * s1            src/matvec_q.hip:1310-1327 (P4ROCmFP4::block)
  *   FAST  (e * dx) * (s0 + s1)                       src/matvec_q.hip:1492-1502, src/expert_cpu.cpp:50-63
+ *   MXFP4 (e * dx) * (s0 + s1), e the E8M0 scale     src/matvec_q.hip:1461-1472 (PFMXFP4), 1492-1502
+ *   NVFP4 per 32 values (sub-blocks 2h, 2h + 1 of a 64-block): (dx * e0) * s0 + (dx * e1) * s1
+ *                                                    src/matvec_q.hip:1357-1372 (P4NVFP4::block)
  *   Q4_K  per 8 lanes of 16 bytes: (d * dx) * isum - (dmin * dx) * msum     src/matvec_q.hip:1752-1789
  *   Q5_K  the same with 5-bit levels (qh bit 2c / 2c + 1 as bit 4)           src/matvec_q.hip:1752-1789,1928-1930
  *   Q6_K  per 8 lanes of 16 bytes: (d * dx) * (isum - 32 * offs)            src/matvec_q.hip:1716-1750
@@ -972,6 +1085,30 @@ static float row_q8(int t, const uint8_t *row, int K, const int8_t *q, const flo
             const float term = orc_ue4m3_half(b[16]) * d[ib] * (float)s;
             acc += term;
             m += fabs((double)term);
+        }
+    } else if (t == ORC_MXFP4) {
+        for (int ib = 0; ib < K / 32; ++ib) {
+            const uint8_t *b = row + 17 * ib;
+            int s = 0;
+            for (int j = 0; j < 16; ++j)
+                s += k_e2m1[b[1 + j] & 0xf] * q[32 * ib + j] + k_e2m1[b[1 + j] >> 4] * q[32 * ib + 16 + j];
+            const float term = orc_e8m0_half(b[0]) * d[ib] * (float)s;
+            acc += term;
+            m += fabs((double)term);
+        }
+    } else if (t == ORC_NVFP4) {
+        for (int ib = 0; ib < K / 32; ++ib) {
+            const uint8_t *b = row + 36 * (ib >> 1);
+            const int s0b = 2 * (ib & 1);   /* sub-blocks s0b (values 0..15) and s0b + 1 (16..31) */
+            int s0 = 0, s1 = 0;
+            for (int j = 0; j < 16; ++j) {
+                s0 += raw_level(ORC_NVFP4, row, 32 * ib + j) * q[32 * ib + j];
+                s1 += raw_level(ORC_NVFP4, row, 32 * ib + 16 + j) * q[32 * ib + 16 + j];
+            }
+            const float t0 = d[ib] * nv_scale(b[s0b]) * (float)s0;
+            const float t1 = d[ib] * nv_scale(b[s0b + 1]) * (float)s1;
+            acc += t0 + t1;
+            m += fabs((double)t0) + fabs((double)t1);
         }
     } else if (t == ORC_Q4_K || t == ORC_Q5_K) {
         const int q5 = t == ORC_Q5_K, BY = q5 ? 176 : 144;

@@ -34,13 +34,14 @@ extern "C" {
 
 /* ggml type ids of the path */
 enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14, ORC_IQ4_XS = 23, ORC_BF16 = 30,
-       ORC_FP4 = 100, ORC_FAST = 101 };
+       ORC_MXFP4 = 39, ORC_NVFP4 = 40, ORC_FP4 = 100, ORC_FAST = 101 };
 
 /* ---- scalars */
 uint16_t orc_f32_to_f16(float f);
 float orc_f16_to_f32(uint16_t h);
 float orc_ue4m3_half(uint8_t e);      /* quant_types.cpp scale decoder (GGUF types 100/101) */
 float orc_ue4m3_fp4common(uint8_t e); /* fp4_common.h decoder (gemm_act_fp4 only) */
+float orc_e8m0_half(uint8_t e);       /* MXFP4's E8M0 scale at half scale */
 void orc_f32_to_f16_n(const float *x, uint16_t *h, int64_t n);
 void orc_f16_to_f32_n(const uint16_t *h, float *x, int64_t n);
 

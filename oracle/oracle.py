@@ -13,11 +13,13 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liboracle.so")
 REF_PATH = os.path.join(_HERE, "_ref", "libref.so")
 
-Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS, FP4, FAST, F32, F16, BF16 = 8, 12, 13, 14, 23, 100, 101, 0, 1, 30
+Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS, MXFP4, NVFP4, FP4, FAST, F32, F16, BF16 = 8, 12, 13, 14, 23, 39, 40, 100, 101, 0, 1, 30
 KQ = (Q4_K, Q5_K, Q6_K, IQ4_XS)
-BLOCK = {Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ4_XS: 256, FP4: 32, FAST: 32, F32: 1, F16: 1, BF16: 1}
-BYTES = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136, FP4: 18, FAST: 17, F32: 4, F16: 2, BF16: 2}
-GROUP = {Q8_0: 32, FP4: 16, FAST: 32, Q4_K: 32, Q5_K: 32, Q6_K: 16, IQ4_XS: 32}
+BLOCK = {Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ4_XS: 256, MXFP4: 32, NVFP4: 64, FP4: 32, FAST: 32, F32: 1, F16: 1,
+         BF16: 1}
+BYTES = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136, MXFP4: 17, NVFP4: 36, FP4: 18, FAST: 17, F32: 4, F16: 2,
+         BF16: 2}
+GROUP = {Q8_0: 32, FP4: 16, FAST: 32, Q4_K: 32, Q5_K: 32, Q6_K: 16, IQ4_XS: 32, MXFP4: 32, NVFP4: 16}
 
 _lib = None
 _ref = None
@@ -46,6 +48,8 @@ def lib():
         L.orc_ue4m3_half.argtypes = [C.c_uint8]
         L.orc_ue4m3_fp4common.restype = C.c_float
         L.orc_ue4m3_fp4common.argtypes = [C.c_uint8]
+        L.orc_e8m0_half.restype = C.c_float
+        L.orc_e8m0_half.argtypes = [C.c_uint8]
         L.orc_f32_to_f16_n.argtypes = [vp, vp, i64]
         L.orc_f16_to_f32_n.argtypes = [vp, vp, i64]
         L.orc_row_size.restype = sz

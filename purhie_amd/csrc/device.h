@@ -31,27 +31,47 @@ __device__ __forceinline__ float ue4m3_half(uint32_t e) {
 // signed int8 dot of 4 bytes, accumulated: v_dot4_i32_i8
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
-// Four 4-bit ROCmFP4 codes -> four int8 codebook values {0, 1, 2, 3, 4, 6, 8, 10} with the sign in bit 3:
+// Four 4-bit FP4 codes -> four int8 codebook values {0, 1, 2, 3, 4, 6, 8, TOP} with the sign in bit 3:
 // two byte lookups by the 3-bit magnitude index (v_perm_b32 on a positive and a negative table of 8), then
 // a third v_perm picks, per byte, the positive (selector i) or the negative (selector 4 + i) result, the
 // selector built from the sign bit. sel: the magnitude indices (bytes 0..7); sgn4: 4 in the bytes whose
-// code is negative, 0 elsewhere.
+// code is negative, 0 elsewhere. TOP 10: ROCmFP4's codebook; TOP 12: E2M1 at half scale (MXFP4, NVFP4).
+template <int TOP = 10>
 __device__ __forceinline__ int fp4_pick(uint32_t sel, uint32_t sgn4) {
-    const uint32_t pos = __builtin_amdgcn_perm(0x0a080604u, 0x03020100u, sel);
-    const uint32_t neg = __builtin_amdgcn_perm(0xf6f8fafcu, 0xfdfeff00u, sel);
+    const uint32_t pos = __builtin_amdgcn_perm(0x00080604u | (uint32_t)TOP << 24, 0x03020100u, sel);
+    const uint32_t neg = __builtin_amdgcn_perm(0x00f8fafcu | (uint32_t)(256 - TOP) << 24, 0xfdfeff00u, sel);
     return (int)__builtin_amdgcn_perm(neg, pos, 0x03020100u | sgn4);
 }
 
 // the codes in the low nibbles of the bytes of w
-__device__ __forceinline__ int fp4x4_lo(uint32_t w) { return fp4_pick(w & 0x07070707u, (w & 0x08080808u) >> 1); }
+template <int TOP = 10>
+__device__ __forceinline__ int fp4x4_lo(uint32_t w) {
+    return fp4_pick<TOP>(w & 0x07070707u, (w & 0x08080808u) >> 1);
+}
 
 // the codes in the high nibbles of the bytes of w
+template <int TOP = 10>
 __device__ __forceinline__ int fp4x4_hi(uint32_t w) {
-    return fp4_pick((w >> 4) & 0x07070707u, (w & 0x80808080u) >> 5);
+    return fp4_pick<TOP>((w >> 4) & 0x07070707u, (w & 0x80808080u) >> 5);
 }
 
 // four codes, one per byte (0..15)
-__device__ __forceinline__ int fp4x4(uint32_t n) { return fp4x4_lo(n); }
+template <int TOP = 10>
+__device__ __forceinline__ int fp4x4(uint32_t n) { return fp4x4_lo<TOP>(n); }
+
+// the int8 level of one code (0..15)
+template <int TOP = 10>
+__device__ __forceinline__ int fp4_level(uint32_t nib) { return (int)(int8_t)(fp4x4<TOP>(nib) & 0xffu); }
+
+// MXFP4's E8M0 scale byte at half scale, 2^(e - 128) (reference src/quant_types.cpp:390-395): e = 0, 1 are the
+// float subnormals 2^-128, 2^-127, else the exponent field e - 1
+__device__ __forceinline__ float e8m0_half(uint32_t e) {
+    e &= 0xffu;
+    return __uint_as_float(e < 2 ? 0x00200000u << e : (e - 1) << 23);
+}
+
+// NVFP4's scale byte: UE4M3 at half scale, the sign bit ignored (reference src/quant_types.cpp:409-416)
+__device__ __forceinline__ float nv_scale(uint32_t e) { return ue4m3_half(e & 0x7fu); }
 
 // Four IQ4_NL / IQ4_XS indices (one per byte, 0..15) -> their int8 levels, ggml's kvalues_iq4nl {-127, -104, -83,
 // -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113}: the low 3 bits look up both halves of the table with

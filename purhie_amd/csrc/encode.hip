@@ -1,9 +1,9 @@
 // encode.hip -- the weight encoders on the GPU: fp32 rows -> GGUF blocks (Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS,
-// ROCmFP4, ROCmFP4_FAST) and F32 / F16 / BF16 rows, bit-identical to the reference's CPU encoders
-// (src/quantize.cpp:28-64, 161-358, 362-476, 851-974, 975-1109), which reproduce ggml's _ref quantizers and
-// ROCmFPX's rocmfp4.c.
+// MXFP4, NVFP4, ROCmFP4, ROCmFP4_FAST) and F32 / F16 / BF16 rows, bit-identical to the reference's CPU encoders
+// (src/quantize.cpp:28-64, 161-358, 362-476, 651-750, 851-974, 975-1109), which reproduce ggml's _ref quantizers
+// and ROCmFPX's rocmfp4.c.
 //
-// One thread per block (Q8_0, ROCmFP4, FAST: 32 values) or super-block (K-quants: 256 values). The
+// One thread per block (Q8_0, ROCmFP4, FAST, MXFP4: 32 values; NVFP4: 64) or super-block (K-quants: 256). The
 // searches are the reference's, step for step, in single precision: this file is compiled without
 // floating-point contraction (a fused multiply-add rounds a sum of squares differently and can pick
 // another scale on a tie), divisions and square roots are IEEE-rounded (hipcc's default), and nothing is
@@ -431,6 +431,82 @@ __device__ void enc_fast_block(const float *x, uint8_t *out) {
     out[16] = e;
 }
 
+// ---------------------------------------------------------------- MXFP4 / NVFP4 (src/quantize.cpp:651-750)
+
+__constant__ float k_e2m1f[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};  // E2M1 at half scale
+
+// ggml's best_index_mxfp4: the first index whose level times e is nearest x (a NaN x: every error is NaN, 0)
+__device__ inline uint8_t e2m1_index(float x, float e) {
+    int best = 0;
+    float best_err = fabsf(k_e2m1f[0] * e - x);
+    for (int i = 1; i < 16; ++i) {
+        const float err = fabsf(k_e2m1f[i] * e - x);
+        if (err < best_err) {
+            best = i;
+            best_err = err;
+        }
+    }
+    return (uint8_t)best;
+}
+
+// floor(log2f(a)) as the host's libm gives it. It differs from the exponent of a only where a lies a few units
+// below a power of two and log2f rounds up to the integer; there log2f equals the double log2 rounded to float,
+// which is what this returns (the two floors agree for every positive finite float, checked on the host).
+__device__ inline float floor_log2f(float a) { return floorf((float)log2((double)a)); }
+
+// float -> uint8_t as an x86-64 build converts it: truncation to int32 (out of range or NaN: INT_MIN), low byte
+__device__ inline uint8_t x86_u8(float v) {
+    const int i = (v >= -2147483648.0f && v < 2147483648.0f) ? (int)v : (int)0x80000000u;
+    return (uint8_t)i;
+}
+
+// MXFP4: e = floor(log2(amax)) - 2 + 127, d = 2^(e - 128), each value's nearest level
+__device__ void enc_mxfp4_block(const float *x, uint8_t *out) {
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j)
+        if (amax < fabsf(x[j])) amax = fabsf(x[j]);
+    const uint8_t e = amax > 0.0f ? x86_u8(floor_log2f(amax) - 2 + 127) : 0;
+    const float d = e8m0_half(e);
+    out[0] = e;
+    for (int j = 0; j < 16; ++j) out[1 + j] = (uint8_t)(e2m1_index(x[j], d) | (e2m1_index(x[16 + j], d) << 4));
+}
+
+// ggml_fp32_to_ue4m3: nearest on the fp32 bits (the bit below the kept 3 decides), clamped to 448 and the code
+// 0x7E, subnormal codes m = (int)(x * 512 + 0.5)
+__device__ inline uint8_t f32_to_ue4m3(float x) {
+    if (!(x > 0.0f)) return 0;
+    if (x > 448.0f) x = 448.0f;
+    const uint32_t bits = __float_as_uint(x);
+    int e = (int)((bits >> 23) & 0xffu) - 120;
+    if (e <= 0) {
+        int m = (int)(x * 512.0f + 0.5f);
+        if (m > 7) m = 7;
+        return m < 1 ? 0 : (uint8_t)m;
+    }
+    if (e >= 15) return 0x7e;
+    int m = (int)((bits >> 20) & 7u) + (int)((bits >> 19) & 1u);
+    if (m > 7) {
+        m = 0;
+        if (++e >= 15) return 0x7e;
+    }
+    return (uint8_t)((e << 3) | m);
+}
+
+// NVFP4: per 16 values the UE4M3 code of amax / 6 and each value's nearest level at its half-scale value
+__device__ void enc_nvfp4_block(const float *x, uint8_t *out) {
+    for (int s = 0; s < 4; ++s) {
+        const float *xb = x + 16 * s;
+        float amax = 0.0f;
+        for (int j = 0; j < 16; ++j)
+            if (amax < fabsf(xb[j])) amax = fabsf(xb[j]);
+        const uint8_t ue = f32_to_ue4m3(amax / 6.0f);
+        const float d = ue4m3_half(ue);
+        out[s] = ue;
+        for (int j = 0; j < 8; ++j)
+            out[4 + 8 * s + j] = (uint8_t)(e2m1_index(xb[j], d) | (e2m1_index(xb[8 + j], d) << 4));
+    }
+}
+
 // ---------------------------------------------------------------- IQ4_XS (src/quantize.cpp:851-974)
 
 __constant__ int8_t k_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
@@ -530,12 +606,15 @@ __device__ void enc_iq4_xs_block(const float *x, uint8_t *out) {
 template <int TYPE>
 __global__ void __launch_bounds__(256) k_encode(const float *__restrict__ x, uint8_t *__restrict__ y, long long nrows,
                                                 long long ncols, long long row_bytes) {
-    constexpr int VALS = (TYPE == TY_Q4_K || TYPE == TY_Q5_K || TYPE == TY_Q6_K || TYPE == TY_IQ4_XS) ? 256 : 32;
+    constexpr int VALS = (TYPE == TY_Q4_K || TYPE == TY_Q5_K || TYPE == TY_Q6_K || TYPE == TY_IQ4_XS) ? 256
+                         : TYPE == TY_NVFP4                                                          ? 64
+                                                                                                      : 32;
     constexpr int BYTES = TYPE == TY_Q8_0   ? 34
                           : TYPE == TY_Q4_K ? 144
                           : TYPE == TY_Q5_K ? 176
                           : TYPE == TY_Q6_K ? 210
                           : TYPE == TY_IQ4_XS ? 136
+                          : TYPE == TY_NVFP4 ? 36
                           : TYPE == TY_FP4  ? 18
                                             : 17;
     const long long per_row = ncols / VALS;
@@ -550,6 +629,8 @@ __global__ void __launch_bounds__(256) k_encode(const float *__restrict__ x, uin
     else if (TYPE == TY_IQ4_XS) enc_iq4_xs_block(src, dst);
     else if (TYPE == TY_Q6_K) enc_q6_k_block(src, dst);
     else if (TYPE == TY_FP4) enc_fp4_block(src, dst);
+    else if (TYPE == TY_MXFP4) enc_mxfp4_block(src, dst);
+    else if (TYPE == TY_NVFP4) enc_nvfp4_block(src, dst);
     else enc_fast_block(src, dst);
 }
 
@@ -565,7 +646,8 @@ __global__ void k_encode_float(const float *__restrict__ x, uint8_t *__restrict_
 int encode_block_values(int type) {
     switch (type) {
     case 0: case 1: case 30: return 1;
-    case TY_Q8_0: case TY_FP4: case TY_FAST: return 32;
+    case TY_Q8_0: case TY_FP4: case TY_FAST: case TY_MXFP4: return 32;
+    case TY_NVFP4: return 64;
     case TY_Q4_K: case TY_Q5_K: case TY_Q6_K: case TY_IQ4_XS: return 256;
     }
     return 0;
@@ -591,6 +673,12 @@ hipError_t launch_encode(int type, const float *x, uint8_t *y, long long nrows, 
     case TY_Q6_K: hipLaunchKernelGGL(k_encode<TY_Q6_K>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes); break;
     case TY_FP4: hipLaunchKernelGGL(k_encode<TY_FP4>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes); break;
     case TY_FAST: hipLaunchKernelGGL(k_encode<TY_FAST>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes); break;
+    case TY_MXFP4:
+        hipLaunchKernelGGL(k_encode<TY_MXFP4>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes);
+        break;
+    case TY_NVFP4:
+        hipLaunchKernelGGL(k_encode<TY_NVFP4>, grid, dim3(256), 0, stream, x, y, nrows, ncols, row_bytes);
+        break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

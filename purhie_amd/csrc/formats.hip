@@ -78,6 +78,29 @@ __global__ void k_dequant(int type, const uint8_t *__restrict__ src, float *__re
         }
         break;
     }
+    case TY_MXFP4: {  // E8M0 scale, then FAST's value bytes (src/quant_types.cpp:397-407)
+        const uint8_t *b = src + g * 17;
+        const float d = e8m0_half(b[0]);
+        for (int j = 0; j < 16; ++j) {
+            o[j] = (float)fp4_level<12>(b[1 + j] & 0xfu) * d;
+            o[j + 16] = (float)fp4_level<12>(b[1 + j] >> 4) * d;
+        }
+        break;
+    }
+    case TY_NVFP4: {  // half (g & 1) of a 64-value block: sub-blocks 2h, 2h + 1 (src/quant_types.cpp:409-422)
+        const uint8_t *b = src + (g >> 1) * 36;
+        const int s0 = 2 * (int)(g & 1);
+        for (int s = s0; s < s0 + 2; ++s) {
+            const float d = nv_scale(b[s]);
+            const uint8_t *q = b + 4 + 8 * s;
+            float *os = o + 16 * (s - s0);
+            for (int j = 0; j < 8; ++j) {
+                os[j] = (float)fp4_level<12>(q[j] & 0xfu) * d;
+                os[j + 8] = (float)fp4_level<12>(q[j] >> 4) * d;
+            }
+        }
+        break;
+    }
     case TY_Q6_K: {
         const uint8_t *b = src + (g >> 3) * 210;
         const int part = (int)(g & 7);  // values 32 part .. 32 part + 31
@@ -122,6 +145,8 @@ void to_float_sync_q6_k(const void *s, float *d, int64_t n) { (void)qt_to_float(
 void to_float_sync_iq4_xs(const void *s, float *d, int64_t n) { (void)qt_to_float(TY_IQ4_XS, s, d, n); }
 void to_float_sync_fp4(const void *s, float *d, int64_t n) { (void)qt_to_float(QT_Q4_0_ROCMFP4, s, d, n); }
 void to_float_sync_fast(const void *s, float *d, int64_t n) { (void)qt_to_float(QT_Q4_0_ROCMFP4_FAST, s, d, n); }
+void to_float_sync_mxfp4(const void *s, float *d, int64_t n) { (void)qt_to_float(QT_MXFP4, s, d, n); }
+void to_float_sync_nvfp4(const void *s, float *d, int64_t n) { (void)qt_to_float(QT_NVFP4, s, d, n); }
 void to_float_sync_f32(const void *s, float *d, int64_t n) { (void)qt_to_float(QT_F32, s, d, n); }
 void to_float_sync_f16(const void *s, float *d, int64_t n) { (void)qt_to_float(QT_F16, s, d, n); }
 void to_float_sync_bf16(const void *s, float *d, int64_t n) { (void)qt_to_float(QT_BF16, s, d, n); }
@@ -136,6 +161,8 @@ const qt_traits k_traits[] = {
     {TY_Q6_K, "q6_K", 256, 210, to_float_sync_q6_k, 1},
     {TY_IQ4_XS, "iq4_xs", 256, 136, to_float_sync_iq4_xs, 1},
     {QT_BF16, "bf16", 1, 2, to_float_sync_bf16, 1},
+    {QT_MXFP4, "mxfp4", 32, 17, to_float_sync_mxfp4, 1},
+    {QT_NVFP4, "nvfp4", 64, 36, to_float_sync_nvfp4, 1},
     {QT_Q4_0_ROCMFP4, "q4_0_rocmfp4", 32, 18, to_float_sync_fp4, 1},
     {QT_Q4_0_ROCMFP4_FAST, "q4_0_rocmfp4_fast", 32, 17, to_float_sync_fast, 1},
 };

@@ -68,17 +68,20 @@ __global__ void k_act_f16(const int8_t *__restrict__ q, const float *__restrict_
 // Each fills rows of the LDS weight tile [GB_N][LDS_ROW] (fp16, the type's K order) for K values
 // k0 .. k0 + 127, and for Q8_0 the per-row block scales sdw[4][GB_N].
 
-// 256-entry table: byte -> half2(CB[low nibble], CB[high nibble])
+// 256-entry table: byte -> half2(CB[low nibble], CB[high nibble]) (TOP: the codebook's top level)
+template <int TOP = 10>
 __device__ __forceinline__ void init_fp4_lut(uint32_t *lut) {
     const int b = threadIdx.x;  // blockDim == 256
-    const int lo = (int)(int8_t)(fp4x4(b & 15) & 0xffu), hi = (int)(int8_t)(fp4x4(b >> 4) & 0xffu);
+    const int lo = fp4_level<TOP>(b & 15), hi = fp4_level<TOP>(b >> 4);
     h2 v;
     v.x = (_Float16)(float)lo;
     v.y = (_Float16)(float)hi;
     lut[b] = __builtin_bit_cast(uint32_t, v);
 }
 
-// one 32-value FP4 block: 16 value bytes (4 dwords) and the two half-block scales -> 16 half2 in LDS
+// one 32-value FP4 block: 16 value bytes (4 dwords) and the two half-block scales -> 16 half2 in LDS (the scales
+// are fp16 values: UE4M3 at half scale lies in [2^-10, 240], and a level times it is exact; 1 for the E8M0 types,
+// whose scale is applied per block outside the product)
 __device__ __forceinline__ void fp4_block_to_lds(const uint32_t qs[4], float e0, float e1, const uint32_t *lut,
                                                  _Float16 *dst) {
     h2 sc;
@@ -115,7 +118,8 @@ struct GStage;
 // ROCmFP4: thread t decodes row t / 2, blocks 2 (t & 1) and 2 (t & 1) + 1 of the stage (36 bytes, 4-aligned)
 template <>
 struct GStage<TY_FP4> {
-    static constexpr bool PERM = true, ROW_SCALE = false;
+    static constexpr bool PERM = true, ROW_SCALE = false, LUT = true;
+    static constexpr int TOP = 10;
     struct Raw {
         uint32_t w[9];
     };
@@ -146,7 +150,8 @@ struct GStage<TY_FP4> {
 // realigned by v_alignbyte)
 template <>
 struct GStage<TY_FAST> {
-    static constexpr bool PERM = true, ROW_SCALE = false;
+    static constexpr bool PERM = true, ROW_SCALE = false, LUT = true;
+    static constexpr int TOP = 10;
     // The pair starts 0 or 2 bytes past a dword boundary (row bytes are a multiple of 4): nine aligned dwords
     // from the boundary below cover its 34 bytes. A pair at offset 0 is never a row's last (that one starts
     // at row_bytes - 34, 2 past a boundary), so the two spare bytes it reads are still inside the row.
@@ -189,7 +194,8 @@ struct GStage<TY_FAST> {
 // (exact in fp16) in natural order, and the two fp16 block scales into sdw[block][row]
 template <>
 struct GStage<TY_Q8_0> {
-    static constexpr bool PERM = false, ROW_SCALE = true;
+    static constexpr bool PERM = false, ROW_SCALE = true, LUT = false;
+    static constexpr int TOP = 10;
     struct Raw {
         uint32_t w[17];
     };
@@ -223,6 +229,37 @@ struct GStage<TY_Q8_0> {
     }
 };
 
+// MXFP4: FAST's pair of 17-byte blocks with the E8M0 scale first (byte 0 of a block, values bytes 1..16). An
+// E8M0 scale (2^-128 .. 2^127) is no fp16 value, so the levels go into LDS unscaled (exact) and the scales
+// into sdw as Q8_0's do: each block's exact integer dot then takes (e dx) outside the MFMA, the reference's
+// per-block form (src/matvec_q.hip:1461-1472).
+template <>
+struct GStage<TY_MXFP4> {
+    static constexpr bool PERM = true, ROW_SCALE = true, LUT = true;
+    static constexpr int TOP = 12;
+    using Raw = GStage<TY_FAST>::Raw;
+    __device__ static void load(const uint8_t *W, long long rb, int N, int n0, int k0, Raw &r) {
+        GStage<TY_FAST>::load(W, rb, N, n0, k0, r);
+    }
+    __device__ static void store(const Raw &r, const uint32_t *lut, _Float16 *sW, float *sdw) {
+        const int row = threadIdx.x >> 1, p = threadIdx.x & 1;
+        _Float16 *dst = sW + row * LDS_ROW + 64 * p;
+        uint32_t w[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) w[k] = align_bytes(k < 8 ? r.w[k + 1] : 0u, r.w[k], r.off);
+        // block 0: byte 0 scale, bytes 1..16 values; block 1: byte 17 scale, bytes 18..33 values
+        uint32_t qa[4], qb[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            qa[k] = align_bytes(w[k + 1], w[k], 1);
+            qb[k] = align_bytes(w[k + 5], w[k + 4], 2);
+        }
+        fp4_block_to_lds(qa, 1.0f, 1.0f, lut, dst);
+        fp4_block_to_lds(qb, 1.0f, 1.0f, lut, dst + 32);
+        sdw[(2 * p) * GB_N + row] = e8m0_half(w[0]);
+        sdw[(2 * p + 1) * GB_N + row] = e8m0_half(w[4] >> 8);
+    }
+};
 
 template <int TYPE>
 __global__ void __launch_bounds__(G_THREADS, 2) k_gemm(GemmArgs a) {
@@ -250,7 +287,7 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm(GemmArgs a) {
         n0 = blockIdx.y * GB_N;
     }
     const uint8_t *W = a.W + (long long)e * a.N * a.row_bytes;
-    if (!S::ROW_SCALE) init_fp4_lut(lut);
+    if (S::LUT) init_fp4_lut<S::TOP>(lut);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wn = (wave & 1) * 64, wt = (wave >> 1) * 64;  // the wave's 64 x 64 sub-tile
@@ -370,7 +407,7 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm(GemmArgs a) {
 
 int gemm_supported(int type) {
     return type == TY_FP4 || type == TY_FAST || type == TY_Q8_0 || type == TY_Q4_K || type == TY_Q5_K || type == TY_Q6_K ||
-           type == TY_IQ4_XS;
+           type == TY_IQ4_XS || type == TY_MXFP4 || type == TY_NVFP4;
 }
 
 int gemm_k_multiple() { return GB_K; }
@@ -380,7 +417,7 @@ int gemm_token_tile() { return GB_T; }
 hipError_t launch_act_f16(int type, const int8_t *q, const float *d, int T, int K, int Tpad, _Float16 *xh, float *dxp,
                           hipStream_t stream) {
     const long long n = (long long)(Tpad + 1) * (K / 32);
-    const int perm = GStage<TY_FP4>::PERM && (type == TY_FP4 || type == TY_FAST);
+    const int perm = type == TY_FP4 || type == TY_FAST || type == TY_MXFP4;
     hipLaunchKernelGGL(k_act_f16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, q, d, T, K, Tpad, perm, xh,
                        dxp);
     return hipGetLastError();
@@ -391,6 +428,7 @@ hipError_t launch_gemm(int type, const GemmArgs &a, dim3 grid, hipStream_t strea
     case TY_FP4: hipLaunchKernelGGL(k_gemm<TY_FP4>, grid, dim3(G_THREADS), 0, stream, a); break;
     case TY_FAST: hipLaunchKernelGGL(k_gemm<TY_FAST>, grid, dim3(G_THREADS), 0, stream, a); break;
     case TY_Q8_0: hipLaunchKernelGGL(k_gemm<TY_Q8_0>, grid, dim3(G_THREADS), 0, stream, a); break;
+    case TY_MXFP4: hipLaunchKernelGGL(k_gemm<TY_MXFP4>, grid, dim3(G_THREADS), 0, stream, a); break;
     default: return hipErrorInvalidDeviceFunction;
     }
     return hipGetLastError();
@@ -453,6 +491,7 @@ constexpr int GS_T_MOE = 64;              // tokens per workgroup over MoE exper
 // the stage's two weight blocks of row n0 + t (thread t), decoded into the 64 halves of its LDS row
 template <int TYPE>
 struct SplitStage {
+    static constexpr int TOP = 10;
     static constexpr int BB = TYPE == TY_FP4 ? 18 : 17;  // block bytes
     struct Raw {
         uint32_t w[9];
@@ -490,6 +529,38 @@ struct SplitStage {
     }
 };
 
+// NVFP4: the stage is one 36-byte block (4-aligned). Its sub-blocks (0, 1) and (2, 3) are regrouped into the
+// ROCmFP4 byte order of two 32-value blocks (byte i: value i low, value 16 + i high), which the permuted token
+// rows expect, with the four UE4M3 scales as the half-block scales.
+template <>
+struct SplitStage<TY_NVFP4> {
+    static constexpr int TOP = 12;
+    struct Raw {
+        uint32_t w[9];
+    };
+    __device__ static void load(const uint8_t *W, long long rb, int N, int n0, int k0, Raw &r) {
+        const int row = n0 + threadIdx.x;
+        const int rr = row < N ? row : N - 1;
+        const uint8_t *b = W + (long long)rr * rb + (long long)(k0 / 64) * 36;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) r.w[k] = ld32(b + 4 * k);
+    }
+    __device__ static void store(const Raw &r, const uint32_t *lut, _Float16 *sW) {
+        _Float16 *dst = sW + threadIdx.x * GS_ROW;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            uint32_t q[4];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const uint32_t lo = r.w[1 + 4 * h + k], hi = r.w[3 + 4 * h + k];  // sub-blocks 2h, 2h + 1
+                q[k] = (lo & 0x0f0f0f0fu) | ((hi & 0x0f0f0f0fu) << 4);
+                q[2 + k] = ((lo >> 4) & 0x0f0f0f0fu) | (hi & 0xf0f0f0f0u);
+            }
+            fp4_block_to_lds(q, nv_scale(r.w[0] >> (16 * h)), nv_scale(r.w[0] >> (16 * h + 8)), lut, dst + 32 * h);
+        }
+    }
+};
+
 // workgroup tile 256 weight rows x TT tokens (128; 64 for MoE expert tiles, whose runs average a few dozen
 // entries, and for prompts of at most 64 tokens); wave w computes rows 128 (w & 1) .. + 127 x tokens TT / 2 (w >> 1) .. (8 x TT / 32 MFMA tiles): per
 // 32-block a wave reads 8 weight and 2 x TT / 32 token fragments for 16 TT / 32 MFMAs
@@ -521,7 +592,7 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm_split(GemmArgs a) {
         n0 = blockIdx.y * GS_N;
     }
     const uint8_t *W = a.W + (long long)e * a.N * a.row_bytes;
-    init_fp4_lut(lut);
+    init_fp4_lut<S::TOP>(lut);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wn = (wave & 1) * 128, wt = (wave >> 1) * (TT / 2);
@@ -631,7 +702,7 @@ __global__ void __launch_bounds__(G_THREADS, 2) k_gemm_split(GemmArgs a) {
     }
 }
 
-bool gemm_split(int type) { return type == TY_FP4 || type == TY_FAST; }
+bool gemm_split(int type) { return type == TY_FP4 || type == TY_FAST || type == TY_NVFP4; }
 
 int gemm_split_k_multiple() { return GS_K; }
 
@@ -644,7 +715,7 @@ int gemm_rows_per_wg(int type) { return gemm_split(type) ? GS_N : gemm_kquant(ty
 hipError_t launch_act_split(int type, const int8_t *q, const float *d, int T, int K, int rows, int8_t *xq,
                             _Float16 *xs, float *ts, hipStream_t stream) {
     hipLaunchKernelGGL(k_act_split, dim3((unsigned)rows), dim3(256), 0, stream, q, d, T, K,
-                       (type == TY_FP4 || type == TY_FAST) ? 1 : 0, xq, xs, ts);
+                       (type == TY_FP4 || type == TY_FAST || type == TY_NVFP4) ? 1 : 0, xq, xs, ts);
     return hipGetLastError();
 }
 
@@ -657,6 +728,10 @@ hipError_t launch_gemm_split(int type, const GemmArgs &a, dim3 grid, hipStream_t
     case TY_FAST:
         if (a.n_tiles || a.tt == GS_T_MOE) hipLaunchKernelGGL((k_gemm_split<TY_FAST, GS_T_MOE>), grid, dim3(G_THREADS), 0, stream, a);
         else hipLaunchKernelGGL((k_gemm_split<TY_FAST, GS_T>), grid, dim3(G_THREADS), 0, stream, a);
+        break;
+    case TY_NVFP4:
+        if (a.n_tiles || a.tt == GS_T_MOE) hipLaunchKernelGGL((k_gemm_split<TY_NVFP4, GS_T_MOE>), grid, dim3(G_THREADS), 0, stream, a);
+        else hipLaunchKernelGGL((k_gemm_split<TY_NVFP4, GS_T>), grid, dim3(G_THREADS), 0, stream, a);
         break;
     default: return hipErrorInvalidDeviceFunction;
     }

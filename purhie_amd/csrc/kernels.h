@@ -8,7 +8,8 @@
 namespace pq {
 
 // ggml type ids of the path's weight formats
-constexpr int TY_Q8_0 = 8, TY_Q4_K = 12, TY_Q5_K = 13, TY_Q6_K = 14, TY_IQ4_XS = 23, TY_FP4 = 100, TY_FAST = 101;
+constexpr int TY_Q8_0 = 8, TY_Q4_K = 12, TY_Q5_K = 13, TY_Q6_K = 14, TY_IQ4_XS = 23, TY_MXFP4 = 39, TY_NVFP4 = 40,
+              TY_FP4 = 100, TY_FAST = 101;
 
 // quantized activation output pointers (the layout of qmatvec_q8)
 struct Q8Ptrs {

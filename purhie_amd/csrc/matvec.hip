@@ -103,16 +103,26 @@ struct Mv<TY_Q8_0> {
 };
 
 // one 32-value FP4 block (16 value bytes as 4 dwords: value j in the low nibble of byte j, j + 16 in its
-// high nibble) against its Q8_0 activation block: the two half-block integer sums
+// high nibble) against its Q8_0 activation block: the two half-block integer sums (TOP: the codebook's top)
+template <int TOP = 10>
 __device__ __forceinline__ void fp4_block_dots(const uint32_t qs[4], const int4 xa, const int4 xb, int &s0, int &s1) {
-    s0 = dot4(fp4x4_lo(qs[0]), xa.x, 0);
-    s0 = dot4(fp4x4_lo(qs[1]), xa.y, s0);
-    s0 = dot4(fp4x4_lo(qs[2]), xa.z, s0);
-    s0 = dot4(fp4x4_lo(qs[3]), xa.w, s0);
-    s1 = dot4(fp4x4_hi(qs[0]), xb.x, 0);
-    s1 = dot4(fp4x4_hi(qs[1]), xb.y, s1);
-    s1 = dot4(fp4x4_hi(qs[2]), xb.z, s1);
-    s1 = dot4(fp4x4_hi(qs[3]), xb.w, s1);
+    s0 = dot4(fp4x4_lo<TOP>(qs[0]), xa.x, 0);
+    s0 = dot4(fp4x4_lo<TOP>(qs[1]), xa.y, s0);
+    s0 = dot4(fp4x4_lo<TOP>(qs[2]), xa.z, s0);
+    s0 = dot4(fp4x4_lo<TOP>(qs[3]), xa.w, s0);
+    s1 = dot4(fp4x4_hi<TOP>(qs[0]), xb.x, 0);
+    s1 = dot4(fp4x4_hi<TOP>(qs[1]), xb.y, s1);
+    s1 = dot4(fp4x4_hi<TOP>(qs[2]), xb.z, s1);
+    s1 = dot4(fp4x4_hi<TOP>(qs[3]), xb.w, s1);
+}
+
+// one 16-value NVFP4 sub-block (2 dwords: value i in the low nibble of byte i, i + 8 in the high nibble) against
+// its 16 activation values
+__device__ __forceinline__ int nv_sub_dot(uint32_t a0, uint32_t a1, const int4 x) {
+    int s = dot4(fp4x4_lo<12>(a0), x.x, 0);
+    s = dot4(fp4x4_lo<12>(a1), x.y, s);
+    s = dot4(fp4x4_hi<12>(a0), x.z, s);
+    return dot4(fp4x4_hi<12>(a1), x.w, s);
 }
 
 // ROCmFP4 (type 100): a task is a pair of 18-byte blocks (36 bytes, 4-aligned: K % 64 == 0): block 0's
@@ -210,6 +220,61 @@ struct Mv<TY_FAST> {
                 int s0, s1;
                 fp4_block_dots(qs, xv[0], xv[1], s0, s1);
                 acc[t] = __builtin_fmaf(v ? e * x.d[t][dof + j] : 0.0f, (float)(s0 + s1), acc[t]);
+            }
+        }
+    }
+};
+
+// MXFP4 (type 39): a task is a quad of 17-byte blocks (68 bytes, 4-aligned: K % 128 == 0); block j's E8M0
+// scale at byte 17 j, its 16 value bytes from 17 j + 1. Per block the reference's term (e dx) (s0 + s1).
+template <>
+struct Mv<TY_MXFP4> : Mv<TY_FAST> {
+    template <int NT>
+    __device__ static void compute(const Raw &r, const Lane &, const Act<NT> &x, int xo, int dof, int, float acc[NT],
+                                   bool v) {
+        uint32_t w[18];
+#pragma unroll
+        for (int k = 0; k < 17; ++k) w[k] = r.w[k];
+        w[17] = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t qs[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) qs[k] = dw(w, 17 * j + 1 + 4 * k);
+            const float e = e8m0_half(dw(w, 17 * j));
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const int4 *xv = (const int4 *)(x.q[t] + xo + 32 * j);
+                int s0, s1;
+                fp4_block_dots<12>(qs, xv[0], xv[1], s0, s1);
+                acc[t] = __builtin_fmaf(v ? e * x.d[t][dof + j] : 0.0f, (float)(s0 + s1), acc[t]);
+            }
+        }
+    }
+};
+
+// NVFP4 (type 40): a task is one 36-byte block (64 values, 4-aligned): its four scale bytes (dword 0) and four
+// 8-byte sub-blocks (dwords 1..8). Activation blocks 2 g and 2 g + 1 take sub-blocks (0, 1) and (2, 3):
+// (dx e0) s0 + (dx e1) s1 each.
+template <>
+struct Mv<TY_NVFP4> : Mv<TY_FP4> {
+    template <int NT>
+    __device__ static void compute(const Raw &r, const Lane &, const Act<NT> &x, int xo, int dof, int, float acc[NT],
+                                   bool v) {
+        float e[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) e[s] = nv_scale(r.w[0] >> (8 * s));
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int4 *xv = (const int4 *)(x.q[t] + xo);
+            const float2 dl = *(const float2 *)(x.d[t] + dof);
+            const float2 dx = v ? dl : make_float2(0.0f, 0.0f);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int s0 = nv_sub_dot(r.w[1 + 4 * h], r.w[2 + 4 * h], xv[2 * h]);
+                const int s1 = nv_sub_dot(r.w[3 + 4 * h], r.w[4 + 4 * h], xv[2 * h + 1]);
+                const float d = h ? dx.y : dx.x;
+                acc[t] += __builtin_fmaf(e[2 * h + 1] * d, (float)s1, e[2 * h] * d * (float)s0);
             }
         }
     }
@@ -571,7 +636,7 @@ __device__ __forceinline__ int cb_value(uint32_t nib) { return (int)(int8_t)(fp4
 
 template <int TYPE>
 __global__ void k_block_dots(const uint8_t *W, long long rb, const int8_t *q, int32_t *out, int N, int K) {
-    constexpr int G = (TYPE == TY_FP4 || TYPE == TY_Q6_K) ? 16 : 32;
+    constexpr int G = (TYPE == TY_FP4 || TYPE == TY_Q6_K || TYPE == TY_NVFP4) ? 16 : 32;
     const int ng = K / G;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long long)N * ng) return;
@@ -591,6 +656,13 @@ __global__ void k_block_dots(const uint8_t *W, long long rb, const int8_t *q, in
             const uint32_t nib = v < 16 ? (b[v] & 0xfu) : (b[v - 16] >> 4);
             s += cb_value(nib) * xg[j];
         }
+    } else if (TYPE == TY_MXFP4) {
+        const uint8_t *b = row + 17 * g + 1;
+        for (int j = 0; j < 16; ++j)
+            s += fp4_level<12>(b[j] & 0xfu) * xg[j] + fp4_level<12>(b[j] >> 4) * xg[16 + j];
+    } else if (TYPE == TY_NVFP4) {
+        const uint8_t *b = row + 36 * (g >> 2) + 4 + 8 * (g & 3);
+        for (int j = 0; j < 8; ++j) s += fp4_level<12>(b[j] & 0xfu) * xg[j] + fp4_level<12>(b[j] >> 4) * xg[8 + j];
     } else if (TYPE == TY_IQ4_XS) {
         const uint8_t *b = row + 136 * (g >> 3) + 8 + 16 * (g & 7);
         for (int i2 = 0; i2 < 16; ++i2) {
@@ -625,7 +697,8 @@ int matvec_lanes(int type, int K, long long rows) {
     switch (type) {
     case TY_Q8_0: nt = Mv<TY_Q8_0>::tasks(K); U = Mv<TY_Q8_0>::U; break;
     case TY_FP4: nt = Mv<TY_FP4>::tasks(K); U = Mv<TY_FP4>::U; break;
-    case TY_FAST: nt = Mv<TY_FAST>::tasks(K); U = Mv<TY_FAST>::U; break;
+    case TY_FAST: case TY_MXFP4: nt = Mv<TY_FAST>::tasks(K); U = Mv<TY_FAST>::U; break;
+    case TY_NVFP4: nt = Mv<TY_FP4>::tasks(K); U = Mv<TY_FP4>::U; break;
     case TY_Q4_K: nt = Mv<TY_Q4_K>::tasks(K); U = Mv<TY_Q4_K>::U; break;
     case TY_Q5_K: nt = Mv<TY_Q5_K>::tasks(K); U = Mv<TY_Q5_K>::U; break;
     case TY_IQ4_XS: nt = Mv<TY_IQ4_XS>::tasks(K); U = Mv<TY_IQ4_XS>::U; break;
@@ -689,6 +762,8 @@ hipError_t launch_matvec(int type, const MvArgs &a, hipStream_t stream) {
     case TY_Q8_0: return launch_nt<TY_Q8_0>(a, stream);
     case TY_FP4: return launch_nt<TY_FP4>(a, stream);
     case TY_FAST: return launch_nt<TY_FAST>(a, stream);
+    case TY_MXFP4: return launch_nt<TY_MXFP4>(a, stream);
+    case TY_NVFP4: return launch_nt<TY_NVFP4>(a, stream);
     case TY_Q4_K: return launch_nt<TY_Q4_K>(a, stream);
     case TY_Q5_K: return launch_nt<TY_Q5_K>(a, stream);
     case TY_IQ4_XS: return launch_nt<TY_IQ4_XS>(a, stream);
@@ -727,6 +802,8 @@ hipError_t launch_matvec_id(int type, const MvIdArgs &a, hipStream_t stream) {
     case TY_Q8_0: return launch_id_t<TY_Q8_0>(a, stream);
     case TY_FP4: return launch_id_t<TY_FP4>(a, stream);
     case TY_FAST: return launch_id_t<TY_FAST>(a, stream);
+    case TY_MXFP4: return launch_id_t<TY_MXFP4>(a, stream);
+    case TY_NVFP4: return launch_id_t<TY_NVFP4>(a, stream);
     case TY_Q4_K: return launch_id_t<TY_Q4_K>(a, stream);
     case TY_Q5_K: return launch_id_t<TY_Q5_K>(a, stream);
     case TY_IQ4_XS: return launch_id_t<TY_IQ4_XS>(a, stream);
@@ -737,13 +814,19 @@ hipError_t launch_matvec_id(int type, const MvIdArgs &a, hipStream_t stream) {
 
 hipError_t launch_block_dots(int type, const uint8_t *W, long long rb, const int8_t *q, int32_t *out, int N, int K,
                              hipStream_t stream) {
-    const int G = (type == TY_FP4 || type == TY_Q6_K) ? 16 : 32;
+    const int G = (type == TY_FP4 || type == TY_Q6_K || type == TY_NVFP4) ? 16 : 32;
     const long long n = (long long)N * (K / G);
     const dim3 grid((unsigned)((n + 255) / 256));
     switch (type) {
     case TY_Q8_0: hipLaunchKernelGGL(k_block_dots<TY_Q8_0>, grid, dim3(256), 0, stream, W, rb, q, out, N, K); break;
     case TY_FP4: hipLaunchKernelGGL(k_block_dots<TY_FP4>, grid, dim3(256), 0, stream, W, rb, q, out, N, K); break;
     case TY_FAST: hipLaunchKernelGGL(k_block_dots<TY_FAST>, grid, dim3(256), 0, stream, W, rb, q, out, N, K); break;
+    case TY_MXFP4:
+        hipLaunchKernelGGL(k_block_dots<TY_MXFP4>, grid, dim3(256), 0, stream, W, rb, q, out, N, K);
+        break;
+    case TY_NVFP4:
+        hipLaunchKernelGGL(k_block_dots<TY_NVFP4>, grid, dim3(256), 0, stream, W, rb, q, out, N, K);
+        break;
     case TY_Q4_K: hipLaunchKernelGGL(k_block_dots<TY_Q4_K>, grid, dim3(256), 0, stream, W, rb, q, out, N, K); break;
     case TY_Q5_K: hipLaunchKernelGGL(k_block_dots<TY_Q5_K>, grid, dim3(256), 0, stream, W, rb, q, out, N, K); break;
     case TY_IQ4_XS:

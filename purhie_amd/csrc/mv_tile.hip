@@ -54,7 +54,7 @@ struct Lx {
     const int8_t *x;
     const float *d;
     const int32_t *s;
-    const float *lut;  // UE4M3 byte -> half scale
+    const float *lut;  // scale byte -> its value (Tu<TYPE>::scale)
     int xt, nd, ns;
 };
 
@@ -267,6 +267,7 @@ template <>
 struct Tu<TY_FP4> {
     static constexpr int VALS = 256, BYTES = 144, NDW = 36, ACT = 32, SUMS = 0, LEAD = 0;
     static constexpr bool LUT = true;
+    __device__ static float scale(uint32_t e) { return ue4m3_half(e); }
     __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read16(p, w, aux); }
     template <int NT>
     __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT]) {
@@ -337,6 +338,7 @@ template <>
 struct Tu<TY_FAST> {
     static constexpr int VALS = 256, BYTES = 136, NDW = 34, ACT = 32, SUMS = 0, LEAD = 8;
     static constexpr bool LUT = true;
+    __device__ static float scale(uint32_t e) { return ue4m3_half(e); }
     __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read8(p, w, aux); }
     template <int NT>
     __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT]) {
@@ -358,6 +360,75 @@ struct Tu<TY_FAST> {
                 const int4 *xv = (const int4 *)(x.x + t * x.xt + 32 * j);
                 const int s = dot4x(lo, xv[0]) + dot4x(hi, xv[1]);
                 acc[t] = __builtin_fmaf(e * x.d[t * x.nd + j], (float)s, acc[t]);
+            }
+        }
+    }
+};
+
+// MXFP4 (type 39): eight 17-byte blocks (an E8M0 scale byte, then FAST's 16 value bytes), E2M1 levels; per
+// block (e dx) (s0 + s1) (reference src/matvec_q.hip:1461-1472 PFMXFP4, 1492-1502).
+template <>
+struct Tu<TY_MXFP4> {
+    static constexpr int VALS = 256, BYTES = 136, NDW = 34, ACT = 32, SUMS = 0, LEAD = 8;
+    static constexpr bool LUT = true;
+    __device__ static float scale(uint32_t e) { return e8m0_half(e); }
+    __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read8(p, w, aux); }
+    template <int NT>
+    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT]) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int off = 17 * j;
+            int lo[4], hi[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t q = dwb(w, off + 1 + 4 * k);
+                lo[k] = fp4x4_lo<12>(q);
+                hi[k] = fp4x4_hi<12>(q);
+            }
+            const float e = x.lut[byteb(w, off)];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const int4 *xv = (const int4 *)(x.x + t * x.xt + 32 * j);
+                const int s = dot4x(lo, xv[0]) + dot4x(hi, xv[1]);
+                acc[t] = __builtin_fmaf(e * x.d[t * x.nd + j], (float)s, acc[t]);
+            }
+        }
+    }
+};
+
+// NVFP4 (type 40): four 36-byte blocks of 64 values (four scale bytes, then four 8-byte sub-blocks of 16: value
+// i in the low nibble of byte i % 8, i >= 8 in the high nibble), E2M1 levels. Activation block 2 m + h takes
+// sub-blocks 2 h (values 0..15) and 2 h + 1 (16..31) of block m: (dx e0) s0 + (dx e1) s1 (reference
+// src/matvec_q.hip:1357-1372 P4NVFP4::block).
+template <>
+struct Tu<TY_NVFP4> {
+    static constexpr int VALS = 256, BYTES = 144, NDW = 36, ACT = 32, SUMS = 0, LEAD = 0;
+    static constexpr bool LUT = true;
+    __device__ static float scale(uint32_t e) { return nv_scale(e); }
+    __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read16(p, w, aux); }
+    template <int NT>
+    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT]) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t a0 = w[9 * m + 1 + 4 * h], a1 = w[9 * m + 2 + 4 * h];
+                const uint32_t b0 = w[9 * m + 3 + 4 * h], b1 = w[9 * m + 4 + 4 * h];
+                const int la[4] = {fp4x4_lo<12>(a0), fp4x4_lo<12>(a1), fp4x4_hi<12>(a0), fp4x4_hi<12>(a1)};
+                const int lb[4] = {fp4x4_lo<12>(b0), fp4x4_lo<12>(b1), fp4x4_hi<12>(b0), fp4x4_hi<12>(b1)};
+                const float e0 = x.lut[byteb(w, 36 * m + 2 * h)], e1 = x.lut[byteb(w, 36 * m + 2 * h + 1)];
+                const int b = 2 * m + h;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const int4 *xv = (const int4 *)(x.x + t * x.xt + 32 * b);
+                    const int s0 = dot4x(la, xv[0]), s1 = dot4x(lb, xv[1]);
+                    const float dx = x.d[t * x.nd + b];
+                    acc[t] += __builtin_fmaf(e1 * dx, (float)s1, e0 * dx * (float)s0);
+                }
             }
         }
     }
@@ -462,8 +533,8 @@ struct Stager {
         for (int e = tid + TL_DN * THR; e < ndt; e += THR) ld[e] = d[e];
         if (Tu<TYPE>::SUMS)
             for (int e = tid + TL_SN * THR; e < nst; e += THR) put_s(L, smem, e, load_s(bs, e));
-        if (Tu<TYPE>::LUT)
-            for (int e = tid; e < 256; e += THR) ((float *)(smem + L.off_lut))[e] = ue4m3_half((uint32_t)e);
+        if constexpr (Tu<TYPE>::LUT)
+            for (int e = tid; e < 256; e += THR) ((float *)(smem + L.off_lut))[e] = Tu<TYPE>::scale((uint32_t)e);
     }
 };
 
@@ -679,6 +750,8 @@ hipError_t launch_matvec_tile(int type, const MvArgs &a, hipStream_t stream) {
     case TY_Q8_0: return tile_dense_t<TY_Q8_0>(a, stream);
     case TY_FP4: return tile_dense_t<TY_FP4>(a, stream);
     case TY_FAST: return tile_dense_t<TY_FAST>(a, stream);
+    case TY_MXFP4: return tile_dense_t<TY_MXFP4>(a, stream);
+    case TY_NVFP4: return tile_dense_t<TY_NVFP4>(a, stream);
     case TY_Q4_K: return tile_dense_t<TY_Q4_K>(a, stream);
     case TY_Q5_K: return tile_dense_t<TY_Q5_K>(a, stream);
     case TY_IQ4_XS: return tile_dense_t<TY_IQ4_XS>(a, stream);
@@ -718,6 +791,8 @@ hipError_t launch_matvec_id_tile(int type, const MvIdArgs &a, hipStream_t stream
     case TY_Q8_0: return tile_id<TY_Q8_0>(a, stream);
     case TY_FP4: return tile_id<TY_FP4>(a, stream);
     case TY_FAST: return tile_id<TY_FAST>(a, stream);
+    case TY_MXFP4: return tile_id<TY_MXFP4>(a, stream);
+    case TY_NVFP4: return tile_id<TY_NVFP4>(a, stream);
     case TY_Q4_K: return tile_id<TY_Q4_K>(a, stream);
     case TY_Q5_K: return tile_id<TY_Q5_K>(a, stream);
     case TY_IQ4_XS: return tile_id<TY_IQ4_XS>(a, stream);

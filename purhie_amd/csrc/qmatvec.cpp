@@ -19,7 +19,7 @@ namespace {
 
 bool is_int8_type(int t) {
     return t == TY_Q8_0 || t == TY_Q4_K || t == TY_Q5_K || t == TY_Q6_K || t == TY_IQ4_XS || t == TY_FP4 ||
-           t == TY_FAST;
+           t == TY_FAST || t == TY_MXFP4 || t == TY_NVFP4;
 }
 bool reads_q8k(int t) { return t == TY_Q4_K || t == TY_Q5_K || t == TY_Q6_K || t == TY_IQ4_XS; }
 int act_blk(int t) { return reads_q8k(t) ? 256 : 32; }
@@ -27,8 +27,8 @@ int act_blk(int t) { return reads_q8k(t) ? 256 : 32; }
 // required K multiple of each int8 kernel (src/qmatvec.cpp:423-429)
 int k_multiple(int t) {
     switch (t) {
-    case TY_Q8_0: case TY_FP4: return 64;
-    case TY_FAST: return 128;
+    case TY_Q8_0: case TY_FP4: case TY_NVFP4: return 64;
+    case TY_FAST: case TY_MXFP4: return 128;
     case TY_Q4_K: case TY_Q5_K: case TY_Q6_K: case TY_IQ4_XS: return 256;
     }
     return 0;

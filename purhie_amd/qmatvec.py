@@ -14,11 +14,13 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libpurhie_qmv.so")
 
 QT_F32, QT_F16, QT_Q8_0, QT_Q4_K, QT_Q5_K, QT_Q6_K, QT_IQ4_XS, QT_BF16 = 0, 1, 8, 12, 13, 14, 23, 30
+QT_MXFP4, QT_NVFP4 = 39, 40
 QT_Q4_0_ROCMFP4, QT_Q4_0_ROCMFP4_FAST = 100, 101
 KQUANTS = (QT_Q4_K, QT_Q5_K, QT_Q6_K, QT_IQ4_XS)
 NAMES = {QT_Q8_0: "q8_0", QT_Q4_K: "q4_K", QT_Q5_K: "q5_K", QT_Q6_K: "q6_K", QT_IQ4_XS: "iq4_xs", QT_Q4_0_ROCMFP4: "q4_0_rocmfp4",
-         QT_Q4_0_ROCMFP4_FAST: "q4_0_rocmfp4_fast"}
-GROUP = {QT_Q8_0: 32, QT_Q4_0_ROCMFP4: 16, QT_Q4_0_ROCMFP4_FAST: 32, QT_Q4_K: 32, QT_Q5_K: 32, QT_Q6_K: 16, QT_IQ4_XS: 32}
+         QT_Q4_0_ROCMFP4_FAST: "q4_0_rocmfp4_fast", QT_MXFP4: "mxfp4", QT_NVFP4: "nvfp4"}
+GROUP = {QT_Q8_0: 32, QT_Q4_0_ROCMFP4: 16, QT_Q4_0_ROCMFP4_FAST: 32, QT_Q4_K: 32, QT_Q5_K: 32, QT_Q6_K: 16, QT_IQ4_XS: 32,
+         QT_MXFP4: 32, QT_NVFP4: 16}
 
 
 class HipError(RuntimeError):

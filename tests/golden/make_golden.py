@@ -22,7 +22,7 @@ sys.path.insert(0, ROOT)
 from oracle import oracle as O  # noqa: E402
 from purhie_amd import synth  # noqa: E402
 
-TYPES = (8, 12, 13, 14, 23, 100, 101)
+TYPES = (8, 12, 13, 14, 23, 39, 40, 100, 101)
 
 
 def enc_rows(seed, K):

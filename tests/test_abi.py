@@ -60,7 +60,7 @@ def test_row_sizes_and_traits_match_reference_metadata():
              (8, 100): 0, (12, 300): 0}
     for (t, k), want in cases.items():
         assert lib.qt_row_size(t, k) == want, (t, k)
-    assert [lib.qt_vec_dot_q8k(t) for t in (8, 12, 13, 14, 23, 100, 101)] == [0, 1, 1, 1, 1, 0, 0]
+    assert [lib.qt_vec_dot_q8k(t) for t in (8, 12, 13, 14, 23, 39, 40, 100, 101)] == [0, 1, 1, 1, 1, 0, 0, 0, 0]
 
 
 def test_q8_buffer_layout():

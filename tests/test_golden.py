@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-TYPES = (8, 12, 13, 14, 23, 100, 101)
+TYPES = (8, 12, 13, 14, 23, 39, 40, 100, 101)
 TOL = 1e-5
 
 

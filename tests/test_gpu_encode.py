@@ -10,7 +10,7 @@ import pytest
 from purhie_amd import synth
 
 pytestmark = pytest.mark.gpu
-TYPES = (8, 12, 13, 14, 23, 100, 101)
+TYPES = (8, 12, 13, 14, 23, 39, 40, 100, 101)
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
@@ -60,7 +60,23 @@ def test_encode_device_matches_oracle(Q, oracle, t):
     assert np.array_equal(y.cpu().numpy().reshape(N, -1), oracle.quantize(t, x))
 
 
-@pytest.mark.parametrize("src_t,dst_t", [(1, 100), (30, 12), (8, 101), (100, 8), (12, 14), (14, 13)])
+def test_encode_mxfp4_exponent_rounding_points(Q, oracle):
+    """blocks whose maximum lies at or a few units below a power of two, where log2f may round up to the integer
+    and the E8M0 exponent with it: the device encoder equals the oracle (itself checked against the compiled
+    reference at the same points)"""
+    rows = []
+    for k in range(-30, 20):
+        for ulps in range(6):
+            amax = (np.float32(2.0 ** k).view(np.uint32) - np.uint32(ulps)).view(np.float32)
+            x = np.clip(synth.gaussian(1000 + 8 * k + ulps, 32, 0, 0.3), -0.9, 0.9).astype(np.float32) * amax
+            x[7] = amax
+            rows.append(x)
+    x = np.stack(rows).astype(np.float32)
+    assert np.array_equal(Q.encode(39, x, 32), oracle.quantize(39, x))
+
+
+@pytest.mark.parametrize("src_t,dst_t", [(1, 100), (30, 12), (8, 101), (100, 8), (12, 14), (14, 13), (1, 40),
+                                         (40, 39)])
 def test_reencode_from_other_type(Q, oracle, src_t, dst_t):
     K = 512
     x = synth.gaussian(720 + src_t, 8 * K, 0, 0.02).reshape(8, K)

@@ -9,7 +9,7 @@ from purhie_amd import synth
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
-GEMM_TYPES = (100, 101, 8, 12, 13, 14, 23)
+GEMM_TYPES = (100, 101, 8, 12, 13, 14, 23, 39, 40)
 
 
 @pytest.fixture(scope="module")
@@ -88,7 +88,7 @@ def test_gemm_ldy_and_split_invariance(Q, oracle, t):
 
 @pytest.mark.parametrize("t,N,K", [(100, 768, 2048), (100, 2048, 768), (8, 512, 1024), (101, 256, 1024),
                                    (12, 768, 2048), (13, 512, 1024), (14, 2048, 768), (23, 512, 1024),
-                                   (12, 200, 512)])
+                                   (39, 256, 1024), (40, 768, 2048), (12, 200, 512)])
 def test_moe_tiled_gemm(Q, oracle, t, N, K):
     """expert tiles from the grouping (config 4 shapes, and K-quant experts): entry i of tile k multiplies input
     row in_rows[i] by expert tile_e[k] into output row out_rows[i]"""

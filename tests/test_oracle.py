@@ -13,7 +13,7 @@ import pytest
 
 from purhie_amd import synth
 
-TYPES_ENC = (8, 100, 101, 12, 13, 14, 23)  # Q8_0, ROCmFP4, FAST, Q4_K, Q5_K, Q6_K, IQ4_XS
+TYPES_ENC = (8, 100, 101, 12, 13, 14, 23, 39, 40)  # Q8_0, ROCmFP4, FAST, Q4_K, Q5_K, Q6_K, IQ4_XS, MXFP4, NVFP4
 
 
 def families():
@@ -53,7 +53,7 @@ def test_encoders_match_reference(ref, t):
         assert np.array_equal(a, b), f"type {t} family {name}: {int((a != b).sum())} bytes differ"
 
 
-@pytest.mark.parametrize("t", (8, 100, 101))
+@pytest.mark.parametrize("t", (8, 100, 101, 39, 40))
 def test_encoders_nan_inf_match_reference(ref, t):
     # the reference skips the K-quants here: ggml's own K-quant encoders are undefined on NaN
     x = synth.gaussian(17, 8 * 256).reshape(8, 256)
@@ -125,6 +125,30 @@ def test_ue4m3_decoders(oracle):
         if 0x08 <= e <= 0x7E:
             assert w == v / 2
     assert L.orc_ue4m3_fp4common(0x7F) == 120.0 and L.orc_ue4m3_fp4common(0xFF) == 120.0
+    # MXFP4's E8M0 byte at half scale: 2^(e - 128) for every byte, the two subnormals included
+    for e in range(256):
+        assert L.orc_e8m0_half(e) == 2.0 ** (e - 128)
+
+
+def test_mxfp4_exponent_at_rounding_points(ref):
+    """MXFP4's block exponent floor(log2f(amax)) where log2f rounds up to the next integer (amax one or two
+    units below a power of two): the oracle equals the compiled reference there, and at 2^k exactly"""
+    rows = []
+    for k in (-20, -9, -6, -3, -1, 0, 1, 3, 8):
+        for ulps in (0, 1, 2, 3):
+            top = np.float32(2.0 ** k)
+            amax = (top.view(np.uint32) - np.uint32(ulps)).view(np.float32)
+            x = synth.gaussian(900 + k * 4 + ulps, 32, 0, 0.1) * amax
+            x = np.clip(x, -amax * np.float32(0.9), amax * np.float32(0.9))
+            x[5] = -amax
+            rows.append(x.astype(np.float32))
+    x = np.stack(rows)
+    assert np.array_equal(ref.quantize(39, x), ref.ref_quantize(39, x))
+    e = ref.quantize(39, x)[:, 0].astype(int).reshape(9, 4)
+    k = np.array([-20, -9, -6, -3, -1, 0, 1, 3, 8])[:, None]
+    assert np.all(e[:, 0] == k[:, 0] + 125)              # amax = 2^k: exponent k
+    below = e[:, 1:] - (k + 124)                          # amax below 2^k: k - 1, or k where log2f rounds up
+    assert set(below.reshape(-1).tolist()) == {0, 1} and below[-1, 0] == 1 and below[4, 0] == 0
 
 
 def test_gemm_act_fp4_closed_forms(oracle):
@@ -277,6 +301,7 @@ def test_block_dots_brute_force(oracle, t):
     kq = t in (12, 13, 14, 23)
     a = oracle.quantize_act(x, kq)
     dots = oracle.block_dots(t, W, N, K, a["q"])
+    e2m1 = [0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12]
     G = oracle.GROUP[t]
     # independent restatement of each raw level from the byte layout (quant_types.cpp's decoders)
     lv = np.zeros((N, K), np.int64)
@@ -291,6 +316,15 @@ def test_block_dots_brute_force(oracle, t):
                 j = v % 32
                 nib = (b[j] & 15) if j < 16 else (b[j - 16] >> 4)
                 lv[n, v] = [0, 1, 2, 3, 4, 6, 8, 10, 0, -1, -2, -3, -4, -6, -8, -10][nib]
+            elif t == 39:  # MXFP4: the E8M0 byte, then FAST's value bytes
+                b = row[17 * (v // 32) + 1:]
+                j = v % 32
+                lv[n, v] = e2m1[(b[j] & 15) if j < 16 else (b[j - 16] >> 4)]
+            elif t == 40:  # NVFP4: 4 scale bytes, sub-block s in bytes 4 + 8 s, value j in byte j % 8, j >= 8 high
+                b = row[36 * (v // 64):]
+                s, j = (v % 64) // 16, v % 16
+                byte = b[4 + 8 * s + j % 8]
+                lv[n, v] = e2m1[(byte >> 4) if j >= 8 else (byte & 15)]
             elif t == 12:
                 b = row[144 * (v // 256):]
                 w = v % 256
