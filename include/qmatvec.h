@@ -32,14 +32,22 @@ void qmatvec_free(void);
 int qmatvec_set_out_scale(const void *owner, const void *W, size_t bytes, const float *s, int n);
 void qmatvec_drop_out_scales(const void *owner);
 
-/* replaces src/qmatvec.h:29: 1 if a float-activation matvec exists for the type (none here: the
- * path is the int8 one below) */
+/* replaces src/qmatvec.h:29: 1 if a float-activation matvec exists for the type: F32, F16 and BF16 (the
+ * quantized types' path is the int8 one below) */
 int qmatvec_supported(int type);
 
-/* The float-activation, 16-bit-copy, low-rank, split-Q8_0 and float MoE entries of the reference
- * (src/qmatvec.h:33-75,145-147,179-199) are outside this path. They are exported so that the engine links
- * unchanged; their *_supported queries return 0 and the launches return hipErrorInvalidDeviceFunction,
- * as the reference's do for a kernel its code object lacks. */
+/* Float activations over F32 / F16 / BF16 weights (replace src/qmatvec.h:33-75). F16 / BF16 weights multiply the
+ * activations rounded to the weight type (nearest even), so every product is exact; F32 and _bf16f multiply
+ * the fp32 activations as they are. Same arguments, checks and error codes as the reference's.
+ *   qmatvec_launch_bf16f    BF16 weights (row_bytes = 2 K), fp32 activations not rounded, T rows
+ *   qmatvec_launch          one row of x; type F32 / F16 / BF16, row_bytes = qt_row_size(type, K)
+ *   qmatvec_launch_batch    T rows; F16 / BF16 batches qmatvec_half_supported takes go to the MFMA GEMM (the
+ *                           16-bit copy of x in a stream-ordered pool buffer), the rest to the decode kernel
+ *   qmatvec_launch_batch_h  the same with the caller's scratch xh (16-byte aligned, xh_bytes >= 2 T K) for the copy
+ *   qmatvec_half_supported  F16 / BF16, GEMMs on, T >= 32 (any T in prefill mode), N >= 64, K % 8 == 0,
+ *                           row_bytes >= 2 K and a multiple of 16, W 16-byte aligned
+ *   qmatvec_round_half      x -> xh rounded to the type (n % 8 == 0, both 16-byte aligned)
+ *   qmatvec_launch_batch_hx the GEMM on xh (T rows of K values) */
 hipError_t qmatvec_launch_bf16f(const void *W, size_t row_bytes, const float *x, float *y, int N, int K, int T,
                                 hipStream_t stream);
 hipError_t qmatvec_launch(int type, const void *W, size_t row_bytes, const float *x, float *y, int N, int K,
@@ -52,6 +60,11 @@ int qmatvec_half_supported(int type, const void *W, size_t row_bytes, int N, int
 hipError_t qmatvec_round_half(int type, const float *x, uint16_t *xh, long long n, hipStream_t stream);
 hipError_t qmatvec_launch_batch_hx(int type, const void *W, size_t row_bytes, const uint16_t *xh, float *y, int N,
                                    int K, int T, hipStream_t stream);
+
+/* The low-rank, split-Q8_0 and float MoE entries of the reference (src/qmatvec.h:68-75,145-147,179-199) are
+ * outside this path. They are exported so that the engine links unchanged; their *_supported queries return 0
+ * and the launches return hipErrorInvalidDeviceFunction, as the reference's do for a kernel its code object
+ * lacks. */
 int qmatvec_q8_0s_source_supported(int type, int K);
 hipError_t qmatvec_quantize_rows_q8_0(int type, const void *W, size_t row_bytes, int N, int K, int8_t *qs, uint16_t *d,
                                       hipStream_t stream);

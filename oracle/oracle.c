@@ -922,6 +922,46 @@ int orc_quantize(int t, const float *x, void *dst, int64_t nrows, int64_t k, int
     return 0;
 }
 
+/* ================================================================ float activations */
+
+/* src/matvec_q.hip:713-721 (f16_round), 805-809 (bf16_round) */
+float orc_act_round(int t, int round, float x) {
+    pthread_once(&g_half_once, half_init);
+    if (!round || t == ORC_F32) return x;
+    if (t == ORC_F16) return orc_f16_to_f32(orc_f32_to_f16(x));
+    const uint32_t u = fbits(x);
+    return bitsf(((u + 0x7fffu + ((u >> 16) & 1u)) >> 16) << 16);
+}
+
+void orc_act_round_n(int t, int round, const float *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_act_round(t, round, x[i]);
+}
+
+int orc_matvec_float(int t, int round, const void *W, size_t rb, int N, int K, int T, const float *x, double *ref,
+                     double *mag) {
+    if ((t != ORC_F32 && t != ORC_F16 && t != ORC_BF16) || rb < orc_row_size(t, K)) return -1;
+    pthread_once(&g_half_once, half_init);
+    float *w = (float *)malloc((size_t)K * 4), *xa = (float *)malloc((size_t)K * 4);
+    if (!w || !xa) { free(w); free(xa); return -1; }
+    for (int tt = 0; tt < T; ++tt) {
+        for (int k = 0; k < K; ++k) xa[k] = orc_act_round(t, round, x[(size_t)tt * K + k]);
+        for (int n = 0; n < N; ++n) {
+            orc_to_float(t, (const uint8_t *)W + (size_t)n * rb, w, K);
+            double s = 0.0, m = 0.0;
+            for (int k = 0; k < K; ++k) {
+                const double p = (double)w[k] * (double)xa[k];
+                s += p;
+                m += fabs(p);
+            }
+            ref[(size_t)tt * N + n] = s;
+            mag[(size_t)tt * N + n] = m;
+        }
+    }
+    free(w);
+    free(xa);
+    return 0;
+}
+
 /* ================================================================ activation quantizers */
 
 /* Q8_0 activations (src/q8_device.h:54-76, src/expert_cpu.cpp:39-48): per 32 values am = max |x|

@@ -51,6 +51,16 @@ int orc_type_size(int type);            /* bytes per block */
 size_t orc_row_size(int type, int64_t k);
 int orc_to_float(int type, const void *src, float *dst, int64_t n);
 
+/* ---- float activations over F32 / F16 / BF16 weights (src/matvec_q.hip:700-1075, 3391-3547)
+ * orc_act_round: the activation as the kernels multiply it: rounded to the weight type when round is set
+ * (F16: nearest even; BF16: (u + 0x7fff + lsb) >> 16 on the bits, no NaN case), else as it is (F32 always).
+ * orc_matvec_float: ref[n] = sum_k w[n][k] act(x[k]) and mag[n] = sum_k |w act(x)| in double (the products of
+ * 16-bit weights and rounded activations are exact); T tokens of K values in x, outputs [T][N]. */
+float orc_act_round(int type, int round, float x);
+void orc_act_round_n(int type, int round, const float *x, float *y, int64_t n);
+int orc_matvec_float(int type, int round, const void *W, size_t rb, int N, int K, int T, const float *x, double *ref,
+                     double *mag);
+
 /* ---- encoders: nrows rows of k floats -> rows of orc_row_size bytes; n_threads <= 0: all cores */
 int orc_quantize(int type, const float *x, void *dst, int64_t nrows, int64_t k, int n_threads);
 

@@ -44,6 +44,9 @@ def lib():
         L.orc_f32_to_f16.argtypes = [C.c_float]
         L.orc_f16_to_f32.restype = C.c_float
         L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_act_round_n.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_int64]
+        L.orc_matvec_float.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                       C.c_void_p, C.c_void_p]
         L.orc_ue4m3_half.restype = C.c_float
         L.orc_ue4m3_half.argtypes = [C.c_uint8]
         L.orc_ue4m3_fp4common.restype = C.c_float
@@ -147,6 +150,25 @@ def matvec(t, W, N, K, act, want_ref=True, n_threads=0):
     assert lib().orc_matvec(t, _ptr(W), row_size(t, K), N, K, _ptr(act["q"]), _ptr(act["d"]),
                             _ptr(bs), _ptr(y), _ptr(ref), _ptr(mag), n_threads) == 0
     return y, ref, mag
+
+
+def act_round(t, x, round=True):
+    """activations as the float kernels multiply them (rounded to the F16 / BF16 weight type)"""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().orc_act_round_n(t, int(round), _ptr(x), _ptr(y), x.size)
+    return y
+
+
+def matvec_float(t, W, N, K, x, round=True):
+    """float activations x [T][K] over F32 / F16 / BF16 rows W: (ref, mag) [T][N] in double"""
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, K)
+    T = x.shape[0]
+    ref = np.zeros((T, N), np.float64)
+    mag = np.zeros((T, N), np.float64)
+    assert lib().orc_matvec_float(t, int(round), _ptr(W), W.size // N, N, K, T, _ptr(x), _ptr(ref), _ptr(mag)) == 0
+    return ref, mag
 
 
 def moe_router(logits, n_used):

@@ -104,6 +104,15 @@ int gemm_rows_per_wg(int type);  // weight rows per GEMM workgroup (token tiles:
 hipError_t launch_act_split(int type, const int8_t *q, const float *d, int T, int K, int rows, int8_t *xq,
                             _Float16 *xs, float *ts, hipStream_t stream);
 hipError_t launch_gemm_split(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);
+
+// Float activations over F32 / F16 / BF16 weights (type ids 0, 1, 30): the decode matvec for T tokens (round:
+// the activations rounded to the 16-bit weight type), the F16 / BF16 MFMA GEMM on activations rounded to 16 bits
+// (xh), and that rounding (n % 8 == 0)
+hipError_t launch_mv_float(int type, bool round, const uint8_t *W, long long rb, const float *x, float *y, int N, int K,
+                           int T, hipStream_t stream);
+hipError_t launch_gemm_float(int type, const uint8_t *W, long long rb, const uint16_t *xh, float *y, int N, int K,
+                             int T, hipStream_t stream);
+hipError_t launch_round_half(int type, const float *x, uint16_t *xh, long long n, hipStream_t stream);
 // the K-quant GEMM (Q4_K, Q6_K): pre-pass of the Q8_K activation (`rows` rows, T real) and the kernel
 bool gemm_kquant(int type);
 constexpr int GEMM_KQ_ROWS = 128;  // weight rows per K-quant GEMM workgroup

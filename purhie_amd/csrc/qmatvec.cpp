@@ -211,31 +211,83 @@ void qmatvec_drop_out_scales(const void *owner) {
     g_n_scales.store((int)g_scales.size());
 }
 
-int qmatvec_supported(int type) {
-    (void)type;
-    return 0;
+// ---- float activations over F32 / F16 / BF16 weights (src/qmatvec.cpp:255-366). The quantized types have no
+// float-activation kernel here (their path is the int8 one): qmatvec_supported answers 0 for them and their
+// float launches return hipErrorInvalidDeviceFunction, the reference's answer for a missing kernel.
+namespace {
+bool float_type(int t) { return t == QT_F32 || t == QT_F16 || t == QT_BF16; }
+bool half_type(int t) { return t == QT_F16 || t == QT_BF16; }
+bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+// the decode kernel over T tokens, after the reference's argument checks
+hipError_t float_rows(int type, bool round, const void *W, size_t row_bytes, const float *x, float *y, int N, int K,
+                      int T, hipStream_t stream) {
+    if (!float_type(type)) return hipErrorInvalidDeviceFunction;
+    if (!W || !x || !y || N < 0 || K <= 0 || T < 1 || row_bytes != qt_row_size(type, K)) return hipErrorInvalidValue;
+    if (N == 0) return hipSuccess;
+    return launch_mv_float(type, round, (const uint8_t *)W, (long long)row_bytes, x, y, N, K, T, stream);
+}
+}  // namespace
+
+int qmatvec_supported(int type) { return float_type(type) ? 1 : 0; }
+
+hipError_t qmatvec_launch_bf16f(const void *W, size_t row_bytes, const float *x, float *y, int N, int K, int T,
+                                hipStream_t stream) {
+    if (!W || !x || !y || T < 1 || row_bytes != (size_t)K * 2) return hipErrorInvalidValue;
+    return float_rows(QT_BF16, false, W, row_bytes, x, y, N, K, T, stream);
 }
 
-// ---- the float-activation entries: outside this path (the reference's answer for a missing kernel)
-hipError_t qmatvec_launch_bf16f(const void *, size_t, const float *, float *, int, int, int, hipStream_t) {
-    return hipErrorInvalidDeviceFunction;
+hipError_t qmatvec_launch(int type, const void *W, size_t row_bytes, const float *x, float *y, int N, int K,
+                          hipStream_t stream) {
+    return float_rows(type, true, W, row_bytes, x, y, N, K, 1, stream);
 }
-hipError_t qmatvec_launch(int, const void *, size_t, const float *, float *, int, int, hipStream_t) {
-    return hipErrorInvalidDeviceFunction;
+
+int qmatvec_half_supported(int type, const void *W, size_t row_bytes, int N, int K, int T) {
+    return half_type(type) && mfma_on() && (g_prefill || T >= gemm_min_t()) && T >= 1 && N >= 64 && K > 0 &&
+           K % 8 == 0 && row_bytes >= (size_t)K * 2 && row_bytes % 16 == 0 && al16(W);
 }
-hipError_t qmatvec_launch_batch(int, const void *, size_t, const float *, float *, int, int, int, hipStream_t) {
-    return hipErrorInvalidDeviceFunction;
+
+hipError_t qmatvec_round_half(int type, const float *x, uint16_t *xh, long long n, hipStream_t stream) {
+    if (!half_type(type)) return hipErrorInvalidDeviceFunction;
+    if (!x || !xh || n < 0 || n % 8 != 0 || !al16(x) || !al16(xh)) return hipErrorInvalidValue;
+    return launch_round_half(type, x, xh, n, stream);
 }
-hipError_t qmatvec_launch_batch_h(int, const void *, size_t, const float *, uint16_t *, size_t, float *, int, int, int,
-                                  hipStream_t) {
-    return hipErrorInvalidDeviceFunction;
+
+hipError_t qmatvec_launch_batch_hx(int type, const void *W, size_t row_bytes, const uint16_t *xh, float *y, int N,
+                                   int K, int T, hipStream_t stream) {
+    if (!qmatvec_half_supported(type, W, row_bytes, N, K, T)) return hipErrorInvalidDeviceFunction;
+    if (!xh || !y || !al16(xh)) return hipErrorInvalidValue;
+    return launch_gemm_float(type, (const uint8_t *)W, (long long)row_bytes, xh, y, N, K, T, stream);
 }
-int qmatvec_half_supported(int, const void *, size_t, int, int, int) { return 0; }
-hipError_t qmatvec_round_half(int, const float *, uint16_t *, long long, hipStream_t) {
-    return hipErrorInvalidDeviceFunction;
+
+hipError_t qmatvec_launch_batch(int type, const void *W, size_t row_bytes, const float *x, float *y, int N, int K,
+                                int T, hipStream_t stream) {
+    return qmatvec_launch_batch_h(type, W, row_bytes, x, nullptr, 0, y, N, K, T, stream);
 }
-hipError_t qmatvec_launch_batch_hx(int, const void *, size_t, const uint16_t *, float *, int, int, int, hipStream_t) {
-    return hipErrorInvalidDeviceFunction;
+
+// F16 / BF16 batches the GEMM takes: x rounded to 16 bits first, into the caller's scratch buffer xh when it holds
+// T K values, else into one from the stream-ordered pool (the GEMM reads 16-bit activations: half the bytes of
+// rounding fp32 ones while staging, measured 2x faster); every other batch through the decode kernel, token by
+// token in its order
+hipError_t qmatvec_launch_batch_h(int type, const void *W, size_t row_bytes, const float *x, uint16_t *xh,
+                                  size_t xh_bytes, float *y, int N, int K, int T, hipStream_t stream) {
+    if (qmatvec_half_supported(type, W, row_bytes, N, K, T) && x && y && al16(x) && (!xh || al16(xh))) {
+        const size_t need = (size_t)T * K * 2;
+        void *own = nullptr;
+        if (!xh || xh_bytes < need) {
+            const hipError_t e = hipMallocAsync(&own, need, stream);
+            if (e != hipSuccess) return e;
+            xh = (uint16_t *)own;
+        }
+        hipError_t e = qmatvec_round_half(type, x, xh, (long long)T * K, stream);
+        if (e == hipSuccess) e = qmatvec_launch_batch_hx(type, W, row_bytes, xh, y, N, K, T, stream);
+        if (own) {
+            const hipError_t f = hipFreeAsync(own, stream);
+            if (e == hipSuccess) e = f;
+        }
+        return e;
+    }
+    return float_rows(type, true, W, row_bytes, x, y, N, K, T, stream);
 }
 int qmatvec_q8_0s_source_supported(int, int) { return 0; }
 hipError_t qmatvec_quantize_rows_q8_0(int, const void *, size_t, int, int, int8_t *, uint16_t *, hipStream_t) {

@@ -82,6 +82,15 @@ def lib():
             "qmatvec_set_prefill": (None, [i32]),
             "qmatvec_prefill": (i32, []),
             "qmatvec_set_out_scale": (i32, [vp, vp, sz, vp, i32]),
+            "qmatvec_supported": (i32, [i32]),
+            "qmatvec_launch": (i32, [i32, vp, sz, vp, vp, i32, i32, vp]),
+            "qmatvec_launch_bf16f": (i32, [vp, sz, vp, vp, i32, i32, i32, vp]),
+            "qmatvec_launch_batch": (i32, [i32, vp, sz, vp, vp, i32, i32, i32, vp]),
+            "qmatvec_launch_batch_h": (i32, [i32, vp, sz, vp, vp, sz, vp, i32, i32, i32, vp]),
+            "qmatvec_half_supported": (i32, [i32, vp, sz, i32, i32, i32]),
+            "qmatvec_round_half": (i32, [i32, vp, vp, ll, vp]),
+            "qmatvec_launch_batch_hx": (i32, [i32, vp, sz, vp, vp, i32, i32, i32, vp]),
+            "qmatvec_set_prefill_fp32": (None, [i32]),
             "qmatvec_drop_out_scales": (None, [vp]),
             "qt_get_traits": (C.POINTER(qt_traits), [i32]),
             "qt_row_size": (sz, [i32, i64]),

@@ -470,3 +470,52 @@ def test_moe_combine_variants_step_by_step(oracle):
                                      (w, None, None, es), (None, sh, None, None)):
         got = oracle.moe_combine(down, wts, shared, gate, ids if scale is not None else None, scale)
         assert np.array_equal(got.view(np.uint32), want(wts, shared, gate, scale).view(np.uint32))
+
+
+def test_act_round_closed_form(oracle):
+    """the float kernels' activation rounding (src/matvec_q.hip:713-721, 805-809): BF16 is round to nearest even
+    on a grid of 2^(e - 8) (8 significant bits; 2^-133 below the normal range), checked here in float64 with
+    numpy's half-to-even rounding, overflow to infinity included; F16 is IEEE round to nearest even (numpy's
+    float16 cast); F32, and BF16 without rounding, keep x"""
+    u = synth.splitmix64(77, 1 << 18) & np.uint64(0xFFFFFFFF)
+    x = u.astype(np.uint32).view(np.float32)
+    x = x[np.isfinite(x)]
+    # exact bf16 midpoints and their neighbours, and values near the largest bf16
+    mids = ((synth.splitmix64(78, 4096) & np.uint64(0x7F7F0000)).astype(np.uint32) | np.uint32(0x8000))
+    x = np.concatenate([x, mids.view(np.float32), (mids + np.uint32(1)).view(np.float32),
+                        (mids - np.uint32(1)).view(np.float32), np.float32([3.3961e38, -3.3961e38, 3.39e38])])
+    got = oracle.act_round(30, x)
+    m, e = np.frexp(x.astype(np.float64))
+    q = np.ldexp(1.0, np.maximum(e, -125) - 8)
+    with np.errstate(over="ignore"):
+        want = (np.round(x / q) * q).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    with np.errstate(over="ignore"):
+        h = x.astype(np.float16).astype(np.float32)
+    assert np.array_equal(oracle.act_round(1, x).view(np.uint32), h.view(np.uint32))
+    for t, r in ((0, True), (30, False), (1, False)):
+        assert np.array_equal(oracle.act_round(t, x, r).view(np.uint32), x.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", (0, 1, 30))
+def test_matvec_float_closed_form(oracle, t):
+    """one-hot weight rows give the rounded activation itself; random rows the float64 dot of the decoded
+    weights (the reference's decoder, pinned above) with the rounded activations"""
+    K, N = 96, 5
+    x = synth.gaussian(80 + t, 2 * K).reshape(2, K)
+    if t == 0:
+        enc = lambda w: w.astype(np.float32).view(np.uint8)
+    elif t == 1:
+        enc = lambda w: w.astype(np.float16).view(np.uint8)
+    else:
+        enc = lambda w: (w.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16).view(np.uint8)
+    eye = np.zeros((N, K), np.float32)
+    eye[np.arange(N), [0, 7, 33, 64, 95]] = 1.0
+    ref, mag = oracle.matvec_float(t, enc(eye), N, K, x)
+    assert np.array_equal(ref, oracle.act_round(t, x)[:, [0, 7, 33, 64, 95]].astype(np.float64))
+    w = synth.gaussian(81 + t, N * K, 0, 0.05).reshape(N, K)
+    Wb = enc(w)
+    wd = oracle.to_float(t, Wb, K).astype(np.float64)
+    xa = oracle.act_round(t, x).astype(np.float64)
+    ref, mag = oracle.matvec_float(t, Wb, N, K, x)
+    assert np.allclose(ref, xa @ wd.T, rtol=1e-13, atol=0) and np.allclose(mag, np.abs(xa) @ np.abs(wd).T, rtol=1e-13)
