@@ -1,0 +1,66 @@
+/* moe_layer.h -- one MoE FFN (router, the routed experts and the shared expert) as one call of
+ * libpurhie_qmv.so (gfx950). No counterpart in the reference's library ABI: it is the engine's moe_core /
+ * moe_core_one / shared_as_slot (src/qwen_model.cpp:1093-1166) over the kernels of qmatvec.h and moe_ops.h,
+ * with the same dispatch rules:
+ *   - one token with a shared expert of the routed experts' width, types and row sizes: the shared expert rides
+ *     as slot n_used (id -1) of the experts' launches (gate / up, SwiGLU, down in 3 launches instead of 6; the
+ *     same arithmetic per row, the shared output added last by the combine);
+ *   - 8 tokens or more: the (token, slot) entries grouped by expert for the expert-tiled GEMMs, at the largest
+ *     tile all three expert matrices take (qmatvec_id_batch_tile);
+ *   - otherwise the expert-indexed matvecs, token by token in the decode order (gate / up as one pair launch,
+ *     down with x_per_slot);
+ *   - the shared expert's gate / up and down as plain launches, its output weighted by sigmoid(x . shexp_gate)
+ *     (or 1 without one) and added after the routed experts.
+ * The router logits come from the int8 path when the router's type has an int8 kernel at n_embd, else from
+ * the float-activation path (F32 / F16 / BF16 routers). */
+#ifndef PURHIE_MOE_LAYER_H
+#define PURHIE_MOE_LAYER_H
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "qmatvec.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct purhie_moe_weights {
+    int n_embd, n_ff_exp, n_ff_shexp, n_expert, n_expert_used;
+    /* the routed experts: gate / up [n_expert * n_ff_exp] rows of n_embd (one type), down [n_expert * n_embd]
+     * rows of n_ff_exp */
+    int type_gate_up, type_down;
+    const void *gate_exps, *up_exps, *down_exps;
+    size_t rb_gate_up, rb_down;
+    /* the router: [n_expert] rows of n_embd */
+    int type_router;
+    const void *router;
+    size_t rb_router;
+    /* the shared expert (gate_shexp NULL: none): gate / up [n_ff_shexp] rows of n_embd, down [n_embd] rows of
+     * n_ff_shexp; shexp_gate [n_embd] fp32 (NULL: weight 1) */
+    int type_shexp_gate_up, type_shexp_down;
+    const void *gate_shexp, *up_shexp, *down_shexp;
+    size_t rb_shexp_gate_up, rb_shexp_down;
+    const float *shexp_gate;
+} purhie_moe_weights;
+
+/* Device workspace bytes purhie_moe_ffn needs for T tokens (0: the layer cannot run: a type without an int8
+ * kernel at its K, n_expert > 1024, n_expert_used > 63, or a size out of range). */
+size_t purhie_moe_workspace_bytes(const purhie_moe_weights *w, int T);
+
+/* 1 if a call with T tokens takes the one-token shared-expert-as-slot form */
+int purhie_moe_shared_as_slot(const purhie_moe_weights *w, int T);
+
+/* out [T][n_embd] = the MoE FFN of the T rows of xn [T][n_embd] (fp32), given xn also quantized as one
+ * flattened [T * n_embd] vector in q8_xn (qmatvec_quantize, or a producer's fused quantization). ws: device
+ * memory of at least purhie_moe_workspace_bytes(w, T) bytes, 256-byte aligned. Every launch goes on stream;
+ * nothing is allocated. Returns hipErrorInvalidValue for bad arguments, else the first launch error. */
+hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qmatvec_q8 *q8_xn, int T, float *out,
+                          void *ws, size_t ws_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PURHIE_MOE_LAYER_H */

@@ -1,0 +1,194 @@
+// moe_layer.cpp -- one MoE FFN as one library call (include/moe_layer.h): the engine's moe_core /
+// moe_core_one / shared_as_slot (reference src/qwen_model.cpp:1093-1166) over this library's launches. Host
+// code only: it lays out the caller's workspace and issues the launches on the caller's stream.
+#include "../../include/moe_layer.h"
+#include "../../include/moe_ops.h"
+#include "../../include/qmatvec.h"
+#include "../../include/quant_types.h"
+
+#include <algorithm>
+
+namespace {
+
+constexpr int GROUP_MIN_T = 8;  // batches from this size group their entries by expert (src/qwen_model.cpp:1142)
+
+bool float_router(int t) { return t == QT_F32 || t == QT_F16 || t == QT_BF16; }
+
+bool has_shexp(const purhie_moe_weights *w) { return w->gate_shexp && w->up_shexp && w->down_shexp; }
+
+// src/qwen_model.cpp:1095-1103: the shared expert has the routed experts' width, types and row sizes
+bool slot_form(const purhie_moe_weights *w) {
+    return has_shexp(w) && w->n_ff_shexp == w->n_ff_exp && w->type_shexp_gate_up == w->type_gate_up &&
+           w->type_shexp_down == w->type_down && w->rb_shexp_gate_up == w->rb_gate_up &&
+           w->rb_shexp_down == w->rb_down;
+}
+
+long long round256(long long n) { return (n + 255) / 256 * 256; }
+
+// the workspace regions, each 256-byte aligned
+struct Layout {
+    float *logits = nullptr, *wts = nullptr, *sg = nullptr, *g = nullptr, *u = nullptr, *act = nullptr;
+    float *down = nullptr, *ffg = nullptr, *ffu = nullptr, *sact = nullptr, *shout = nullptr;
+    int32_t *ids = nullptr, *tok = nullptr, *pair = nullptr, *ntiles = nullptr, *te = nullptr, *ts = nullptr,
+            *tn = nullptr;
+    void *qx = nullptr, *qs = nullptr;
+    uint16_t *xh = nullptr;  // a 16-bit copy of xn for an F16 / BF16 router's GEMM
+    int ns = 0, tile = 0, max_tiles = 0, qx_k = 0, qs_k = 0;
+    bool slot = false, grouped = false;
+    size_t bytes = 0;
+};
+
+bool valid(const purhie_moe_weights *w, int T) {
+    if (!w || T < 1 || w->n_embd <= 0 || w->n_ff_exp <= 0 || w->n_expert <= 0 || w->n_expert > 1024 ||
+        w->n_expert_used < 1 || w->n_expert_used > 63 || w->n_expert_used > w->n_expert)
+        return false;
+    if (!w->gate_exps || !w->up_exps || !w->down_exps || !w->router) return false;
+    const int E = w->n_embd, FE = w->n_ff_exp;
+    if (!qmatvec_q8_supported(w->type_gate_up, E) || !qmatvec_q8_supported(w->type_down, FE)) return false;
+    if (w->rb_gate_up != qt_row_size(w->type_gate_up, E) || w->rb_down != qt_row_size(w->type_down, FE)) return false;
+    if (w->rb_router != qt_row_size(w->type_router, E)) return false;
+    if (!qmatvec_q8_supported(w->type_router, E) && !float_router(w->type_router)) return false;
+    if (has_shexp(w)) {
+        const int FS = w->n_ff_shexp;
+        if (FS <= 0 || !qmatvec_q8_supported(w->type_shexp_gate_up, E) || !qmatvec_q8_supported(w->type_shexp_down, FS))
+            return false;
+        if (w->rb_shexp_gate_up != qt_row_size(w->type_shexp_gate_up, E) ||
+            w->rb_shexp_down != qt_row_size(w->type_shexp_down, FS))
+            return false;
+    }
+    // the flattened vectors of the launches stay within int
+    const long long big = (long long)T * (w->n_expert_used + 1) * std::max(E, FE);
+    return big < (1LL << 30) && (long long)T * w->n_expert < (1LL << 30);
+}
+
+Layout layout(const purhie_moe_weights *w, int T, char *base) {
+    Layout L;
+    const int E = w->n_embd, FE = w->n_ff_exp, NE = w->n_expert, NU = w->n_expert_used;
+    const int FS = has_shexp(w) ? w->n_ff_shexp : 0;
+    L.slot = T == 1 && slot_form(w);
+    L.grouped = !L.slot && T >= GROUP_MIN_T;
+    L.ns = L.slot ? NU + 1 : NU;
+    if (L.grouped) {
+        L.tile = std::min({qmatvec_id_batch_tile(w->type_gate_up, FE, E), qmatvec_id_batch_tile(w->type_down, E, FE)});
+        L.max_tiles = gpu_moe_max_tiles(T, NU, NE, L.tile);
+    }
+    L.qx_k = (int)round256((long long)T * L.ns * FE);
+    L.qs_k = FS ? (int)round256((long long)T * FS) : 0;
+    size_t off = 0;
+    auto take = [&](size_t n) {
+        char *p = base ? base + off : nullptr;
+        off += (n + 255) & ~(size_t)255;
+        return p;
+    };
+    L.logits = (float *)take((size_t)T * NE * 4);
+    if (w->type_router == QT_F16 || w->type_router == QT_BF16) L.xh = (uint16_t *)take((size_t)T * E * 2);
+    L.ids = (int32_t *)take((size_t)T * L.ns * 4);
+    L.wts = (float *)take((size_t)T * NU * 4);
+    L.sg = (float *)take((size_t)T * 4);
+    L.g = (float *)take((size_t)T * L.ns * FE * 4);
+    L.u = (float *)take((size_t)T * L.ns * FE * 4);
+    L.act = (float *)take((size_t)T * L.ns * FE * 4);
+    L.down = (float *)take((size_t)T * L.ns * E * 4);
+    L.qx = take(qmatvec_q8_bytes(L.qx_k));
+    if (L.grouped) {
+        L.tok = (int32_t *)take((size_t)T * NU * 4);
+        L.pair = (int32_t *)take((size_t)T * NU * 4);
+        L.ntiles = (int32_t *)take(4);
+        L.te = (int32_t *)take((size_t)L.max_tiles * 4);
+        L.ts = (int32_t *)take((size_t)L.max_tiles * 4);
+        L.tn = (int32_t *)take((size_t)L.max_tiles * 4);
+    }
+    if (FS && !L.slot) {
+        L.ffg = (float *)take((size_t)T * FS * 4);
+        L.ffu = (float *)take((size_t)T * FS * 4);
+        L.sact = (float *)take((size_t)T * FS * 4);
+        L.shout = (float *)take((size_t)T * E * 4);
+        L.qs = take(qmatvec_q8_bytes(L.qs_k));
+    }
+    L.bytes = off;
+    return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t purhie_moe_workspace_bytes(const purhie_moe_weights *w, int T) {
+    if (!valid(w, T)) return 0;
+    return layout(w, T, nullptr).bytes;
+}
+
+int purhie_moe_shared_as_slot(const purhie_moe_weights *w, int T) { return valid(w, T) && T == 1 && slot_form(w); }
+
+hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qmatvec_q8 *q8_xn, int T, float *out,
+                          void *ws, size_t ws_bytes, hipStream_t stream) {
+    if (!valid(w, T) || !xn || !q8_xn || !out || !ws || ((uintptr_t)ws & 255)) return hipErrorInvalidValue;
+    if ((long long)T * w->n_embd > q8_xn->max_k) return hipErrorInvalidValue;
+    const Layout L = layout(w, T, (char *)ws);
+    if (ws_bytes < L.bytes) return hipErrorInvalidValue;
+    const int E = w->n_embd, FE = w->n_ff_exp, NE = w->n_expert, NU = w->n_expert_used;
+    const bool sh = has_shexp(w);
+    qmatvec_q8 qx, qs;
+    qmatvec_q8_bind(&qx, L.qx, L.qx_k);
+    hipError_t e;
+#define PQ_TRY(call)                       \
+    do {                                   \
+        if ((e = (call)) != hipSuccess) return e; \
+    } while (0)
+
+    // router logits [T][NE]
+    if (qmatvec_q8_supported(w->type_router, E))
+        PQ_TRY(qmatvec_launch_q8_batch(w->type_router, w->router, w->rb_router, q8_xn, L.logits, NE, NE, E, T, stream));
+    else
+        PQ_TRY(qmatvec_launch_batch_h(w->type_router, w->router, w->rb_router, xn, L.xh, L.xh ? (size_t)T * E * 2 : 0,
+                                      L.logits, NE, E, T, stream));
+    PQ_TRY(gpu_moe_router(L.logits, xn, sh ? w->shexp_gate : nullptr, L.ids, L.wts, sh && w->shexp_gate ? L.sg : nullptr,
+                          NE, NU, E, T, stream, L.ns));
+    const float *sg = sh && w->shexp_gate ? L.sg : nullptr;
+
+    if (L.slot) {  // src/qwen_model.cpp:1105-1134: one token, the shared expert as slot NU (id -1)
+        PQ_TRY(qmatvec_launch_q8_id_x(w->type_gate_up, w->gate_exps, w->up_exps, w->gate_shexp, w->up_shexp,
+                                      w->rb_gate_up, L.ids, L.ns, 0, q8_xn, L.g, L.u, FE, E, 1, stream));
+        PQ_TRY(gpu_swiglu(L.g, L.u, L.act, L.ns * FE, &qx, stream));
+        PQ_TRY(qmatvec_launch_q8_id_x(w->type_down, w->down_exps, nullptr, w->down_shexp, nullptr, w->rb_down, L.ids,
+                                      L.ns, 1, &qx, L.down, nullptr, E, FE, 1, stream));
+        return gpu_moe_combine(L.down, L.wts, L.down + (size_t)NU * E, sg, out, NU, E, 1, stream);
+    }
+
+    // src/qwen_model.cpp:1137-1166
+    if (L.grouped) {
+        PQ_TRY(gpu_moe_group(L.ids, T, NU, NE, L.tile, L.tok, L.pair, L.ntiles, L.te, L.ts, L.tn, stream));
+        PQ_TRY(qmatvec_launch_q8_id_batch(w->type_gate_up, w->gate_exps, w->rb_gate_up, q8_xn, L.g, FE, E, L.max_tiles,
+                                          L.tile, L.ntiles, L.te, L.ts, L.tn, L.tok, L.pair, stream));
+        PQ_TRY(qmatvec_launch_q8_id_batch(w->type_gate_up, w->up_exps, w->rb_gate_up, q8_xn, L.u, FE, E, L.max_tiles,
+                                          L.tile, L.ntiles, L.te, L.ts, L.tn, L.tok, L.pair, stream));
+    } else {
+        PQ_TRY(qmatvec_launch_q8_id_pair(w->type_gate_up, w->gate_exps, w->up_exps, w->rb_gate_up, L.ids, NU, 0, q8_xn,
+                                         L.g, L.u, FE, E, T, stream));
+    }
+    if (sh) {
+        const int FS = w->n_ff_shexp;
+        PQ_TRY(qmatvec_launch_q8_batch(w->type_shexp_gate_up, w->gate_shexp, w->rb_shexp_gate_up, q8_xn, L.ffg, FS, FS,
+                                       E, T, stream));
+        PQ_TRY(qmatvec_launch_q8_batch(w->type_shexp_gate_up, w->up_shexp, w->rb_shexp_gate_up, q8_xn, L.ffu, FS, FS,
+                                       E, T, stream));
+    }
+    PQ_TRY(gpu_swiglu(L.g, L.u, L.act, T * NU * FE, &qx, stream));
+    if (L.grouped)
+        PQ_TRY(qmatvec_launch_q8_id_batch(w->type_down, w->down_exps, w->rb_down, &qx, L.down, E, FE, L.max_tiles,
+                                          L.tile, L.ntiles, L.te, L.ts, L.tn, L.pair, L.pair, stream));
+    else
+        PQ_TRY(qmatvec_launch_q8_id(w->type_down, w->down_exps, w->rb_down, L.ids, NU, 1, &qx, L.down, E, FE, T,
+                                    stream));
+    if (!sh) return gpu_moe_combine(L.down, L.wts, nullptr, nullptr, out, NU, E, T, stream);
+
+    const int FS = w->n_ff_shexp;
+    qmatvec_q8_bind(&qs, L.qs, L.qs_k);
+    PQ_TRY(gpu_swiglu(L.ffg, L.ffu, L.sact, T * FS, &qs, stream));
+    PQ_TRY(qmatvec_launch_q8_batch(w->type_shexp_down, w->down_shexp, w->rb_shexp_down, &qs, L.shout, E, E, FS, T,
+                                   stream));
+    return gpu_moe_combine(L.down, L.wts, L.shout, sg, out, NU, E, T, stream);
+#undef PQ_TRY
+}
+
+}  // extern "C"

@@ -1,5 +1,6 @@
 """ctypes mirror of include/moe_ops.h (the fused add + RMSNorm + quantize and SwiGLU + quantize producers, and
-the MoE router, grouping and combine of libpurhie_qmv.so), the reference's src/gpu_ops.h entry points. Device buffers are torch tensors; every
+the MoE router, grouping and combine of libpurhie_qmv.so), the reference's src/gpu_ops.h entry points, and of
+include/moe_layer.h (one MoE FFN per call, the engine's moe_core dispatch). Device buffers are torch tensors; every
 call runs the library's HIP kernels (no CPU path)."""
 import ctypes as C
 
@@ -23,15 +24,43 @@ def lib():
             "gpu_moe_combine": [vp, vp, vp, vp, vp, i32, i32, i32, vp],
             "gpu_moe_combine_scaled": [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp],
             "gpu_moe_group": [vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp],
+            "purhie_moe_shared_as_slot": [C.POINTER(MoeWeights), i32],
+            "purhie_moe_ffn": [C.POINTER(MoeWeights), vp, pq8, i32, vp, vp, C.c_size_t, vp],
         }.items():
             f = getattr(L, name)
             f.restype, f.argtypes = i32, args
+        L.purhie_moe_workspace_bytes.restype = C.c_size_t
+        L.purhie_moe_workspace_bytes.argtypes = [C.POINTER(MoeWeights), i32]
         _sigs_done = True
     return L
 
 
+class MoeWeights(C.Structure):
+    """purhie_moe_weights (include/moe_layer.h)"""
+    _fields_ = [("n_embd", C.c_int), ("n_ff_exp", C.c_int), ("n_ff_shexp", C.c_int), ("n_expert", C.c_int),
+                ("n_expert_used", C.c_int),
+                ("type_gate_up", C.c_int), ("type_down", C.c_int),
+                ("gate_exps", C.c_void_p), ("up_exps", C.c_void_p), ("down_exps", C.c_void_p),
+                ("rb_gate_up", C.c_size_t), ("rb_down", C.c_size_t),
+                ("type_router", C.c_int), ("router", C.c_void_p), ("rb_router", C.c_size_t),
+                ("type_shexp_gate_up", C.c_int), ("type_shexp_down", C.c_int),
+                ("gate_shexp", C.c_void_p), ("up_shexp", C.c_void_p), ("down_shexp", C.c_void_p),
+                ("rb_shexp_gate_up", C.c_size_t), ("rb_shexp_down", C.c_size_t),
+                ("shexp_gate", C.c_void_p)]
+
+
 def _p(t):
     return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def ffn(w, xn, q8, T, out, ws, stream=None):
+    """purhie_moe_ffn: out [T][n_embd] from xn [T][n_embd] and its quantized form q8 (a Q.Q8), ws a device
+    uint8 tensor of at least workspace_bytes(w, T) bytes"""
+    _check("purhie_moe_ffn", lib().purhie_moe_ffn(C.byref(w), _p(xn), q8.ref, T, _p(out), _p(ws), ws.numel(), stream))
+
+
+def workspace_bytes(w, T):
+    return lib().purhie_moe_workspace_bytes(C.byref(w), T)
 
 
 def _check(fn, rc):
