@@ -8,7 +8,8 @@
  *   - 8 tokens or more: the (token, slot) entries grouped by expert for the expert-tiled GEMMs, at the largest
  *     tile all three expert matrices take (qmatvec_id_batch_tile);
  *   - otherwise the expert-indexed matvecs, token by token in the decode order (gate / up as one pair launch,
- *     down with x_per_slot);
+ *     down with x_per_slot; for a Q8_0-activation down type the SwiGLU and its quantization run inside the down
+ *     launch, qmatvec_launch_q8_id_swiglu, with the same bits);
  *   - the shared expert's gate / up and down as plain launches, its output weighted by sigmoid(x . shexp_gate)
  *     (or 1 without one) and added after the routed experts.
  * The router logits come from the int8 path when the router's type has an int8 kernel at n_embd, else from

@@ -163,6 +163,17 @@ hipError_t qmatvec_launch_q8_id_x(int type, const void *W, const void *W2, const
                                   size_t row_bytes, const int32_t *ids, int n_used, int x_per_slot,
                                   const qmatvec_q8 *q, float *y, float *y2, int N, int K, int T, hipStream_t stream);
 
+/* No counterpart in the reference (it launches gpu_swiglu, then qmatvec_launch_q8_id with x_per_slot = 1): the
+ * expert down matvec of a decode step with the SwiGLU launch folded in. Entry (t, slot) reads row t * n_used +
+ * slot of g and u (K floats each), quantizes SwiGLU(g, u) = g / (1 + exp(-g)) * u to Q8_0 in the kernel and
+ * multiplies it by expert ids[t * n_used + slot] (Wx for -1) into row t * n_used + slot of y: bit-identical to
+ * the two launches, one launch fewer. For the Q8_0-activation types (Q8_0, ROCmFP4, FAST, MXFP4, NVFP4), K % 256
+ * == 0, K <= 16384; _supported says whether a launch takes it. */
+int qmatvec_q8_id_swiglu_supported(int type, int K);
+hipError_t qmatvec_launch_q8_id_swiglu(int type, const void *W, const void *Wx, size_t row_bytes, const int32_t *ids,
+                                       int n_used, const float *g, const float *u, float *y, int N, int K, int T,
+                                       hipStream_t stream);
+
 /* replaces src/qmatvec.h:189-195: MoE prefill over gpu_moe_group's expert tiles (tile k: expert
  * tile_e[k], entries tile_start[k] .. + tile_n[k] - 1 of in_rows / out_rows) */
 int qmatvec_id_batch_tile(int type, int N, int K);

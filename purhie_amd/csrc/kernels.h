@@ -56,8 +56,12 @@ struct MvIdArgs {
     // tile_n[k]) multiplies input row in_rows[tile_start[k] + i] by expert tile_e[k] into output row out_rows[..]
     const int32_t *n_tiles, *tile_e, *tile_start, *tile_n, *in_rows, *out_rows;
     int tile, max_tiles;
+    // set: the input rows are SwiGLU(sw_g, sw_u) (row in_row of each, K floats), quantized to Q8_0 in the kernel
+    // (q / d unused; the tile kernel of a Q8_0-activation type only)
+    const float *sw_g, *sw_u;
 };
 hipError_t launch_matvec_id(int type, const MvIdArgs &a, hipStream_t stream);
+bool matvec_id_swiglu_supported(int type, int K);
 
 // the one-unit-per-lane tile kernels (mv_tile.hip); hipErrorNotSupported for a shape or alignment they do
 // not take (launch_matvec / launch_matvec_id then use the per-wave kernels)

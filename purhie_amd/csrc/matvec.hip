@@ -793,7 +793,17 @@ static hipError_t launch_id_t(const MvIdArgs &a, hipStream_t stream) {
     return hipErrorInvalidValue;
 }
 
+// the SwiGLU-fused input exists in the tile kernel of the Q8_0-activation types only
+bool matvec_id_swiglu_supported(int type, int K) {
+    return tile_enabled() && (type == TY_Q8_0 || type == TY_FP4 || type == TY_FAST || type == TY_MXFP4 ||
+                              type == TY_NVFP4) && K % 256 == 0 && K <= 16384;
+}
+
 hipError_t launch_matvec_id(int type, const MvIdArgs &a, hipStream_t stream) {
+    if (a.sw_g) {  // (no per-wave form)
+        const hipError_t e = launch_matvec_id_tile(type, a, stream);
+        return e == hipErrorNotSupported ? hipErrorInvalidDeviceFunction : e;
+    }
     if (tile_enabled()) {
         const hipError_t e = launch_matvec_id_tile(type, a, stream);
         if (e != hipErrorNotSupported) return e;

@@ -146,12 +146,20 @@ hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qm
                           NE, NU, E, T, stream, L.ns));
     const float *sg = sh && w->shexp_gate ? L.sg : nullptr;
 
+    // the expert down matvec reads SwiGLU(g, u) quantized in its own kernel where the type allows (the same bits
+    // as gpu_swiglu's quantization and the plain launch: one launch fewer)
+    const bool fuse = !L.grouped && qmatvec_q8_id_swiglu_supported(w->type_down, FE);
     if (L.slot) {  // src/qwen_model.cpp:1105-1134: one token, the shared expert as slot NU (id -1)
         PQ_TRY(qmatvec_launch_q8_id_x(w->type_gate_up, w->gate_exps, w->up_exps, w->gate_shexp, w->up_shexp,
                                       w->rb_gate_up, L.ids, L.ns, 0, q8_xn, L.g, L.u, FE, E, 1, stream));
-        PQ_TRY(gpu_swiglu(L.g, L.u, L.act, L.ns * FE, &qx, stream));
-        PQ_TRY(qmatvec_launch_q8_id_x(w->type_down, w->down_exps, nullptr, w->down_shexp, nullptr, w->rb_down, L.ids,
-                                      L.ns, 1, &qx, L.down, nullptr, E, FE, 1, stream));
+        if (fuse) {
+            PQ_TRY(qmatvec_launch_q8_id_swiglu(w->type_down, w->down_exps, w->down_shexp, w->rb_down, L.ids, L.ns, L.g,
+                                               L.u, L.down, E, FE, 1, stream));
+        } else {
+            PQ_TRY(gpu_swiglu(L.g, L.u, L.act, L.ns * FE, &qx, stream));
+            PQ_TRY(qmatvec_launch_q8_id_x(w->type_down, w->down_exps, nullptr, w->down_shexp, nullptr, w->rb_down,
+                                          L.ids, L.ns, 1, &qx, L.down, nullptr, E, FE, 1, stream));
+        }
         return gpu_moe_combine(L.down, L.wts, L.down + (size_t)NU * E, sg, out, NU, E, 1, stream);
     }
 
@@ -173,13 +181,18 @@ hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qm
         PQ_TRY(qmatvec_launch_q8_batch(w->type_shexp_gate_up, w->up_shexp, w->rb_shexp_gate_up, q8_xn, L.ffu, FS, FS,
                                        E, T, stream));
     }
-    PQ_TRY(gpu_swiglu(L.g, L.u, L.act, T * NU * FE, &qx, stream));
-    if (L.grouped)
-        PQ_TRY(qmatvec_launch_q8_id_batch(w->type_down, w->down_exps, w->rb_down, &qx, L.down, E, FE, L.max_tiles,
-                                          L.tile, L.ntiles, L.te, L.ts, L.tn, L.pair, L.pair, stream));
-    else
-        PQ_TRY(qmatvec_launch_q8_id(w->type_down, w->down_exps, w->rb_down, L.ids, NU, 1, &qx, L.down, E, FE, T,
-                                    stream));
+    if (fuse) {
+        PQ_TRY(qmatvec_launch_q8_id_swiglu(w->type_down, w->down_exps, nullptr, w->rb_down, L.ids, NU, L.g, L.u, L.down,
+                                           E, FE, T, stream));
+    } else {
+        PQ_TRY(gpu_swiglu(L.g, L.u, L.act, T * NU * FE, &qx, stream));
+        if (L.grouped)
+            PQ_TRY(qmatvec_launch_q8_id_batch(w->type_down, w->down_exps, w->rb_down, &qx, L.down, E, FE, L.max_tiles,
+                                              L.tile, L.ntiles, L.te, L.ts, L.tn, L.pair, L.pair, stream));
+        else
+            PQ_TRY(qmatvec_launch_q8_id(w->type_down, w->down_exps, w->rb_down, L.ids, NU, 1, &qx, L.down, E, FE, T,
+                                        stream));
+    }
     if (!sh) return gpu_moe_combine(L.down, L.wts, nullptr, nullptr, out, NU, E, T, stream);
 
     const int FS = w->n_ff_shexp;

@@ -538,16 +538,48 @@ struct Stager {
     }
 };
 
-// One tile: rows [row0, row0 + nr) of one matrix (contiguous, nb units each, nr * nb <= THR).
-template <int TYPE, int NT, int THR, class Rows>
+// The activation of one token as SwiGLU(g, u) = g / (1 + exp(-g)) * u, quantized to Q8_0 straight into the tile's
+// LDS (values and block scales where the stager puts them): the arithmetic of gpu_swiglu and of the quantizer's
+// Q8_0 step (q8dev.h), so the tile sees the bits the two launches give. Half a wave holds a 32-value block (K % 32
+// == 0: a half-wave is all in or all out).
+template <int TYPE, int THR>
+__device__ __forceinline__ void stage_swiglu_q8_0(const TileLds<TYPE> &L, uint8_t *smem, const float *g,
+                                                  const float *u, int K) {
+    float *ld = (float *)(smem + L.off_d);
+    for (int base = 0; base < K; base += THR) {
+        const int i = base + (int)threadIdx.x;
+        const bool active = i < K;
+        float v = 0.0f;
+        if (active) {
+            const float a = g[i];
+            v = a / (1.0f + expf(-a)) * u[i];
+        }
+        float am = fabsf(v);
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+        const float id0 = am != 0.0f ? 127.0f / am : 0.0f;
+        if (active) {
+            smem[(i >> 8) * TL_PAD + (i & 255)] = (uint8_t)(int8_t)(int)rintf(v * id0);
+            if ((threadIdx.x & 31) == 0) ld[i >> 5] = __half2float(__float2half(am / 127.0f));
+        }
+    }
+    if constexpr (Tu<TYPE>::LUT)
+        for (int e = threadIdx.x; e < 256; e += THR) ((float *)(smem + L.off_lut))[e] = Tu<TYPE>::scale((uint32_t)e);
+}
+
+// One tile: rows [row0, row0 + nr) of one matrix (contiguous, nb units each, nr * nb <= THR). SW: the activation
+// is SwiGLU(sg, su) quantized here (NT 1, a Q8_0-activation type), else q / d / bs staged as they are.
+template <int TYPE, int NT, int THR, class Rows, bool SW = false>
 __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int row0, int nr, int K, int nb, int lg,
-                                          const int8_t *q, const float *d, const int32_t *bs) {
+                                          const int8_t *q, const float *d, const int32_t *bs,
+                                          const float *sg = nullptr, const float *su = nullptr) {
     using P = Tu<TYPE>;
     using TL = TileLds<TYPE>;
+    static_assert(!SW || (NT == 1 && P::ACT == 32 && P::SUMS == 0), "SwiGLU staging: one token, Q8_0 activation");
     const TL L(K, NT, THR);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     Stager<TYPE, NT, THR> st;
-    st.issue(L, q, d, bs, K);
+    if constexpr (!SW) st.issue(L, q, d, bs, K);
 
     // this wave's units [64 wave, 64 wave + wu) of the tile: bytes [g, g + wu BYTES), loaded as the 16-byte
     // chunks from the aligned address a at or below g (each chunk holds at least one byte of the range)
@@ -565,7 +597,8 @@ __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int r
         c[i] = ld128_nt(ga + 16 * (ci < nch ? ci : nch - 1));
     }
 
-    st.commit(L, smem, q, d, bs, K);
+    if constexpr (SW) stage_swiglu_q8_0<TYPE, THR>(L, smem, sg, su, K);
+    else st.commit(L, smem, q, d, bs, K);
     __syncthreads();
     uint8_t *region = smem + L.off_w + wave * TL::REGION;
 #pragma unroll
@@ -649,7 +682,7 @@ __global__ void __launch_bounds__(THR) k_mv_tile(MvArgs a, TileArgs ta) {
 
 // MoE: grid (tiles, n_used * nmat, T); slot j of token t uses expert ids[t * n_used + j] (-1: Wx). Tiles mode:
 // grid (tiles, tile, max_tiles) over moe_group's expert tiles, one entry per block.
-template <int TYPE, int THR>
+template <int TYPE, int THR, bool SW = false>
 __global__ void __launch_bounds__(THR) k_mv_tile_id(MvIdArgs a, TileArgs ta) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     IdEntry en;
@@ -661,8 +694,12 @@ __global__ void __launch_bounds__(THR) k_mv_tile_id(MvIdArgs a, TileArgs ta) {
                       a.y[m] + en.out_row * a.N, e < 0 ? a.sx[m] : a.es[m] ? a.es[m][e] : a.s[m]};
     const int row0 = (int)blockIdx.x * ta.R;
     const int nr = a.N - row0 < ta.R ? a.N - row0 : ta.R;
-    tile_body<TYPE, 1, THR>(smem, rows, row0, nr, K, ta.nb, ta.lg, a.q + in_row * K, a.d + in_row * (K / Tu<TYPE>::ACT),
-                       a.bs ? a.bs + in_row * (K / 16) : nullptr);
+    if constexpr (SW)
+        tile_body<TYPE, 1, THR, IdRows, true>(smem, rows, row0, nr, K, ta.nb, ta.lg, nullptr, nullptr, nullptr,
+                                              a.sw_g + in_row * K, a.sw_u + in_row * K);
+    else
+        tile_body<TYPE, 1, THR>(smem, rows, row0, nr, K, ta.nb, ta.lg, a.q + in_row * K,
+                                a.d + in_row * (K / Tu<TYPE>::ACT), a.bs ? a.bs + in_row * (K / 16) : nullptr);
 }
 
 // ---------------------------------------------------------------- host side
@@ -767,6 +804,14 @@ static hipError_t tile_id_thr(const MvIdArgs &a, hipStream_t stream) {
     const dim3 grid = a.n_tiles ? dim3(gx, (unsigned)a.tile, (unsigned)a.max_tiles)
                                 : dim3(gx, (unsigned)(a.n_used * a.nmat), (unsigned)a.T);
     const size_t lds = (size_t)TileLds<TYPE>(a.K, 1, THR).bytes;
+    if constexpr (Tu<TYPE>::ACT == 32 && Tu<TYPE>::SUMS == 0) {
+        if (a.sw_g) {
+            hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, true>), grid, dim3(THR), lds, stream, a, ta);
+            return hipGetLastError();
+        }
+    } else if (a.sw_g) {
+        return hipErrorInvalidDeviceFunction;
+    }
     hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR>), grid, dim3(THR), lds, stream, a, ta);
     return hipGetLastError();
 }
@@ -776,7 +821,9 @@ static hipError_t tile_id(const MvIdArgs &a, hipStream_t stream) {
     // (null Wx entries pass the alignment check; a row of activation is K values, K / ACT scales and K / 16
     // sums on from the previous one, which keeps every row as aligned as the first when K % VALS == 0)
     const uint8_t *W[4] = {a.W[0], a.Wx[0], a.nmat > 1 ? a.W[1] : nullptr, a.nmat > 1 ? a.Wx[1] : nullptr};
-    if (!tile_takes<TYPE>(a.K, 1, W, 4, a.row_bytes, a.q, a.d, a.bs)) return hipErrorNotSupported;
+    // (SwiGLU staging reads its floats one by one: no activation pointer to check, null passes)
+    if (!tile_takes<TYPE>(a.K, 1, W, 4, a.row_bytes, a.sw_g ? nullptr : a.q, a.sw_g ? nullptr : a.d, a.bs))
+        return hipErrorNotSupported;
     // (expert-indexed launches keep whole 256-thread tiles: every workgroup first reads its entry's expert id and
     // stages its activation, and smaller tiles measured slower, e.g. config 4's expert down matvec 7.5 vs 6.0 us)
     switch (tile_threads(a.K / Tu<TYPE>::VALS, 1ll << 40)) {

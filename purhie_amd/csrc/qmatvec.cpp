@@ -445,6 +445,47 @@ hipError_t qmatvec_launch_q8_id_x(int type, const void *W, const void *W2, const
     return launch_matvec_id(type, a, stream);
 }
 
+int qmatvec_q8_id_swiglu_supported(int type, int K) {
+    return qmatvec_q8_supported(type, K) && matvec_id_swiglu_supported(type, K) ? 1 : 0;
+}
+
+// the expert down matvec of a decode step with the SwiGLU launch folded in: entry (t, slot) reads row
+// t * n_used + slot of g and u, and the kernel quantizes SwiGLU of it to Q8_0 as gpu_swiglu's fused quantizer
+// would, so y is bit-identical to gpu_swiglu(g, u, .., q8) followed by qmatvec_launch_q8_id(.., x_per_slot = 1, q8)
+hipError_t qmatvec_launch_q8_id_swiglu(int type, const void *W, const void *Wx, size_t row_bytes, const int32_t *ids,
+                                       int n_used, const float *g, const float *u, float *y, int N, int K, int T,
+                                       hipStream_t stream) {
+    if (!qmatvec_q8_id_swiglu_supported(type, K)) return hipErrorInvalidDeviceFunction;
+    const uintptr_t am = w_align(type) - 1;
+    if (!W || !ids || !g || !u || !y || T <= 0 || n_used <= 0 || N <= 0 || row_bytes != qt_row_size(type, K) ||
+        ((uintptr_t)W & am) != 0 || ((uintptr_t)Wx & am) != 0)
+        return hipErrorInvalidValue;
+    MvIdArgs a{};
+    a.W[0] = (const uint8_t *)W;
+    a.Wx[0] = (const uint8_t *)Wx;
+    a.y[0] = y;
+    a.es[0] = a.es[1] = nullptr;
+    a.s[0] = a.s[1] = a.sx[0] = a.sx[1] = 1.0f;
+    OutScale o;
+    if (find_scale(W, o)) {
+        if (o.n > 1) a.es[0] = o.s;
+        else a.s[0] = o.s[0];
+    }
+    if (Wx) a.sx[0] = dense_scale(Wx);
+    a.row_bytes = (long long)row_bytes;
+    a.ids = ids;
+    a.sw_g = g;
+    a.sw_u = u;
+    a.n_used = n_used;
+    a.x_per_slot = 1;
+    a.N = N;
+    a.K = K;
+    a.T = T;
+    a.nmat = 1;
+    a.L = matvec_lanes(type, K, (long long)N * n_used * T);
+    return launch_matvec_id(type, a, stream);
+}
+
 hipError_t qmatvec_launch_q8_id(int type, const void *W, size_t row_bytes, const int32_t *ids, int n_used,
                                 int x_per_slot, const qmatvec_q8 *q, float *y, int N, int K, int T, hipStream_t stream) {
     return qmatvec_launch_q8_id_x(type, W, nullptr, nullptr, nullptr, row_bytes, ids, n_used, x_per_slot, q, y,

@@ -83,6 +83,8 @@ def lib():
             "qmatvec_prefill": (i32, []),
             "qmatvec_set_out_scale": (i32, [vp, vp, sz, vp, i32]),
             "qmatvec_supported": (i32, [i32]),
+            "qmatvec_q8_id_swiglu_supported": (i32, [i32, i32]),
+            "qmatvec_launch_q8_id_swiglu": (i32, [i32, vp, vp, sz, vp, i32, vp, vp, vp, i32, i32, i32, vp]),
             "qmatvec_launch": (i32, [i32, vp, sz, vp, vp, i32, i32, vp]),
             "qmatvec_launch_bf16f": (i32, [vp, sz, vp, vp, i32, i32, i32, vp]),
             "qmatvec_launch_batch": (i32, [i32, vp, sz, vp, vp, i32, i32, i32, vp]),
