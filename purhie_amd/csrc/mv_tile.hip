@@ -541,31 +541,49 @@ struct Stager {
 // The activation of one token as SwiGLU(g, u) = g / (1 + exp(-g)) * u, quantized to Q8_0 straight into the tile's
 // LDS (values and block scales where the stager puts them): the arithmetic of gpu_swiglu and of the quantizer's
 // Q8_0 step (q8dev.h), so the tile sees the bits the two launches give. Half a wave holds a 32-value block (K % 32
-// == 0: a half-wave is all in or all out).
+// == 0: a half-wave is all in or all out). issue() loads the first SW_R values of each thread before the weights
+// are issued (as the stager's first loads), commit() the rest, then computes and writes.
+constexpr int SW_R = 4;
 template <int TYPE, int THR>
-__device__ __forceinline__ void stage_swiglu_q8_0(const TileLds<TYPE> &L, uint8_t *smem, const float *g,
-                                                  const float *u, int K) {
-    float *ld = (float *)(smem + L.off_d);
-    for (int base = 0; base < K; base += THR) {
-        const int i = base + (int)threadIdx.x;
-        const bool active = i < K;
-        float v = 0.0f;
-        if (active) {
-            const float a = g[i];
-            v = a / (1.0f + expf(-a)) * u[i];
+struct SwStager {
+    float gv[SW_R], uv[SW_R];
+    __device__ __forceinline__ void issue(const float *g, const float *u, int K) {
+#pragma unroll
+        for (int j = 0; j < SW_R; ++j) {
+            const int i = j * THR + (int)threadIdx.x, c = i < K ? i : K - 1;  // (clamped, unconditional loads)
+            gv[j] = g[c];
+            uv[j] = u[c];
         }
+    }
+    __device__ __forceinline__ void put(const TileLds<TYPE> &L, uint8_t *smem, int i, bool active, float a,
+                                        float b) {
+        float v = 0.0f;
+        if (active) v = a / (1.0f + expf(-a)) * b;
         float am = fabsf(v);
 #pragma unroll
         for (int off = 16; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
         const float id0 = am != 0.0f ? 127.0f / am : 0.0f;
         if (active) {
             smem[(i >> 8) * TL_PAD + (i & 255)] = (uint8_t)(int8_t)(int)rintf(v * id0);
-            if ((threadIdx.x & 31) == 0) ld[i >> 5] = __half2float(__float2half(am / 127.0f));
+            if ((threadIdx.x & 31) == 0) ((float *)(smem + L.off_d))[i >> 5] = __half2float(__float2half(am / 127.0f));
         }
     }
-    if constexpr (Tu<TYPE>::LUT)
-        for (int e = threadIdx.x; e < 256; e += THR) ((float *)(smem + L.off_lut))[e] = Tu<TYPE>::scale((uint32_t)e);
-}
+    __device__ __forceinline__ void commit(const TileLds<TYPE> &L, uint8_t *smem, const float *g, const float *u,
+                                           int K) {
+#pragma unroll
+        for (int j = 0; j < SW_R; ++j) {
+            const int i = j * THR + (int)threadIdx.x;
+            if (j * THR < K) put(L, smem, i, i < K, gv[j], uv[j]);  // (uniform)
+        }
+        for (int base = SW_R * THR; base < K; base += THR) {
+            const int i = base + (int)threadIdx.x;
+            put(L, smem, i, i < K, i < K ? g[i] : 0.0f, i < K ? u[i] : 0.0f);
+        }
+        if constexpr (Tu<TYPE>::LUT)
+            for (int e = threadIdx.x; e < 256; e += THR)
+                ((float *)(smem + L.off_lut))[e] = Tu<TYPE>::scale((uint32_t)e);
+    }
+};
 
 // One tile: rows [row0, row0 + nr) of one matrix (contiguous, nb units each, nr * nb <= THR). SW: the activation
 // is SwiGLU(sg, su) quantized here (NT 1, a Q8_0-activation type), else q / d / bs staged as they are.
@@ -579,7 +597,9 @@ __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int r
     const TL L(K, NT, THR);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     Stager<TYPE, NT, THR> st;
-    if constexpr (!SW) st.issue(L, q, d, bs, K);
+    SwStager<TYPE, THR> sws;
+    if constexpr (SW) sws.issue(sg, su, K);
+    else st.issue(L, q, d, bs, K);
 
     // this wave's units [64 wave, 64 wave + wu) of the tile: bytes [g, g + wu BYTES), loaded as the 16-byte
     // chunks from the aligned address a at or below g (each chunk holds at least one byte of the range)
@@ -597,7 +617,7 @@ __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int r
         c[i] = ld128_nt(ga + 16 * (ci < nch ? ci : nch - 1));
     }
 
-    if constexpr (SW) stage_swiglu_q8_0<TYPE, THR>(L, smem, sg, su, K);
+    if constexpr (SW) sws.commit(L, smem, sg, su, K);
     else st.commit(L, smem, q, d, bs, K);
     __syncthreads();
     uint8_t *region = smem + L.off_w + wave * TL::REGION;
