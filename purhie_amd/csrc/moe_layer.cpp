@@ -130,6 +130,8 @@ hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qm
     const bool sh = has_shexp(w);
     qmatvec_q8 qx, qs;
     qmatvec_q8_bind(&qx, L.qx, L.qx_k);
+    if (!qt_vec_dot_q8k(w->type_down)) qx.qK = nullptr;  // (a Q8_0-activation down never reads the Q8_K side: the
+                                                          // SwiGLU launch then skips it)
     hipError_t e;
 #define PQ_TRY(call)                       \
     do {                                   \
@@ -197,6 +199,7 @@ hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qm
 
     const int FS = w->n_ff_shexp;
     qmatvec_q8_bind(&qs, L.qs, L.qs_k);
+    if (!qt_vec_dot_q8k(w->type_shexp_down)) qs.qK = nullptr;
     PQ_TRY(gpu_swiglu(L.ffg, L.ffu, L.sact, T * FS, &qs, stream));
     PQ_TRY(qmatvec_launch_q8_batch(w->type_shexp_down, w->down_shexp, w->rb_shexp_down, &qs, L.shout, E, E, FS, T,
                                    stream));
