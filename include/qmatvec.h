@@ -27,8 +27,12 @@ int qmatvec_init(const char *co_path);
 void qmatvec_free(void);
 
 /* replaces src/qmatvec.h:24-26: NVFP4-style output scale registry (the outputs of launches on the
- * matrix at W are multiplied by s[0], or by s[e] for expert e of n stacked experts). s is read on the
- * host at launch time. Returns 0 or -1. */
+ * matrix at W, bytes long, are multiplied by s[0], or by s[e] for expert e of n stacked experts of bytes / n
+ * each). s must stay readable by both the CPU and the GPU (pinned or managed memory) while it is registered:
+ * dense launches read their factor on the host at launch time, expert-indexed launches and expert-tiled GEMMs
+ * over n > 1 experts hand s to the kernel, which reads s[e] on the device. owner groups registrations for
+ * qmatvec_drop_out_scales. Where registered ranges overlap, the earliest registration holding W applies.
+ * Returns 0 or -1. */
 int qmatvec_set_out_scale(const void *owner, const void *W, size_t bytes, const float *s, int n);
 void qmatvec_drop_out_scales(const void *owner);
 
@@ -198,7 +202,30 @@ hipError_t qmatvec_launch_id_batch_f(int type, const void *W, size_t row_bytes, 
                                      const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
                                      const int32_t *out_rows, hipStream_t stream);
 
-/* No counterpart in the reference: a test hook for the parity tests. The integer dot of every weight
+/* No counterpart in the reference: test hooks for the parity tests (no effect on the results).
+ * qmatvec_debug_capture(out, n_ints): capture mode on (out: device memory the caller zeroed) or off (out null).
+ *   While on, each int8 launch runs its kernel's capture instantiation -- the same decode and integer dot code,
+ *   which also adds every integer sum it forms into out (integer atomics, so sums a kernel splits over lanes
+ *   arrive whole). Layouts (G = qmatvec_debug_capture_unit(type, 0), U = qmatvec_debug_capture_unit(type, 1)):
+ *     decode, dense (launch_q8 / _pair / _multi / _multi_t, and _batch below the GEMM threshold): the dot of scale
+ *       group g of launch row r (the rows of Ws[0], then Ws[1], ...) for token t at out[(t * Nrows + r) * (K / G) + g];
+ *     decode, expert-indexed (_id / _id_pair / _id_x / _id_swiglu): matrix m's row r for output row o (t * n_used +
+ *       slot) at out[((m * T * n_used + o) * N + r) * (K / G) + g]; the expert-tiled launch in decode order: output
+ *       row o = out_rows[..] and m = 0;
+ *     GEMM (_batch at the GEMM threshold, _id_batch): the exact integer the epilogue scales (K-quants: a 256-value
+ *       super-block's sum of sub-block scale times dot) of token t (dense) or output row o (expert tiles) and row r
+ *       at out[(t * N + r) * (K / U) + unit]; U = 0: that GEMM has no integer sums and writes nothing.
+ *   A launch whose capture would not fit n_ints returns hipErrorInvalidValue (tiles mode: the caller sizes out for
+ *   the largest output row). G is the values one weight scale covers (16 for ROCmFP4, NVFP4, Q6_K; else 32), the
+ *   dots are of the raw levels (Q4_K 0..15, Q5_K 0..31, Q6_K 0..63, IQ4_XS the table levels).
+ * qmatvec_debug_decode_path(mode): 1 = the tile kernels where they take the shape (the default; PURHIE_MV_TILE=0 in
+ *   the environment at load makes it 0), 0 = the per-wave kernels only, other values only query; returns the
+ *   previous mode. */
+hipError_t qmatvec_debug_capture(int32_t *out, size_t n_ints);
+int qmatvec_debug_capture_unit(int type, int gemm);
+int qmatvec_debug_decode_path(int mode);
+
+/* No counterpart in the reference: a test hook, an independent scalar kernel. The integer dot of every weight
  * scale group (Q8_0 / FAST / MXFP4 / Q4_K / Q5_K / IQ4_XS: 32 values, ROCmFP4 / NVFP4 / Q6_K: 16) of every row
  * against the quantized activation, computed by the same device decoders as the matvec kernels: out[N][K / group].
  * Q4_K / Q5_K / Q6_K dot the raw levels (0..15 / 0..31 / 0..63), IQ4_XS the table levels (-127..113). */

@@ -1078,6 +1078,45 @@ int orc_block_dots(int t, const void *W, size_t rb, int N, int K, const int8_t *
     return 0;
 }
 
+/* The exact integer a K-quant super-block contributes before its float scales (per row n and super-block u,
+ * out[n * K / 256 + u]), against the Q8_K activation qK (bsK its 16-value sums):
+ *   Q4_K, Q5_K  isum = sum_j sc_j dot_j over the 8 sub-blocks (raw levels)   src/matvec_q.hip:1752-1789
+ *   Q6_K        isum = sum_g sc_g (dot_g - 32 bs_g) over the 16 groups       src/matvec_q.hip:1716-1750
+ *   IQ4_XS      isum = sum_j (ls_j - 32) dot_j (table levels)                src/matvec_q.hip:1788-1810
+ * (the reference forms these per lane and adds the lanes' floats; the sum over a super-block is the integer the
+ * GEMM's epilogue scales by d dx) */
+int orc_unit_isum(int t, const void *W, size_t rb, int N, int K, const int8_t *qK, const int32_t *bsK, int32_t *out) {
+    if (t != ORC_Q4_K && t != ORC_Q5_K && t != ORC_Q6_K && t != ORC_IQ4_XS) return -1;
+    if (K % 256) return -1;
+    const int nu = K / 256, BY = t == ORC_Q4_K ? 144 : t == ORC_Q5_K ? 176 : t == ORC_Q6_K ? 210 : 136;
+    for (int n = 0; n < N; ++n) {
+        const uint8_t *row = (const uint8_t *)W + (size_t)n * rb;
+        for (int u = 0; u < nu; ++u) {
+            const uint8_t *b = row + (size_t)BY * u;
+            const int8_t *xb = qK + 256 * u;
+            int isum = 0;
+            if (t == ORC_Q6_K) {
+                const int8_t *sc = (const int8_t *)(b + 192);
+                for (int g = 0; g < 16; ++g) {
+                    int dot = 0;
+                    for (int i = 0; i < 16; ++i) dot += k6_level(b, 16 * g + i) * xb[16 * g + i];
+                    isum += sc[g] * (dot - 32 * bsK[16 * u + g]);
+                }
+            } else {
+                for (int j = 0; j < 8; ++j) {
+                    int dot = 0, sc, mn;
+                    for (int i = 0; i < 32; ++i) dot += raw_level(t, row, 256 * u + 32 * j + i) * xb[32 * j + i];
+                    if (t == ORC_IQ4_XS) sc = iq4xs_scale(b, j);
+                    else k4_scale_min(j, b + 4, &sc, &mn);
+                    isum += sc * dot;
+                }
+            }
+            out[(size_t)n * nu + u] = isum;
+        }
+    }
+    return 0;
+}
+
 /* ================================================================ matvec */
 
 /* one row's result in the int8 kernels' per-block form, summed in block order:

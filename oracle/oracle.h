@@ -75,6 +75,8 @@ void orc_quantize_q8_k(const float *x, int64_t k, int8_t *qK, float *dK, int32_t
  * Q6_K 16. Q4_K / Q6_K dot the raw levels (0..15 / 0..63) before any offset. out[N][K / group]. */
 int orc_group_size(int type);
 int orc_block_dots(int type, const void *W, size_t row_bytes, int N, int K, const int8_t *qx, int32_t *out);
+/* the exact integer of each K-quant super-block before its float scales (see oracle.c) */
+int orc_unit_isum(int t, const void *W, size_t rb, int N, int K, const int8_t *qK, const int32_t *bsK, int32_t *out);
 
 /* ---- matvec y[N] = W x_q with the activation's quantized form (q0/d0 for Q8_0-activation types,
  * qK/dK/bsK for K-quants). The float order is the reference CPU path's (sequential over blocks,

@@ -62,6 +62,7 @@ def lib():
         L.orc_quantize_q8_0.argtypes = [vp, i64, vp, vp, vp]
         L.orc_quantize_q8_k.argtypes = [vp, i64, vp, vp, vp]
         L.orc_block_dots.argtypes = [i32, vp, sz, i32, i32, vp, vp]
+        L.orc_unit_isum.argtypes = [i32, vp, sz, i32, i32, vp, vp, vp]
         L.orc_matvec.argtypes = [i32, vp, sz, i32, i32, vp, vp, vp, vp, vp, vp, i32]
         L.orc_cpu_q8_0_quantize.argtypes = [vp, i32, vp, vp]
         L.orc_cpu_matvec_fp4fast_q8.argtypes = [vp, sz, i32, i32, vp, vp, vp]
@@ -137,6 +138,16 @@ def block_dots(t, W, N, K, q):
     q = np.ascontiguousarray(q, dtype=np.int8)
     out = np.zeros((N, K // GROUP[t]), dtype=np.int32)
     assert lib().orc_block_dots(t, _ptr(W), row_size(t, K), N, K, _ptr(q), _ptr(out)) == 0
+    return out
+
+
+def unit_isum(t, W, N, K, qK, bsK):
+    """K-quants: the exact integer of each 256-value super-block before its float scales, [N][K / 256]"""
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    qK = np.ascontiguousarray(qK, dtype=np.int8)
+    bsK = np.ascontiguousarray(bsK, dtype=np.int32)
+    out = np.zeros((N, K // 256), dtype=np.int32)
+    assert lib().orc_unit_isum(t, _ptr(W), row_size(t, K), N, K, _ptr(qK), _ptr(bsK), _ptr(out)) == 0
     return out
 
 
@@ -261,8 +272,20 @@ def ref():
         getattr(R, "_Z16cpu_matvec_q8_q8PKvmiiPKaPKfPf").argtypes = [vp, sz, i32, i32, vp, vp, vp]
         getattr(R, "_Z14cpu_expert_ffnPKvS0_mS0_miiPKaPKffPfS5_").argtypes = [vp, vp, sz, vp, sz, i32, i32, vp, vp,
                                                                            C.c_float, vp, vp]
+        R.refb_have_vnni.restype = i32
+        R.refb_matvec.restype = C.c_double
+        R.refb_matvec.argtypes = [i32, vp, sz, i32, i32, i32, vp, vp, vp, i32, i32, i32]
         _ref = R
     return _ref
+
+
+def ref_time_matvec(t, W, N, K, copies, q, d, threads, reps, chunk):
+    """seconds for `reps` passes of the reference's cpu_matvec_q8_q8 (t 8) or cpu_matvec_fp4fast_q8 (t 101) over
+    rotating copies (W holds `copies` matrices back to back), rows split in chunks over `threads` std::threads, or
+    over the reference's own pool (threads 0); see ref_bench.cpp"""
+    y = np.zeros(N, dtype=np.float32)
+    return ref().refb_matvec(t, _ptr(W), row_size(t, K), N, K, copies, _ptr(q), _ptr(d), _ptr(y), threads, reps,
+                             chunk)
 
 
 def ref_quantize(t, x, n_threads=1):

@@ -155,6 +155,19 @@ struct DenseRows {
     }
 };
 
+// Capture of the integer dots (the test hook of capture mode): put(t, g, v) adds the dot v of scale group g (of
+// the lane's unit, or of its row) for token t. NoCap is the production kernels': it compiles to nothing.
+struct NoCap {
+    __device__ void put(int, int, int) const {}
+};
+struct DotCap {
+    int32_t *p;    // token 0's group 0 (null: this lane captures nothing)
+    long long ts;  // per token
+    __device__ void put(int t, int g, int v) const {
+        if (p) atomicAdd(p + t * ts + g, v);
+    }
+};
+
 // Rows of one (matrix, slot, token) of an expert-indexed launch
 struct IdRows {
     const uint8_t *W;

@@ -284,7 +284,7 @@ struct KStage<TY_Q6_K> {
 
 // ---------------------------------------------------------------- the GEMM
 // wave w computes rows 64 (w & 1) .. + 63 x tokens 64 (w >> 1) .. + 63 (4 x 4 MFMA tiles)
-template <int TYPE>
+template <int TYPE, bool CAP = false>
 __global__ void __launch_bounds__(GK_THREADS, 2) k_gemm_kq(GemmArgs a) {
     using S = KStage<TYPE>;
     constexpr bool MINS = TYPE == TY_Q4_K || TYPE == TY_Q5_K;
@@ -388,6 +388,23 @@ __global__ void __launch_bounds__(GK_THREADS, 2) k_gemm_kq(GemmArgs a) {
                 __builtin_amdgcn_sched_barrier(0);  // (keeps the next block's fragment reads from being hoisted here)
             }
         }
+        if constexpr (CAP) {  // capture mode: the exact integer isum of each (token, row) for this super-block
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int tt = wt + 16 * j + (lane & 15);
+                long long t;
+                if (orow) t = tt < tm.n ? orow[tt] : -1;
+                else t = tm.base + tt < a.T ? tm.base + tt : -1;
+                if (t < 0) continue;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int n = n0 + wn + 16 * i + 4 * (lane >> 4) + r;
+                        if (n < a.N) a.cap[(t * a.N + n) * nsb + s] = (int32_t)isum[i][j][r];
+                    }
+            }
+        }
         // super-block epilogue: y += dK (d isum - dmin msum), the sums restart at zero
         float dk[4];
         h4 fs[4], fm[4];
@@ -444,6 +461,8 @@ __global__ void __launch_bounds__(GK_THREADS, 2) k_gemm_kq(GemmArgs a) {
 
 // ---------------------------------------------------------------- host launchers
 
+int gemm_cap_unit(int type) { return gemm_kquant(type) ? 256 : 0; }
+
 bool gemm_kquant(int type) { return type == TY_Q4_K || type == TY_Q5_K || type == TY_Q6_K || type == TY_IQ4_XS; }
 
 hipError_t launch_act_q8k(const int8_t *q, const float *dK, const int32_t *bs, int T, int K, int rows, _Float16 *xh,
@@ -452,12 +471,18 @@ hipError_t launch_act_q8k(const int8_t *q, const float *dK, const int32_t *bs, i
     return hipGetLastError();
 }
 
+template <int TYPE>
+static void launch_kq(const GemmArgs &a, dim3 grid, hipStream_t stream) {
+    if (a.cap) hipLaunchKernelGGL((k_gemm_kq<TYPE, true>), grid, dim3(GK_THREADS), 0, stream, a);
+    else hipLaunchKernelGGL((k_gemm_kq<TYPE>), grid, dim3(GK_THREADS), 0, stream, a);
+}
+
 hipError_t launch_gemm_kquant(int type, const GemmArgs &a, dim3 grid, hipStream_t stream) {
     switch (type) {
-    case TY_Q4_K: hipLaunchKernelGGL(k_gemm_kq<TY_Q4_K>, grid, dim3(GK_THREADS), 0, stream, a); break;
-    case TY_Q5_K: hipLaunchKernelGGL(k_gemm_kq<TY_Q5_K>, grid, dim3(GK_THREADS), 0, stream, a); break;
-    case TY_IQ4_XS: hipLaunchKernelGGL(k_gemm_kq<TY_IQ4_XS>, grid, dim3(GK_THREADS), 0, stream, a); break;
-    case TY_Q6_K: hipLaunchKernelGGL(k_gemm_kq<TY_Q6_K>, grid, dim3(GK_THREADS), 0, stream, a); break;
+    case TY_Q4_K: launch_kq<TY_Q4_K>(a, grid, stream); break;
+    case TY_Q5_K: launch_kq<TY_Q5_K>(a, grid, stream); break;
+    case TY_IQ4_XS: launch_kq<TY_IQ4_XS>(a, grid, stream); break;
+    case TY_Q6_K: launch_kq<TY_Q6_K>(a, grid, stream); break;
     default: return hipErrorInvalidDeviceFunction;
     }
     return hipGetLastError();

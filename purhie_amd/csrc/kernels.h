@@ -36,8 +36,13 @@ struct MvArgs {
     const float *d;      // its scales; token t at d + t * (K / act block)
     const int32_t *bs;   // Q8_K group sums (K-quants); token t at bs + t * (K / 16)
     int Nt, K, L, T;
+    int32_t *cap;        // capture mode (null: off): every scale group's integer dot is added into
+                         // cap[(t * Nt + row) * (K / G) + group] (G = cap_group(type)); the buffer starts at zero
 };
 hipError_t launch_matvec(int type, const MvArgs &a, hipStream_t stream);
+
+// the values one weight scale covers (the capture's group): 16 for ROCmFP4, NVFP4 and Q6_K, else 32
+constexpr int cap_group(int type) { return type == 100 || type == 40 || type == 14 ? 16 : 32; }
 
 // MoE expert-indexed matvec (decode): grid (row groups, n_used * nmat, T)
 struct MvIdArgs {
@@ -59,6 +64,10 @@ struct MvIdArgs {
     // set: the input rows are SwiGLU(sw_g, sw_u) (row in_row of each, K floats), quantized to Q8_0 in the kernel
     // (q / d unused; the tile kernel of a Q8_0-activation type only)
     const float *sw_g, *sw_u;
+    // capture mode (null: off): the dots of entry (matrix m, output row o) go to
+    // cap[((m * cap_rows + o) * N + row) * (K / G) + group] (cap_rows: T * n_used, or 0 in tiles mode)
+    int32_t *cap;
+    long long cap_rows;
 };
 hipError_t launch_matvec_id(int type, const MvIdArgs &a, hipStream_t stream);
 bool matvec_id_swiglu_supported(int type, int K);
@@ -91,9 +100,14 @@ struct GemmArgs {
     const int32_t *n_tiles, *tile_e, *tile_start, *tile_n, *in_rows, *out_rows;
     const float *es;        // per-expert output scales (null: osc)
     int tt;                 // split GEMM, dense: tokens per workgroup (128, or 64 for short prompts)
+    // capture mode (null: off; the integer-exact GEMMs): the exact integer each epilogue scales, per token (dense:
+    // t; tiles: the entry's output row) and weight row: cap[(t * N + row) * (K / U) + unit], U = gemm_cap_unit(type)
+    int32_t *cap;
 };
 
 int gemm_supported(int type);
+// values per integer the type's GEMM exposes in capture mode (0: its sums are not integers, none captured)
+int gemm_cap_unit(int type);
 int gemm_k_multiple();
 int gemm_token_tile();
 int gemm_id_token_tile(int type);  // the largest MoE expert tile the type's GEMM takes
@@ -126,5 +140,15 @@ hipError_t launch_gemm_kquant(int type, const GemmArgs &a, dim3 grid, hipStream_
 
 // lanes per row the decode kernels use for a matrix of K columns and `rows` rows in total
 int matvec_lanes(int type, int K, long long rows);
+
+// Decode tuning, read from the environment once per process: PURHIE_MV_TILE=0 sends every shape to the per-wave
+// kernels (tile 0; qmatvec_debug_decode_path changes it at run time), PURHIE_MV_THREADS fixes the tile kernel's
+// workgroup size (64 / 128 / 256, else 0 = chosen per launch), PURHIE_MV_LANES the per-wave kernels' lanes per row
+// (8 .. 64, a power of two, else 0 = chosen per shape)
+struct MvTune {
+    int tile, threads, lanes;
+};
+const MvTune &mv_tune();
+void mv_tune_set_tile(int on);
 
 }  // namespace pq

@@ -65,9 +65,9 @@ struct Mv<TY_Q8_0> {
 #pragma unroll
         for (int k = 0; k < 17; ++k) r.w[k] = ld32_nt(p + 4 * k);
     }
-    template <int NT>
+    template <int NT, class Cap>
     __device__ static void compute(const Raw &r, const Lane &, const Act<NT> &x, int xo, int dof, int, float acc[NT],
-                                   bool v) {
+                                   bool v, const Cap &cap) {
         uint32_t qa[8], qb[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -95,6 +95,10 @@ struct Mv<TY_Q8_0> {
             s1 = dot4((int)qb[5], x3.y, s1);
             s1 = dot4((int)qb[6], x3.z, s1);
             s1 = dot4((int)qb[7], x3.w, s1);
+            if (v) {
+                cap.put(t, xo / 32, s0);
+                cap.put(t, xo / 32 + 1, s1);
+            }
             const float2 dx = *(const float2 *)(x.d[t] + dof);
             acc[t] = __builtin_fmaf(v ? e0 * dx.x : 0.0f, (float)s0, acc[t]);
             acc[t] = __builtin_fmaf(v ? e1 * dx.y : 0.0f, (float)s1, acc[t]);
@@ -149,9 +153,9 @@ struct Mv<TY_FP4> {
 #pragma unroll
         for (int k = 0; k < 9; ++k) r.w[k] = ld32_nt(p + 4 * k);
     }
-    template <int NT>
+    template <int NT, class Cap>
     __device__ static void compute(const Raw &r, const Lane &, const Act<NT> &x, int xo, int dof, int, float acc[NT],
-                                   bool v) {
+                                   bool v, const Cap &cap) {
         const uint32_t qa[4] = {r.w[0], r.w[1], r.w[2], r.w[3]};
         uint32_t qb[4];
 #pragma unroll
@@ -164,6 +168,12 @@ struct Mv<TY_FP4> {
             int a0, a1, b0, b1;
             fp4_block_dots(qa, xv[0], xv[1], a0, a1);
             fp4_block_dots(qb, xv[2], xv[3], b0, b1);
+            if (v) {
+                cap.put(t, xo / 16, a0);
+                cap.put(t, xo / 16 + 1, a1);
+                cap.put(t, xo / 16 + 2, b0);
+                cap.put(t, xo / 16 + 3, b1);
+            }
             const float2 dl = *(const float2 *)(x.d[t] + dof);
             const float2 dx = v ? dl : make_float2(0.0f, 0.0f);  // (UE4M3 scales are finite: 0 x e = 0)
             const float ta = __builtin_fmaf(ea1 * dx.x, (float)a1, ea0 * dx.x * (float)a0);
@@ -201,9 +211,9 @@ struct Mv<TY_FAST> {
     __device__ static __forceinline__ uint32_t dw(const uint32_t *w, int off) {  // off compile-time
         return (off & 3) == 0 ? w[off >> 2] : align_bytes(w[(off >> 2) + 1], w[off >> 2], off & 3);
     }
-    template <int NT>
+    template <int NT, class Cap>
     __device__ static void compute(const Raw &r, const Lane &, const Act<NT> &x, int xo, int dof, int, float acc[NT],
-                                   bool v) {
+                                   bool v, const Cap &cap) {
         uint32_t w[18];
 #pragma unroll
         for (int k = 0; k < 17; ++k) w[k] = r.w[k];
@@ -219,6 +229,7 @@ struct Mv<TY_FAST> {
                 const int4 *xv = (const int4 *)(x.q[t] + xo + 32 * j);
                 int s0, s1;
                 fp4_block_dots(qs, xv[0], xv[1], s0, s1);
+                if (v) cap.put(t, xo / 32 + j, s0 + s1);
                 acc[t] = __builtin_fmaf(v ? e * x.d[t][dof + j] : 0.0f, (float)(s0 + s1), acc[t]);
             }
         }
@@ -229,9 +240,9 @@ struct Mv<TY_FAST> {
 // scale at byte 17 j, its 16 value bytes from 17 j + 1. Per block the reference's term (e dx) (s0 + s1).
 template <>
 struct Mv<TY_MXFP4> : Mv<TY_FAST> {
-    template <int NT>
+    template <int NT, class Cap>
     __device__ static void compute(const Raw &r, const Lane &, const Act<NT> &x, int xo, int dof, int, float acc[NT],
-                                   bool v) {
+                                   bool v, const Cap &cap) {
         uint32_t w[18];
 #pragma unroll
         for (int k = 0; k < 17; ++k) w[k] = r.w[k];
@@ -247,6 +258,7 @@ struct Mv<TY_MXFP4> : Mv<TY_FAST> {
                 const int4 *xv = (const int4 *)(x.q[t] + xo + 32 * j);
                 int s0, s1;
                 fp4_block_dots<12>(qs, xv[0], xv[1], s0, s1);
+                if (v) cap.put(t, xo / 32 + j, s0 + s1);
                 acc[t] = __builtin_fmaf(v ? e * x.d[t][dof + j] : 0.0f, (float)(s0 + s1), acc[t]);
             }
         }
@@ -258,9 +270,9 @@ struct Mv<TY_MXFP4> : Mv<TY_FAST> {
 // (dx e0) s0 + (dx e1) s1 each.
 template <>
 struct Mv<TY_NVFP4> : Mv<TY_FP4> {
-    template <int NT>
+    template <int NT, class Cap>
     __device__ static void compute(const Raw &r, const Lane &, const Act<NT> &x, int xo, int dof, int, float acc[NT],
-                                   bool v) {
+                                   bool v, const Cap &cap) {
         float e[4];
 #pragma unroll
         for (int s = 0; s < 4; ++s) e[s] = nv_scale(r.w[0] >> (8 * s));
@@ -273,6 +285,10 @@ struct Mv<TY_NVFP4> : Mv<TY_FP4> {
             for (int h = 0; h < 2; ++h) {
                 const int s0 = nv_sub_dot(r.w[1 + 4 * h], r.w[2 + 4 * h], xv[2 * h]);
                 const int s1 = nv_sub_dot(r.w[3 + 4 * h], r.w[4 + 4 * h], xv[2 * h + 1]);
+                if (v) {
+                    cap.put(t, xo / 16 + 2 * h, s0);
+                    cap.put(t, xo / 16 + 2 * h + 1, s1);
+                }
                 const float d = h ? dx.y : dx.x;
                 acc[t] += __builtin_fmaf(e[2 * h + 1] * d, (float)s1, e[2 * h] * d * (float)s0);
             }
@@ -343,9 +359,9 @@ struct MvKq {
         r.qs = ld128_nt(p + (Q5 ? 48 : 16) + 16 * s);
         if (Q5) r.qh = ld128_nt(p + 16 + 16 * (s & 1));
     }
-    template <int NT>
+    template <int NT, class Cap>
     __device__ static void compute(const Raw &r, const Lane &o, const Act<NT> &x, int xo, int dof, int bo,
-                                   float acc[NT], bool v) {
+                                   float acc[NT], bool v, const Cap &cap) {
         const uint32_t sc2 = (__builtin_amdgcn_perm(r.h.w, r.h.y, o.p) & o.pmask) |
                              (((__builtin_amdgcn_perm(r.h.w, r.h.y, o.q) >> 6) & 0x0303u) << 4);
         const int sc_lo = (int)(sc2 & 0xffu), sc_hi = (int)(sc2 >> 8);
@@ -377,6 +393,10 @@ struct MvKq {
             shi = dot4(hi[1], xh.y, shi);
             shi = dot4(hi[2], xh.z, shi);
             shi = dot4(hi[3], xh.w, shi);
+            if (v) {  // (16 values of sub-block 2c and of 2c + 1: the other lane of the chunk adds the rest)
+                cap.put(t, xo / 32, slo);
+                cap.put(t, xo / 32 + 1, shi);
+            }
             const int2 b2 = *(const int2 *)(x.bs[t] + bo);
             const int isum = mul24(sc_lo, slo) + mul24(sc_hi, shi);
             const int msum = mul24(mn, b2.x + b2.y);
@@ -416,9 +436,9 @@ struct Mv<TY_IQ4_XS> {
 #pragma unroll
         for (int k = 0; k < 4; ++k) r.q[k] = ld32_nt(p + 8 + 16 * s + 4 * k);
     }
-    template <int NT>
+    template <int NT, class Cap>
     __device__ static void compute(const Raw &r, const Lane &o, const Act<NT> &x, int xo, int dof, int, float acc[NT],
-                                   bool v) {
+                                   bool v, const Cap &cap) {
         int lo[4], hi[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -439,6 +459,7 @@ struct Mv<TY_IQ4_XS> {
             s = dot4(hi[1], xh.y, s);
             s = dot4(hi[2], xh.z, s);
             s = dot4(hi[3], xh.w, s);
+            if (v) cap.put(t, xo / 32, s);
             acc[t] = __builtin_fmaf(v ? dw * x.d[t][dof] : 0.0f, (float)(ls * s), acc[t]);
         }
     }
@@ -496,9 +517,9 @@ struct Mv<TY_Q6_K> {
         r.scp = *(const uint16_t *)(b + 192 + 2 * o.s);
         r.d = *(const uint16_t *)(b + 208);
     }
-    template <int NT>
+    template <int NT, class Cap>
     __device__ static void compute(const Raw &r, const Lane &o, const Act<NT> &x, int xo, int dof, int bo,
-                                   float acc[NT], bool v) {
+                                   float acc[NT], bool v, const Cap &cap) {
         int vlo[4], vhi[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -521,6 +542,10 @@ struct Mv<TY_Q6_K> {
             shi = dot4(vhi[1], xh.y, shi);
             shi = dot4(vhi[2], xh.z, shi);
             shi = dot4(vhi[3], xh.w, shi);
+            if (v) {
+                cap.put(t, xo / 16, slo);
+                cap.put(t, xo / 16 + 4, shi);
+            }
             const int2 b2 = *(const int2 *)(x.bs[t] + bo);
             int isum = mul24(r.sc_lo, slo) + mul24(r.sc_hi, shi);
             isum -= 32 * (mul24(sca, b2.x) + mul24(scb, b2.y));
@@ -541,8 +566,9 @@ __device__ __forceinline__ void load_task(const uint8_t *p, typename Mv<TYPE>::R
 
 // the row's partial sum of this lane: tasks gl, gl + L, ... of the row at wr, MV_U at a time, every load of
 // a batch issued before its arithmetic
-template <int TYPE, int NT, int L>
-__device__ __forceinline__ void row_sum(const uint8_t *wr, int K, int gl, const Act<NT> &x0, float acc[NT]) {
+template <int TYPE, int NT, int L, class Cap>
+__device__ __forceinline__ void row_sum(const uint8_t *wr, int K, int gl, const Act<NT> &x0, float acc[NT],
+                                        const Cap &cap) {
     using P = Mv<TYPE>;
     constexpr int SL = L / P::LDIV;  // units of the lane's task stride
     constexpr int WS = P::W_UNIT * SL, XS = P::X_UNIT * SL, DS = P::D_UNIT * SL, BS = P::B_UNIT * SL;
@@ -560,7 +586,8 @@ __device__ __forceinline__ void row_sum(const uint8_t *wr, int K, int gl, const 
             if (u0 + u < nu) load_task<TYPE>(wp + u * WS, raw[u], o, gl);
 #pragma unroll
         for (int u = 0; u < MV_U; ++u)
-            if (u0 + u < nu) P::template compute<NT>(raw[u], o, x0, xo + u * XS, dof + u * DS, bo + u * BS, acc, true);
+            if (u0 + u < nu)
+                P::template compute<NT>(raw[u], o, x0, xo + u * XS, dof + u * DS, bo + u * BS, acc, true, cap);
         wp += MV_U * WS;
         xo += MV_U * XS;
         dof += MV_U * DS;
@@ -587,7 +614,7 @@ __device__ __forceinline__ void act_view(const int8_t *q, const float *d, const 
 // ---------------------------------------------------------------- long rows (more than MV_U tasks a lane)
 // one row group per wave, the activation read through the caches
 
-template <int TYPE, int NT, int L>
+template <int TYPE, int NT, int L, bool CAP = false>
 __global__ void __launch_bounds__(MV_THREADS) k_matvec(MvArgs a) {
     const int lane = threadIdx.x & 63, gl = lane & (L - 1);
     const int row = (blockIdx.x * (MV_THREADS / 64) + (threadIdx.x >> 6)) * (64 / L) + lane / L;
@@ -598,7 +625,12 @@ __global__ void __launch_bounds__(MV_THREADS) k_matvec(MvArgs a) {
     Act<NT> x;
     act_view<TYPE, NT>(a.q, a.d, a.bs, a.K, x);
     float acc[NT];
-    row_sum<TYPE, NT, L>(wr, a.K, gl, x, acc);
+    if constexpr (CAP) {
+        const int ng = a.K / cap_group(TYPE);
+        row_sum<TYPE, NT, L>(wr, a.K, gl, x, acc, DotCap{a.cap + (long long)row * ng, (long long)a.Nt * ng});
+    } else {
+        row_sum<TYPE, NT, L>(wr, a.K, gl, x, acc, NoCap{});
+    }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const float v = group_sum(acc[t], L);
@@ -609,7 +641,7 @@ __global__ void __launch_bounds__(MV_THREADS) k_matvec(MvArgs a) {
 // ---------------------------------------------------------------- MoE expert-indexed kernel
 // grid (row groups, n_used * nmat, T): slot j of token t uses expert ids[t * n_used + j] (-1: Wx)
 
-template <int TYPE, int L>
+template <int TYPE, int L, bool CAP = false>
 __global__ void __launch_bounds__(MV_THREADS) k_matvec_id(MvIdArgs a) {
     const int lane = threadIdx.x & 63, gl = lane & (L - 1);
     const int row = (blockIdx.x * (MV_THREADS / 64) + (threadIdx.x >> 6)) * (64 / L) + lane / L;
@@ -623,7 +655,13 @@ __global__ void __launch_bounds__(MV_THREADS) k_matvec_id(MvIdArgs a) {
     Act<1> x;
     act_view<TYPE, 1>(a.q + in_row * K, a.d + in_row * kb, a.bs ? a.bs + in_row * (K / 16) : nullptr, K, x);
     float acc[1];
-    row_sum<TYPE, 1, L>(wr, K, gl, x, acc);
+    if constexpr (CAP) {
+        const int ng = K / cap_group(TYPE);
+        row_sum<TYPE, 1, L>(wr, K, gl, x, acc,
+                            DotCap{a.cap + (((long long)m * a.cap_rows + en.out_row) * a.N + row) * ng, 0});
+    } else {
+        row_sum<TYPE, 1, L>(wr, K, gl, x, acc, NoCap{});
+    }
     const float v = group_sum(acc[0], L);
     const float sc = e < 0 ? a.sx[m] : a.es[m] ? a.es[m][e] : a.s[m];
     if (gl == 0) a.y[m][en.out_row * a.N + row] = v * sc;
@@ -710,24 +748,39 @@ int matvec_lanes(int type, int K, long long rows) {
     int L = 8;
     while (L < 64 && (nt + L - 1) / L > U) L <<= 1;
     (void)rows;
-    if (const char *e = getenv("PURHIE_MV_LANES")) {
-        const int v = atoi(e);
-        if (v >= 8 && v <= 64 && (v & (v - 1)) == 0) L = v;
-    }
+    if (mv_tune().lanes) L = mv_tune().lanes;
     return L;
 }
 
-// PURHIE_MV_TILE=0 sends every shape to the per-wave kernels (a tuning and test knob, read per launch)
-static bool tile_enabled() {
-    const char *e = getenv("PURHIE_MV_TILE");
-    return !(e && e[0] == '0');
+namespace {
+MvTune tune_from_env() {
+    MvTune t{1, 0, 0};
+    if (const char *e = getenv("PURHIE_MV_TILE")) t.tile = e[0] == '0' ? 0 : 1;
+    if (const char *e = getenv("PURHIE_MV_THREADS")) {
+        const int v = atoi(e);
+        t.threads = v == 64 || v == 128 || v == 256 ? v : 0;
+    }
+    if (const char *e = getenv("PURHIE_MV_LANES")) {
+        const int v = atoi(e);
+        t.lanes = v >= 8 && v <= 64 && (v & (v - 1)) == 0 ? v : 0;
+    }
+    return t;
 }
+MvTune g_tune = tune_from_env();  // (static initialisation: before any launch)
+}  // namespace
+
+const MvTune &mv_tune() { return g_tune; }
+void mv_tune_set_tile(int on) { __atomic_store_n(&g_tune.tile, on ? 1 : 0, __ATOMIC_RELAXED); }
+
+// the tile kernels where they take the shape, unless PURHIE_MV_TILE=0 or the test hook switched them off
+static bool tile_enabled() { return __atomic_load_n(&g_tune.tile, __ATOMIC_RELAXED) != 0; }
 
 template <int TYPE, int NT, int L>
 static hipError_t launch_tl(const MvArgs &a, hipStream_t stream) {
     const int rows_per_wg = (MV_THREADS / 64) * (64 / L);
     const unsigned grid = (unsigned)((a.Nt + rows_per_wg - 1) / rows_per_wg);
-    hipLaunchKernelGGL((k_matvec<TYPE, NT, L>), dim3(grid), dim3(MV_THREADS), 0, stream, a);
+    if (a.cap) hipLaunchKernelGGL((k_matvec<TYPE, NT, L, true>), dim3(grid), dim3(MV_THREADS), 0, stream, a);
+    else hipLaunchKernelGGL((k_matvec<TYPE, NT, L>), dim3(grid), dim3(MV_THREADS), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -778,7 +831,8 @@ static hipError_t launch_id_tl(const MvIdArgs &a, hipStream_t stream) {
     const unsigned gx = (unsigned)((a.N + rows_per_wg - 1) / rows_per_wg);
     const dim3 grid = a.n_tiles ? dim3(gx, (unsigned)a.tile, (unsigned)a.max_tiles)
                                 : dim3(gx, (unsigned)(a.n_used * a.nmat), (unsigned)a.T);
-    hipLaunchKernelGGL((k_matvec_id<TYPE, L>), grid, dim3(MV_THREADS), 0, stream, a);
+    if (a.cap) hipLaunchKernelGGL((k_matvec_id<TYPE, L, true>), grid, dim3(MV_THREADS), 0, stream, a);
+    else hipLaunchKernelGGL((k_matvec_id<TYPE, L>), grid, dim3(MV_THREADS), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -149,15 +149,21 @@ hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qm
     const float *sg = sh && w->shexp_gate ? L.sg : nullptr;
 
     // the expert down matvec reads SwiGLU(g, u) quantized in its own kernel where the type allows (the same bits
-    // as gpu_swiglu's quantization and the plain launch: one launch fewer)
-    const bool fuse = !L.grouped && qmatvec_q8_id_swiglu_supported(w->type_down, FE);
+    // as gpu_swiglu's quantization and the plain launch: one launch fewer). The fused launch also needs the tile
+    // kernel's alignment (matrices 16-byte aligned); where it refuses a shape (hipErrorInvalidDeviceFunction,
+    // before anything runs) the two launches below run instead.
+    bool fuse = !L.grouped && qmatvec_q8_id_swiglu_supported(w->type_down, FE);
+    auto fused = [&](const void *Wx, float *dst, int ns, int Tn) -> hipError_t {
+        const hipError_t r = qmatvec_launch_q8_id_swiglu(w->type_down, w->down_exps, Wx, w->rb_down, L.ids, ns, L.g,
+                                                         L.u, dst, E, FE, Tn, stream);
+        if (r == hipErrorInvalidDeviceFunction) fuse = false;
+        return r == hipErrorInvalidDeviceFunction ? hipSuccess : r;
+    };
     if (L.slot) {  // src/qwen_model.cpp:1105-1134: one token, the shared expert as slot NU (id -1)
         PQ_TRY(qmatvec_launch_q8_id_x(w->type_gate_up, w->gate_exps, w->up_exps, w->gate_shexp, w->up_shexp,
                                       w->rb_gate_up, L.ids, L.ns, 0, q8_xn, L.g, L.u, FE, E, 1, stream));
-        if (fuse) {
-            PQ_TRY(qmatvec_launch_q8_id_swiglu(w->type_down, w->down_exps, w->down_shexp, w->rb_down, L.ids, L.ns, L.g,
-                                               L.u, L.down, E, FE, 1, stream));
-        } else {
+        if (fuse) PQ_TRY(fused(w->down_shexp, L.down, L.ns, 1));
+        if (!fuse) {
             PQ_TRY(gpu_swiglu(L.g, L.u, L.act, L.ns * FE, &qx, stream));
             PQ_TRY(qmatvec_launch_q8_id_x(w->type_down, w->down_exps, nullptr, w->down_shexp, nullptr, w->rb_down,
                                           L.ids, L.ns, 1, &qx, L.down, nullptr, E, FE, 1, stream));
@@ -183,10 +189,8 @@ hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qm
         PQ_TRY(qmatvec_launch_q8_batch(w->type_shexp_gate_up, w->up_shexp, w->rb_shexp_gate_up, q8_xn, L.ffu, FS, FS,
                                        E, T, stream));
     }
-    if (fuse) {
-        PQ_TRY(qmatvec_launch_q8_id_swiglu(w->type_down, w->down_exps, nullptr, w->rb_down, L.ids, NU, L.g, L.u, L.down,
-                                           E, FE, T, stream));
-    } else {
+    if (fuse) PQ_TRY(fused(nullptr, L.down, NU, T));
+    if (!fuse) {
         PQ_TRY(gpu_swiglu(L.g, L.u, L.act, T * NU * FE, &qx, stream));
         if (L.grouped)
             PQ_TRY(qmatvec_launch_q8_id_batch(w->type_down, w->down_exps, w->rb_down, &qx, L.down, E, FE, L.max_tiles,

@@ -120,8 +120,8 @@ struct TuKq {
     static constexpr int QS = Q5 ? 12 : 4;  // first dword of qs
     static constexpr bool LUT = false;
     __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read16(p, w, aux); }
-    template <int NT>
-    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT]) {
+    template <int NT, class Cap>
+    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT], const Cap &cap) {
         const uint32_t y = w[1], z = w[2], v = w[3];
         const uint32_t sc[2] = {y & 0x3f3f3f3fu, (v & 0x0f0f0f0fu) | ((y >> 2) & 0x30303030u)};
         const uint32_t mn[2] = {z & 0x3f3f3f3fu, ((v >> 4) & 0x0f0f0f0fu) | ((z >> 2) & 0x30303030u)};
@@ -150,6 +150,8 @@ struct TuKq {
                 const int4 *xv = (const int4 *)(x.x + t * x.xt + 64 * c);
                 const int slo = dot8(lo, xv[0], xv[1]);
                 const int shi = dot8(hi, xv[2], xv[3]);
+                cap.put(t, 2 * c, slo);
+                cap.put(t, 2 * c + 1, shi);
                 isum[t] += __mul24(sa, slo) + __mul24(sb, shi);
             }
         }
@@ -191,8 +193,9 @@ struct Tu<TY_Q6_K> {
         for (int i = 0; i < NDW; ++i) w[i] = a[i];
         aux = (uint32_t)((uintptr_t)p & 3u);
     }
-    template <int NT>
-    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t off, const Lx &x, float (&acc)[NT]) {
+    template <int NT, class Cap>
+    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t off, const Lx &x, float (&acc)[NT],
+                                   const Cap &cap) {
         uint32_t v[NDW];
 #pragma unroll
         for (int i = 0; i < NDW; ++i) v[i] = align_bytes(i + 1 < NDW ? w[i + 1] : 0u, w[i], off);
@@ -221,6 +224,7 @@ struct Tu<TY_Q6_K> {
                     for (int t = 0; t < NT; ++t) {
                         const int4 xa = *(const int4 *)(x.x + t * x.xt + 128 * h + 32 * m + 16 * lc);
                         const int dg = dot4x(q[m], xa);
+                        cap.put(t, g, dg);
                         isum[t] += __mul24(sc, dg - 32 * x.s[t * x.ns + g]);
                     }
                 }
@@ -239,8 +243,8 @@ struct Tu<TY_Q8_0> {
     static constexpr int VALS = 128, BYTES = 136, NDW = 34, ACT = 32, SUMS = 0, LEAD = 8;
     static constexpr bool LUT = false;
     __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read8(p, w, aux); }
-    template <int NT>
-    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT]) {
+    template <int NT, class Cap>
+    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT], const Cap &cap) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
 #pragma unroll
@@ -254,6 +258,7 @@ struct Tu<TY_Q8_0> {
             for (int t = 0; t < NT; ++t) {
                 const int4 *xv = (const int4 *)(x.x + t * x.xt + 32 * b);
                 const int s = dot8(qs, xv[0], xv[1]);
+                cap.put(t, b, s);
                 acc[t] = __builtin_fmaf(e * x.d[t * x.nd + b], (float)s, acc[t]);
             }
         }
@@ -269,8 +274,8 @@ struct Tu<TY_FP4> {
     static constexpr bool LUT = true;
     __device__ static float scale(uint32_t e) { return ue4m3_half(e); }
     __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read16(p, w, aux); }
-    template <int NT>
-    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT]) {
+    template <int NT, class Cap>
+    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT], const Cap &cap) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
 #pragma unroll
@@ -288,6 +293,8 @@ struct Tu<TY_FP4> {
             for (int t = 0; t < NT; ++t) {
                 const int4 *xv = (const int4 *)(x.x + t * x.xt + 32 * b);
                 const int s0 = dot4x(lo, xv[0]), s1 = dot4x(hi, xv[1]);
+                cap.put(t, 2 * b, s0);
+                cap.put(t, 2 * b + 1, s1);
                 const float dx = x.d[t * x.nd + b];
                 acc[t] += __builtin_fmaf(e1 * dx, (float)s1, e0 * dx * (float)s0);
             }
@@ -304,8 +311,8 @@ struct Tu<TY_IQ4_XS> {
     static constexpr int VALS = 256, BYTES = 136, NDW = 34, ACT = 256, SUMS = 0, LEAD = 8;
     static constexpr bool LUT = false;
     __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read8(p, w, aux); }
-    template <int NT>
-    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT]) {
+    template <int NT, class Cap>
+    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT], const Cap &cap) {
         const uint32_t sh = w[0] >> 16, sl = w[1];
         int isum[NT];
 #pragma unroll
@@ -323,7 +330,9 @@ struct Tu<TY_IQ4_XS> {
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 const int4 *xv = (const int4 *)(x.x + t * x.xt + 32 * j);
-                isum[t] += ls * (dot4x(lo, xv[0]) + dot4x(hi, xv[1]));
+                const int dj = dot4x(lo, xv[0]) + dot4x(hi, xv[1]);
+                cap.put(t, j, dj);
+                isum[t] += ls * dj;
             }
         }
         const float dw = h2f(w[0] & 0xffffu);
@@ -340,8 +349,8 @@ struct Tu<TY_FAST> {
     static constexpr bool LUT = true;
     __device__ static float scale(uint32_t e) { return ue4m3_half(e); }
     __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read8(p, w, aux); }
-    template <int NT>
-    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT]) {
+    template <int NT, class Cap>
+    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT], const Cap &cap) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
 #pragma unroll
@@ -359,6 +368,7 @@ struct Tu<TY_FAST> {
             for (int t = 0; t < NT; ++t) {
                 const int4 *xv = (const int4 *)(x.x + t * x.xt + 32 * j);
                 const int s = dot4x(lo, xv[0]) + dot4x(hi, xv[1]);
+                cap.put(t, j, s);
                 acc[t] = __builtin_fmaf(e * x.d[t * x.nd + j], (float)s, acc[t]);
             }
         }
@@ -373,8 +383,8 @@ struct Tu<TY_MXFP4> {
     static constexpr bool LUT = true;
     __device__ static float scale(uint32_t e) { return e8m0_half(e); }
     __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read8(p, w, aux); }
-    template <int NT>
-    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT]) {
+    template <int NT, class Cap>
+    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT], const Cap &cap) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
 #pragma unroll
@@ -392,6 +402,7 @@ struct Tu<TY_MXFP4> {
             for (int t = 0; t < NT; ++t) {
                 const int4 *xv = (const int4 *)(x.x + t * x.xt + 32 * j);
                 const int s = dot4x(lo, xv[0]) + dot4x(hi, xv[1]);
+                cap.put(t, j, s);
                 acc[t] = __builtin_fmaf(e * x.d[t * x.nd + j], (float)s, acc[t]);
             }
         }
@@ -408,8 +419,8 @@ struct Tu<TY_NVFP4> {
     static constexpr bool LUT = true;
     __device__ static float scale(uint32_t e) { return nv_scale(e); }
     __device__ static void read(const uint8_t *p, uint32_t (&w)[NDW], uint32_t &aux) { read16(p, w, aux); }
-    template <int NT>
-    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT]) {
+    template <int NT, class Cap>
+    __device__ static void compute(const uint32_t (&w)[NDW], uint32_t, const Lx &x, float (&acc)[NT], const Cap &cap) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
 #pragma unroll
@@ -426,6 +437,8 @@ struct Tu<TY_NVFP4> {
                 for (int t = 0; t < NT; ++t) {
                     const int4 *xv = (const int4 *)(x.x + t * x.xt + 32 * b);
                     const int s0 = dot4x(la, xv[0]), s1 = dot4x(lb, xv[1]);
+                    cap.put(t, 2 * b, s0);
+                    cap.put(t, 2 * b + 1, s1);
                     const float dx = x.d[t * x.nd + b];
                     acc[t] += __builtin_fmaf(e1 * dx, (float)s1, e0 * dx * (float)s0);
                 }
@@ -586,11 +599,14 @@ struct SwStager {
 };
 
 // One tile: rows [row0, row0 + nr) of one matrix (contiguous, nb units each, nr * nb <= THR). SW: the activation
-// is SwiGLU(sg, su) quantized here (NT 1, a Q8_0-activation type), else q / d / bs staged as they are.
-template <int TYPE, int NT, int THR, class Rows, bool SW = false>
+// is SwiGLU(sg, su) quantized here (NT 1, a Q8_0-activation type), else q / d / bs staged as they are. CAP
+// (capture mode): every unit's integer group dots are added into cap (row r's groups at cap + r * K / G, token t
+// cap_ts further on; r counted as row0 is).
+template <int TYPE, int NT, int THR, class Rows, bool SW = false, bool CAP = false>
 __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int row0, int nr, int K, int nb, int lg,
                                           const int8_t *q, const float *d, const int32_t *bs,
-                                          const float *sg = nullptr, const float *su = nullptr) {
+                                          const float *sg = nullptr, const float *su = nullptr,
+                                          int32_t *cap = nullptr, long long cap_ts = 0) {
     using P = Tu<TYPE>;
     using TL = TileLds<TYPE>;
     static_assert(!SW || (NT == 1 && P::ACT == 32 && P::SUMS == 0), "SwiGLU staging: one token, Q8_0 activation");
@@ -644,7 +660,14 @@ __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int r
     x.nd = L.nd;
     x.ns = L.ns;
     float acc[NT];
-    P::template compute<NT>(w, aux, x, acc);
+    if constexpr (CAP) {
+        constexpr int G = cap_group(TYPE);
+        const DotCap dc{tid < nu ? cap + (long long)(row0 + u / nb) * (K / G) + (long long)k * (P::VALS / G) : nullptr,
+                        cap_ts};
+        P::template compute<NT>(w, aux, x, acc, dc);
+    } else {
+        P::template compute<NT>(w, aux, x, acc, NoCap{});
+    }
 
     // partials into the wave's own region (its units were read above; LDS is in order within a wave)
     float *part = (float *)region;
@@ -687,7 +710,7 @@ static TileArgs tile_args(int nb, int thr) {
     return ta;
 }
 
-template <int TYPE, int NT, int THR>
+template <int TYPE, int NT, int THR, bool CAP = false>
 __global__ void __launch_bounds__(THR) k_mv_tile(MvArgs a, TileArgs ta) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const DenseRows rows{a};
@@ -697,12 +720,13 @@ __global__ void __launch_bounds__(THR) k_mv_tile(MvArgs a, TileArgs ta) {
     const int row0 = rows.base(m) + (bx - first) * ta.R;
     const int end = DenseRows::pick(m, a.bound[0], a.bound[1], a.bound[2], a.bound[3]);
     const int nr = end - row0 < ta.R ? end - row0 : ta.R;
-    tile_body<TYPE, NT, THR>(smem, rows, row0, nr, a.K, ta.nb, ta.lg, a.q, a.d, a.bs);
+    tile_body<TYPE, NT, THR, DenseRows, false, CAP>(smem, rows, row0, nr, a.K, ta.nb, ta.lg, a.q, a.d, a.bs, nullptr,
+                                                    nullptr, a.cap, (long long)a.Nt * (a.K / cap_group(TYPE)));
 }
 
 // MoE: grid (tiles, n_used * nmat, T); slot j of token t uses expert ids[t * n_used + j] (-1: Wx). Tiles mode:
 // grid (tiles, tile, max_tiles) over moe_group's expert tiles, one entry per block.
-template <int TYPE, int THR, bool SW = false>
+template <int TYPE, int THR, bool SW = false, bool CAP = false>
 __global__ void __launch_bounds__(THR) k_mv_tile_id(MvIdArgs a, TileArgs ta) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     IdEntry en;
@@ -714,12 +738,15 @@ __global__ void __launch_bounds__(THR) k_mv_tile_id(MvIdArgs a, TileArgs ta) {
                       a.y[m] + en.out_row * a.N, e < 0 ? a.sx[m] : a.es[m] ? a.es[m][e] : a.s[m]};
     const int row0 = (int)blockIdx.x * ta.R;
     const int nr = a.N - row0 < ta.R ? a.N - row0 : ta.R;
+    int32_t *cap = nullptr;
+    if constexpr (CAP) cap = a.cap + ((long long)m * a.cap_rows + en.out_row) * a.N * (K / cap_group(TYPE));
     if constexpr (SW)
-        tile_body<TYPE, 1, THR, IdRows, true>(smem, rows, row0, nr, K, ta.nb, ta.lg, nullptr, nullptr, nullptr,
-                                              a.sw_g + in_row * K, a.sw_u + in_row * K);
+        tile_body<TYPE, 1, THR, IdRows, true, CAP>(smem, rows, row0, nr, K, ta.nb, ta.lg, nullptr, nullptr, nullptr,
+                                                   a.sw_g + in_row * K, a.sw_u + in_row * K, cap, 0);
     else
-        tile_body<TYPE, 1, THR>(smem, rows, row0, nr, K, ta.nb, ta.lg, a.q + in_row * K,
-                                a.d + in_row * (K / Tu<TYPE>::ACT), a.bs ? a.bs + in_row * (K / 16) : nullptr);
+        tile_body<TYPE, 1, THR, IdRows, false, CAP>(smem, rows, row0, nr, K, ta.nb, ta.lg, a.q + in_row * K,
+                                                    a.d + in_row * (K / Tu<TYPE>::ACT),
+                                                    a.bs ? a.bs + in_row * (K / 16) : nullptr, nullptr, nullptr, cap, 0);
 }
 
 // ---------------------------------------------------------------- host side
@@ -747,14 +774,11 @@ static bool tile_takes(int K, int NT, const uint8_t *const *W, int nW, long long
 // Workgroup size: 256 threads, halved (down to 64, while a tile still holds a whole row) as long as the launch
 // would have fewer workgroups than the chip has CUs: a small matrix then spreads over more CUs in smaller tiles.
 // (Measured: config 1's 3072 x 1024 Q8_0 matvec gains 12%; launches of 400+ workgroups lose with smaller tiles.)
-// PURHIE_MV_THREADS (read at each launch) fixes it.
+// PURHIE_MV_THREADS (read once, mv_tune) fixes it.
 constexpr long long TL_MIN_WG = 256;
 
 static int tile_threads(int nb, long long rows) {
-    if (const char *v = getenv("PURHIE_MV_THREADS")) {
-        const int t = atoi(v);
-        if ((t == 64 || t == 128 || t == 256) && nb <= t) return t;
-    }
+    if (const int t = mv_tune().threads; t && nb <= t) return t;
     auto wgs = [&](int t) {
         const long long R = t / nb;
         return (rows + R - 1) / R;
@@ -775,7 +799,8 @@ static hipError_t tile_dense_thr(const MvArgs &a, hipStream_t stream) {
         lo = a.bound[i] > lo ? a.bound[i] : lo;
     }
     const size_t lds = (size_t)TileLds<TYPE>(a.K, NT, THR).bytes;
-    hipLaunchKernelGGL((k_mv_tile<TYPE, NT, THR>), dim3((unsigned)tiles), dim3(THR), lds, stream, a, ta);
+    if (a.cap) hipLaunchKernelGGL((k_mv_tile<TYPE, NT, THR, true>), dim3((unsigned)tiles), dim3(THR), lds, stream, a, ta);
+    else hipLaunchKernelGGL((k_mv_tile<TYPE, NT, THR>), dim3((unsigned)tiles), dim3(THR), lds, stream, a, ta);
     return hipGetLastError();
 }
 
@@ -826,13 +851,15 @@ static hipError_t tile_id_thr(const MvIdArgs &a, hipStream_t stream) {
     const size_t lds = (size_t)TileLds<TYPE>(a.K, 1, THR).bytes;
     if constexpr (Tu<TYPE>::ACT == 32 && Tu<TYPE>::SUMS == 0) {
         if (a.sw_g) {
-            hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, true>), grid, dim3(THR), lds, stream, a, ta);
+            if (a.cap) hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, true, true>), grid, dim3(THR), lds, stream, a, ta);
+            else hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, true>), grid, dim3(THR), lds, stream, a, ta);
             return hipGetLastError();
         }
     } else if (a.sw_g) {
         return hipErrorInvalidDeviceFunction;
     }
-    hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR>), grid, dim3(THR), lds, stream, a, ta);
+    if (a.cap) hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, false, true>), grid, dim3(THR), lds, stream, a, ta);
+    else hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR>), grid, dim3(THR), lds, stream, a, ta);
     return hipGetLastError();
 }
 

@@ -1,17 +1,16 @@
 // qmatvec.cpp -- the C ABI of include/qmatvec.h over this library's HIP kernels.
 //
-// Host-side dispatch mirrors the reference's src/qmatvec.cpp (argument checks, error codes, buffer
-// layout of qmatvec_q8, the output-scale registry); the launch geometry is this library's own
-// (wave64 kernels, lanes per row chosen per shape, activation staged in LDS).
+// Host-side dispatch keeps the reference's src/qmatvec.cpp contract (argument checks, error codes, buffer
+// layout of qmatvec_q8); the launch geometry is this library's own (wave64 kernels, lanes per row chosen per
+// shape, activation staged in LDS). The output-scale registry is out_scale.cpp.
 #include "../../include/qmatvec.h"
 #include "../../include/quant_types.h"
 #include "kernels.h"
+#include "out_scale.h"
 
 #include <atomic>
-#include <mutex>
 #include <stdlib.h>
 #include <string.h>
-#include <vector>
 
 using namespace pq;
 
@@ -41,33 +40,30 @@ int g_inited = 0;
 std::atomic<int> g_prefill{0};
 int g_prefill_fp32 = 0;
 
-// ---- output scales (src/qmatvec.cpp:175-253)
-struct OutScale {
-    const void *owner;
-    const char *lo, *hi;
-    const float *s;
-    int n;
-};
-std::vector<OutScale> g_scales;
-std::mutex g_scales_mu;
-std::atomic<int> g_n_scales{0};
+// capture mode (qmatvec_debug_capture): the integer dots of every int8 launch go to g_cap (g_cap_n ints)
+int32_t *g_cap = nullptr;
+size_t g_cap_n = 0;
 
-bool find_scale(const void *W, OutScale &o) {
-    if (!W || g_n_scales.load(std::memory_order_relaxed) == 0) return false;
-    std::lock_guard<std::mutex> lk(g_scales_mu);
-    for (const OutScale &x : g_scales)
-        if ((const char *)W >= x.lo && (const char *)W < x.hi) {
-            o = x;
-            return true;
-        }
-    return false;
+// the capture buffer for a launch writing `need` ints, or an error when it does not fit
+hipError_t cap_for(long long need, int32_t *&cap) {
+    cap = g_cap;
+    if (g_cap && (need < 0 || (size_t)need > g_cap_n)) return hipErrorInvalidValue;
+    return hipSuccess;
 }
 
-float dense_scale(const void *W) {
-    OutScale o;
-    if (!find_scale(W, o)) return 1.0f;
-    if (o.n == 1) return o.s[0];
-    return o.s[((const char *)W - o.lo) / ((o.hi - o.lo) / o.n)];
+// the output factor of a launch on rows from W (1 without a registration)
+float dense_scale(const void *W) { return scale_dense(W); }
+
+// an expert launch's factors for the stacked experts W: per-expert factors (handed to the kernel, which reads
+// them on the device) or one factor for all
+void expert_scale(const void *W, const float *&es, float &s) {
+    es = nullptr;
+    s = 1.0f;
+    ScaleHit h;
+    if (scale_find(W, h)) {
+        if (h.n > 1) es = h.s;
+        else s = h.s[0];
+    }
 }
 
 void act_ptrs(int type, const qmatvec_q8 *q, const int8_t *&q8, const float *&d8, const int32_t *&bs) {
@@ -171,8 +167,10 @@ hipError_t gemm_dense(int type, const void *W, size_t row_bytes, const qmatvec_q
         a.zero_row = Tpad;
         a.osc = dense_scale(W);
         a.tt = BT;
+        if (gemm_cap_unit(type)) e = cap_for((long long)T * N * (K / gemm_cap_unit(type)), a.cap);
         const int RN = gemm_rows_per_wg(type);
-        e = gemm_launch(type, a, dim3((unsigned)(Tpad / BT), (unsigned)((N + RN - 1) / RN)), stream);
+        if (e == hipSuccess)
+            e = gemm_launch(type, a, dim3((unsigned)(Tpad / BT), (unsigned)((N + RN - 1) / RN)), stream);
     }
     if (w.mem) {
         const hipError_t f = hipFreeAsync(w.mem, stream);
@@ -195,21 +193,6 @@ int qmatvec_init(const char *co_path) {
 }
 
 void qmatvec_free(void) { g_inited = 0; }
-
-int qmatvec_set_out_scale(const void *owner, const void *W, size_t bytes, const float *s, int n) {
-    if (!W || !s || n < 1 || bytes % (size_t)n != 0) return -1;
-    std::lock_guard<std::mutex> lk(g_scales_mu);
-    g_scales.push_back({owner, (const char *)W, (const char *)W + bytes, s, n});
-    g_n_scales.store((int)g_scales.size());
-    return 0;
-}
-
-void qmatvec_drop_out_scales(const void *owner) {
-    std::lock_guard<std::mutex> lk(g_scales_mu);
-    for (size_t i = g_scales.size(); i-- > 0;)
-        if (g_scales[i].owner == owner) g_scales.erase(g_scales.begin() + (long)i);
-    g_n_scales.store((int)g_scales.size());
-}
 
 // ---- float activations over F32 / F16 / BF16 weights (src/qmatvec.cpp:255-366). The quantized types have no
 // float-activation kernel here (their path is the int8 one): qmatvec_supported answers 0 for them and their
@@ -379,6 +362,7 @@ hipError_t qmatvec_launch_q8_multi_t(int type, int n, const void *const *Ws, con
     a.K = K;
     a.T = T;
     a.L = matvec_lanes(type, K, Nt);
+    if (const hipError_t e = cap_for((long long)T * Nt * (K / cap_group(type)), a.cap); e != hipSuccess) return e;
     return launch_matvec(type, a, stream);
 }
 
@@ -423,14 +407,8 @@ hipError_t qmatvec_launch_q8_id_x(int type, const void *W, const void *W2, const
     a.y[1] = y2;
     const void *ws[2] = {W, W2}, *wx[2] = {Wx, W2x};
     for (int m = 0; m < 2; ++m) {
-        a.es[m] = nullptr;
-        a.s[m] = a.sx[m] = 1.0f;
-        OutScale o;
-        if (find_scale(ws[m], o)) {
-            if (o.n > 1) a.es[m] = o.s;  // per-expert factors: read by the kernel (device-visible)
-            else a.s[m] = o.s[0];
-        }
-        if (wx[m]) a.sx[m] = dense_scale(wx[m]);
+        expert_scale(ws[m], a.es[m], a.s[m]);  // (per-expert factors are read by the kernel: device-visible)
+        a.sx[m] = wx[m] ? dense_scale(wx[m]) : 1.0f;
     }
     a.row_bytes = (long long)row_bytes;
     a.ids = ids;
@@ -442,6 +420,8 @@ hipError_t qmatvec_launch_q8_id_x(int type, const void *W, const void *W2, const
     a.T = T;
     a.nmat = W2 ? 2 : 1;
     a.L = matvec_lanes(type, K, (long long)N * n_used * a.nmat * T);
+    a.cap_rows = (long long)T * n_used;
+    if (const hipError_t e = cap_for(a.nmat * a.cap_rows * N * (K / cap_group(type)), a.cap); e != hipSuccess) return e;
     return launch_matvec_id(type, a, stream);
 }
 
@@ -464,14 +444,10 @@ hipError_t qmatvec_launch_q8_id_swiglu(int type, const void *W, const void *Wx, 
     a.W[0] = (const uint8_t *)W;
     a.Wx[0] = (const uint8_t *)Wx;
     a.y[0] = y;
-    a.es[0] = a.es[1] = nullptr;
-    a.s[0] = a.s[1] = a.sx[0] = a.sx[1] = 1.0f;
-    OutScale o;
-    if (find_scale(W, o)) {
-        if (o.n > 1) a.es[0] = o.s;
-        else a.s[0] = o.s[0];
-    }
-    if (Wx) a.sx[0] = dense_scale(Wx);
+    a.es[1] = nullptr;
+    a.s[1] = a.sx[1] = 1.0f;
+    expert_scale(W, a.es[0], a.s[0]);
+    a.sx[0] = Wx ? dense_scale(Wx) : 1.0f;
     a.row_bytes = (long long)row_bytes;
     a.ids = ids;
     a.sw_g = g;
@@ -483,6 +459,8 @@ hipError_t qmatvec_launch_q8_id_swiglu(int type, const void *W, const void *Wx, 
     a.T = T;
     a.nmat = 1;
     a.L = matvec_lanes(type, K, (long long)N * n_used * T);
+    a.cap_rows = (long long)T * n_used;
+    if (const hipError_t e = cap_for(a.cap_rows * N * (K / cap_group(type)), a.cap); e != hipSuccess) return e;
     return launch_matvec_id(type, a, stream);
 }
 
@@ -524,7 +502,10 @@ hipError_t qmatvec_launch_q8_batch(int type, const void *W, size_t row_bytes, co
     const int32_t *bs;
     act_ptrs(type, q, q8, d8, bs);
     const int kb = K / act_blk(type);
+    int32_t *cap;
+    if (const hipError_t e = cap_for((long long)T * N * (K / cap_group(type)), cap); e != hipSuccess) return e;
     for (int t0 = 0; t0 < T; t0 += 4) {
+        a.cap = cap ? cap + (long long)t0 * N * (K / cap_group(type)) : nullptr;
         a.T = T - t0 < 4 ? T - t0 : 4;
         a.y[0] = a.y[1] = a.y[2] = a.y[3] = y + (long long)t0 * ldy;
         a.q = q8 + (long long)t0 * K;
@@ -560,12 +541,8 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
         MvIdArgs a{};
         a.W[0] = (const uint8_t *)W;
         a.y[0] = y;
-        a.s[0] = a.sx[0] = 1.0f;
-        OutScale o;
-        if (find_scale(W, o)) {
-            if (o.n > 1) a.es[0] = o.s;
-            else a.s[0] = o.s[0];
-        }
+        a.sx[0] = 1.0f;
+        expert_scale(W, a.es[0], a.s[0]);
         a.row_bytes = (long long)row_bytes;
         act_ptrs(type, q, a.q, a.d, a.bs);
         a.N = N;
@@ -582,6 +559,8 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
         a.tile = tile;
         a.max_tiles = max_tiles;
         a.L = matvec_lanes(type, K, (long long)N * tile * max_tiles);
+        a.cap = g_cap;  // (tiles mode: output rows come from out_rows on the device; the caller sizes the buffer)
+        a.cap_rows = 0;
         return launch_matvec_id(type, a, stream);
     }
     // every input row the buffer can hold (in_rows index them) goes through the pre-pass; row `rows` is zero
@@ -608,12 +587,8 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
         a.tile_n = tile_n;
         a.in_rows = in_rows;
         a.out_rows = out_rows;
-        OutScale o;
-        a.osc = 1.0f;
-        if (find_scale(W, o)) {
-            if (o.n > 1) a.es = o.s;
-            else a.osc = o.s[0];
-        }
+        expert_scale(W, a.es, a.osc);
+        if (gemm_cap_unit(type)) a.cap = g_cap;  // (tiles mode: rows from out_rows; the caller sizes the buffer)
         const int RN = gemm_rows_per_wg(type);
         e = gemm_launch(type, a, dim3((unsigned)((N + RN - 1) / RN), (unsigned)max_tiles), stream);
     }
@@ -622,6 +597,23 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
         if (e == hipSuccess) e = f;
     }
     return e;
+}
+
+hipError_t qmatvec_debug_capture(int32_t *out, size_t n_ints) {
+    g_cap = out;
+    g_cap_n = out ? n_ints : 0;
+    return hipSuccess;
+}
+
+int qmatvec_debug_capture_unit(int type, int gemm) {
+    if (!is_int8_type(type)) return 0;
+    return gemm ? gemm_cap_unit(type) : cap_group(type);
+}
+
+int qmatvec_debug_decode_path(int mode) {
+    const int prev = mv_tune().tile;
+    if (mode == 0 || mode == 1) mv_tune_set_tile(mode);
+    return prev;
 }
 
 hipError_t qmatvec_debug_block_dots(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, int32_t *out,

@@ -79,6 +79,9 @@ def lib():
             "qmatvec_launch_q8_id_batch": (i32, [i32, vp, sz, pq8, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp,
                                                  vp]),
             "qmatvec_debug_block_dots": (i32, [i32, vp, sz, pq8, vp, i32, i32, vp]),
+            "qmatvec_debug_capture": (i32, [vp, sz]),
+            "qmatvec_debug_capture_unit": (i32, [i32, i32]),
+            "qmatvec_debug_decode_path": (i32, [i32]),
             "qmatvec_set_prefill": (None, [i32]),
             "qmatvec_prefill": (i32, []),
             "qmatvec_set_out_scale": (i32, [vp, vp, sz, vp, i32]),
@@ -210,6 +213,35 @@ def launch_q8_id_x(t, W, W2, Wx, W2x, ids, n_used, x_per_slot, q, y, y2, N, K, T
     _check("qmatvec_launch_q8_id_x",
            lib().qmatvec_launch_q8_id_x(t, _p(W), _p(W2), _p(Wx), _p(W2x), row_size(t, K), _p(ids), n_used,
                                         x_per_slot, q.ref, _p(y), _p(y2), N, K, T, stream))
+
+
+class capture:
+    """capture mode (qmatvec_debug_capture) for the launches inside the `with` block: the kernels also add every
+    integer sum they form into `out` (an int32 device tensor, zeroed here), in the layouts include/qmatvec.h
+    gives"""
+
+    def __init__(self, out):
+        self.out = out
+
+    def __enter__(self):
+        self.out.zero_()
+        _check("qmatvec_debug_capture", lib().qmatvec_debug_capture(_p(self.out), self.out.numel()))
+        return self.out
+
+    def __exit__(self, *exc):
+        lib().qmatvec_debug_capture(None, 0)
+        return False
+
+
+def capture_unit(t, gemm=False):
+    """values per captured integer: the decode kernels' scale group, or the GEMM's epilogue unit (0: none)"""
+    return lib().qmatvec_debug_capture_unit(t, 1 if gemm else 0)
+
+
+def decode_path(mode=None):
+    """the decode kernels in use: 1 = tile kernels where they take the shape, 0 = per-wave kernels only; sets
+    `mode` when given and returns the previous one"""
+    return lib().qmatvec_debug_decode_path(-1 if mode is None else mode)
 
 
 def block_dots(t, W, q, out, N, K, stream=None):

@@ -41,3 +41,28 @@ def ref(oracle):
     if not oracle.ref_available():
         pytest.skip("oracle/_ref/libref.so not built (needs the reference tree: make -f oracle/ref.mk)")
     return oracle
+
+
+def pytest_terminal_summary(terminalreporter):
+    """the per-output readings the fp32 parity checks recorded (tests/parity.py)"""
+    try:
+        from tests import parity
+    except ImportError:
+        return
+    if not parity.STATS:
+        return
+    tr = terminalreporter
+    tr.section("fp32 outputs: relative error and ULP distance (beside the 1e-5 * sum|w x| bound)")
+    tr.write_line(f"{'category':58s} {'outputs':>9s} {'rel<=1e-5|<=2ulp':>17s} {'p99 rel':>9s} {'max rel':>9s} "
+                  f"{'max ulp':>9s}")
+    for k in sorted(parity.STATS):
+        s = parity.STATS[k]
+        frac = s["meet_rel1e-5_or_2ulp"] / max(s["outputs"], 1)
+        tr.write_line(f"{k:58s} {s['outputs']:9d} {frac:17.6f} {s['p99_rel']:9.2e} {s['max_rel']:9.2e} "
+                      f"{s['max_ulp']:9d}")
+    path = os.environ.get("PURHIE_PARITY_STATS")
+    if path:
+        import json
+        os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+        with open(path, "w") as f:
+            json.dump(parity.STATS, f, indent=1, sort_keys=True)

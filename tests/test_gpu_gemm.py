@@ -6,6 +6,7 @@ import numpy as np
 import pytest
 
 from purhie_amd import synth
+from tests import parity
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -49,13 +50,12 @@ def run_batch(Q, t, Wd, x, N, K, ldy=None):
     return host(y)[:, :N]
 
 
-def check_tokens(oracle, t, W, N, K, x, got):
+def check_tokens(oracle, t, W, N, K, x, got, what="prefill GEMM"):
+    from purhie_amd import qmatvec
     for i in range(x.shape[0]):
         a = oracle.quantize_act(x[i], t in (12, 13, 14, 23))
         want, ref, mag = oracle.matvec(t, W, N, K, a)
-        err = np.abs(got[i] - want) / (mag + 1e-30)
-        assert err.max() <= TOL, f"token {i}: max rel err {err.max():.3g}"
-        assert np.all(np.abs(got[i] - ref) <= TOL * mag)
+        parity.check(f"{what} {qmatvec.NAMES[t]}", got[i], want, mag, ref, TOL)
 
 
 @pytest.mark.parametrize("t", GEMM_TYPES)
@@ -117,15 +117,17 @@ def test_moe_tiled_gemm(Q, oracle, t, N, K):
     for tt in range(T):
         a = oracle.quantize_act(x[tt], t in (12, 13, 14, 23))
         for j in range(n_used):
-            want, _, mag = oracle.matvec(t, W.reshape(E, N, rb)[ids[tt, j]], N, K, a)
-            assert np.all(np.abs(got[tt * n_used + j] - want) <= TOL * mag)
+            want, ref, mag = oracle.matvec(t, W.reshape(E, N, rb)[ids[tt, j]], N, K, a)
+            parity.check(f"expert-tiled GEMM {Q.NAMES[t]}", got[tt * n_used + j], want, mag, ref, TOL)
 
 
 @pytest.fixture(params=["tile", "wave"])
 def kpath(request, monkeypatch):
     """the decode kernels under test: the one-unit-per-lane tile kernels or the per-wave kernels"""
-    monkeypatch.setenv("PURHIE_MV_TILE", "1" if request.param == "tile" else "0")
-    return request.param
+    from purhie_amd import qmatvec
+    prev = qmatvec.decode_path(1 if request.param == "tile" else 0)
+    yield request.param
+    qmatvec.decode_path(prev)
 
 
 @pytest.fixture

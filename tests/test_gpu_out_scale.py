@@ -24,8 +24,10 @@ def Q():
 
 @pytest.fixture(params=["tile", "wave"])
 def kpath(request, monkeypatch):
-    monkeypatch.setenv("PURHIE_MV_TILE", "1" if request.param == "tile" else "0")
-    return request.param
+    from purhie_amd import qmatvec
+    prev = qmatvec.decode_path(1 if request.param == "tile" else 0)
+    yield request.param
+    qmatvec.decode_path(prev)
 
 
 def dev(a):

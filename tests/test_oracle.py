@@ -519,3 +519,67 @@ def test_matvec_float_closed_form(oracle, t):
     xa = oracle.act_round(t, x).astype(np.float64)
     ref, mag = oracle.matvec_float(t, Wb, N, K, x)
     assert np.allclose(ref, xa @ wd.T, rtol=1e-13, atol=0) and np.allclose(mag, np.abs(xa) @ np.abs(wd).T, rtol=1e-13)
+
+
+def _kq_block_scale(W, t, N, K):
+    """the fp16 super-block scale d of every (row, super-block), from the byte map (Q6_K: bytes 208..209; IQ4_XS,
+    Q4_K, Q5_K: bytes 0..1)"""
+    by = {12: 144, 13: 176, 14: 210, 23: 136}[t]
+    off = 208 if t == 14 else 0
+    b = W.reshape(N, K // 256, by)[:, :, off:off + 2]
+    return np.ascontiguousarray(b).view(np.float16)[..., 0].astype(np.float64)
+
+
+@pytest.mark.parametrize("t", (14, 23))
+def test_unit_isum_from_decoded_weights(oracle, t):
+    """Q6_K / IQ4_XS: a decoded weight is d times an integer (sc_g (q - 32), or ls level) of magnitude <= 4096,
+    rounded once or twice in fp32, so round(w / d) recovers that integer exactly; the super-block's isum is then
+    sum_i round(w_i / d) qK_i, whatever the oracle's own index and scale code does"""
+    N, K = 6, 1024
+    W = oracle.quantize(t, synth.gaussian(50 + t, N * K, 0, 0.02).reshape(N, K))
+    a = oracle.quantize_act(synth.gaussian(60 + t, K), True)
+    got = oracle.unit_isum(t, W, N, K, a["q"], a["bs"])
+    w = oracle.to_float(t, W.reshape(-1), K).reshape(N, K // 256, 256).astype(np.float64)
+    d = _kq_block_scale(W, t, N, K)
+    ints = np.rint(w / d[..., None])
+    assert np.all(np.abs(ints - w / d[..., None]) < 1e-2)  # integers, as claimed
+    want = (ints.astype(np.int64) * a["q"].reshape(K // 256, 256).astype(np.int64)).sum(-1)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("t", (12, 13))
+def test_unit_isum_zero_sum_activation(oracle, t):
+    """Q4_K / Q5_K: with an activation whose every 32-value sub-block sums to zero (x[i + 16] = -x[i], which the
+    quantizer maps to q[i + 16] = -q[i]), the min term drops out and isum_j = sum_i sc_j (q_i - q_0) qK_i, where
+    sc_j (q_i - q_0) = round((w_i - w_0) / d) is recovered exactly from the decoded weights (|.| <= 1953)"""
+    N, K = 6, 1024
+    W = oracle.quantize(t, synth.gaussian(70 + t, N * K, 0, 0.02).reshape(N, K))
+    h = synth.gaussian(80 + t, K // 2).reshape(-1, 16)
+    x = np.concatenate([h, -h], axis=1).reshape(-1)  # each 32-block: 16 values then their negations
+    a = oracle.quantize_act(x, True)
+    qb = a["q"].reshape(-1, 32).astype(np.int64)
+    assert np.all(qb.sum(1) == 0)
+    got = oracle.unit_isum(t, W, N, K, a["q"], a["bs"])
+    w = oracle.to_float(t, W.reshape(-1), K).reshape(N, K // 32, 32).astype(np.float64)
+    d = np.repeat(_kq_block_scale(W, t, N, K), 8, axis=1)
+    diff = (w - w[:, :, :1]) / d[..., None]
+    ints = np.rint(diff)
+    assert np.all(np.abs(ints - diff) < 1e-2)
+    per_sub = (ints.astype(np.int64) * qb[None]).sum(-1)  # [N][K / 32]
+    want = per_sub.reshape(N, K // 256, 8).sum(-1)
+    assert np.array_equal(got, want)
+
+
+def test_shared_gate_closed_form(oracle):
+    """sg = 1 / (1 + exp(-(x . w))) (src/gpu_ops.hip:213-229): 0.5 exactly for an orthogonal pair, above / below
+    0.5 with the sign of the dot, saturating to 1 / 0, and within fp32 rounding of the float64 logistic"""
+    assert oracle.shared_gate(np.array([1.0, 1.0], np.float32), np.array([1.0, -1.0], np.float32)) == 0.5
+    x = synth.gaussian(90, 2048)
+    w = synth.gaussian(91, 2048, 0, 0.02)
+    d = float(np.dot(x.astype(np.float64), w.astype(np.float64)))
+    sg = oracle.shared_gate(x, w)
+    assert abs(sg - 1.0 / (1.0 + np.exp(-d))) <= 4e-7
+    assert (sg > 0.5) == (d > 0)
+    assert oracle.shared_gate(x, -w) == pytest.approx(1.0 - sg, abs=4e-7)  # the logistic's symmetry
+    big = np.full(64, 4.0, np.float32)
+    assert oracle.shared_gate(big, big) == 1.0 and oracle.shared_gate(big, -big) == 0.0
