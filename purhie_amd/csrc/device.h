@@ -205,6 +205,19 @@ __device__ __forceinline__ bool id_entry(const MvIdArgs &a, IdEntry &o) {
     return true;
 }
 
+// Tile of a dense GEMM grid (token tiles along x, row tiles along y). The hardware deals workgroups to the 8 XCDs
+// round robin by linear id; renumbered, XCD c runs a contiguous range of tiles in which `group` token tiles advance
+// together over the row tiles, so the workgroups resident on one XCD share a few activation and weight tiles in its
+// L2. Only the order changes (a bijection onto the grid): each tile's arithmetic, and so its bits, stay the same.
+__device__ inline void xcd_tile(int &tt, int &rt, int group) {
+    const int ntt = gridDim.x, nrt = gridDim.y, nwg = ntt * nrt;
+    const int L = blockIdx.x + blockIdx.y * ntt, q = nwg >> 3, r = nwg & 7, c = L & 7;
+    const int b = c * q + min(c, r) + (L >> 3);
+    const int tg = b / (group * nrt), w = b - tg * group * nrt, gn = min(group, ntt - tg * group);
+    tt = tg * group + w % gn;
+    rt = w / gn;
+}
+
 // Token rows of a GEMM tile: dense tiles take rows base .. base + tile - 1 of the pre-pass output; MoE tiles take
 // their entries' input rows, and the zero row past the last entry
 struct TokMap {

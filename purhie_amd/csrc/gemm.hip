@@ -561,20 +561,9 @@ struct SplitStage<TY_NVFP4> {
     }
 };
 
-// Tile of a dense grid (token tiles along x, row tiles along y). The hardware deals workgroups to the 8 XCDs
-// round robin by linear id; renumbered, XCD c runs a contiguous range of tiles in which GS_GROUP token tiles
-// advance together over the row tiles, so the workgroups resident on one XCD share a few activation and weight
-// tiles in its L2. Only the order changes: each tile's arithmetic, and so its bits, stay the same.
 constexpr int GS_GROUP = 4;
 
-__device__ inline void dense_tile(int &tt, int &rt) {
-    const int ntt = gridDim.x, nrt = gridDim.y, nwg = ntt * nrt;
-    const int L = blockIdx.x + blockIdx.y * ntt, q = nwg >> 3, r = nwg & 7, c = L & 7;
-    const int b = c * q + min(c, r) + (L >> 3);
-    const int tg = b / (GS_GROUP * nrt), w = b - tg * GS_GROUP * nrt, gn = min(GS_GROUP, ntt - tg * GS_GROUP);
-    tt = tg * GS_GROUP + w % gn;
-    rt = w / gn;
-}
+__device__ inline void dense_tile(int &tt, int &rt) { xcd_tile(tt, rt, GS_GROUP); }
 
 // workgroup tile 256 weight rows x TT tokens (128; 64 for MoE expert tiles, whose runs average a few dozen
 // entries, and for prompts of at most 64 tokens); wave w computes rows 128 (w & 1) .. + 127 x tokens TT / 2 (w >> 1) .. (8 x TT / 32 MFMA tiles): per

@@ -92,6 +92,7 @@ struct GemmArgs {
     const _Float16 *xs;     // split GEMM: their block scales dx 2^s [rows][K / 32]
     const float *ts;        // split GEMM: per-row output factor 2^-s
     const _Float16 *xb;     // K-quant GEMM: the token's 16-value group sums [rows][K / 16] (dx: dK [rows][K / 256])
+    const int32_t *xsum;    // int8 K-quant GEMM: the Q8_K 16-value sums [rows][K / 16] (xq: qK, dx: dK, read in place)
     float *y;
     long long ldy;
     int N, K, T, zero_row;
@@ -137,6 +138,13 @@ constexpr int GEMM_KQ_ROWS = 128;  // weight rows per K-quant GEMM workgroup
 hipError_t launch_act_q8k(const int8_t *q, const float *dK, const int32_t *bs, int T, int K, int rows, _Float16 *xh,
                           _Float16 *xb, float *xd, hipStream_t stream);
 hipError_t launch_gemm_kquant(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);
+// the int8-MFMA K-quant GEMM (gemm_i8.hip): the Q8_K activation read in place (xq = qK, dx = dK, xsum = bsK);
+// dense grid (tokens / gemm_i8kq_token_tile(false), rows / gemm_i8kq_rows()), MoE grid (rows / gemm_i8kq_rows(), tiles) with
+// tiles of up to gemm_i8kq_token_tile(true) entries
+bool gemm_i8kq_supported(int type);
+int gemm_i8kq_token_tile(bool moe);
+int gemm_i8kq_rows();  // weight rows per workgroup
+hipError_t launch_gemm_i8kq(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);
 
 // lanes per row the decode kernels use for a matrix of K columns and `rows` rows in total
 int matvec_lanes(int type, int K, long long rows);

@@ -133,6 +133,27 @@ hipError_t tokens_prep(int type, const qmatvec_q8 *q, int T, int K, int rows, To
     return launch_act_f16(type, q->q0, q->d0, T, K, rows - 1, w.xh, w.dx, stream);
 }
 
+// The K-quant GEMM: the int8-MFMA kernel of gemm_i8.hip, which reads the Q8_K activation in place, or the fp16
+// one of gemm_k.hip (PURHIE_KQ_GEMM=fp16, read once: kept for comparison)
+bool kq_int8(int type) {
+    static const bool fp16 = getenv("PURHIE_KQ_GEMM") && strcmp(getenv("PURHIE_KQ_GEMM"), "fp16") == 0;
+    return !fp16 && gemm_i8kq_supported(type);
+}
+
+// the int8 K-quant GEMM's arguments for the activation q (no staging: it is read where it is)
+GemmArgs i8kq_args(const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N, int K) {
+    GemmArgs a{};
+    a.W = (const uint8_t *)W;
+    a.row_bytes = (long long)row_bytes;
+    a.xq = q->qK;
+    a.dx = q->dK;
+    a.xsum = q->bsK;
+    a.y = y;
+    a.N = N;
+    a.K = K;
+    return a;
+}
+
 hipError_t gemm_launch(int type, const GemmArgs &a, dim3 grid, hipStream_t stream) {
     if (gemm_kquant(type)) return launch_gemm_kquant(type, a, grid, stream);
     return gemm_split(type) ? launch_gemm_split(type, a, grid, stream) : launch_gemm(type, a, grid, stream);
@@ -145,6 +166,16 @@ int gemm_k_mult(int type) {
 
 hipError_t gemm_dense(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, long long ldy, int N,
                       int K, int T, hipStream_t stream) {
+    if (kq_int8(type)) {
+        GemmArgs a = i8kq_args(W, row_bytes, q, y, N, K);
+        a.ldy = ldy;
+        a.T = T;
+        a.osc = dense_scale(W);
+        if (const hipError_t e = cap_for((long long)T * N * (K / 256), a.cap); e != hipSuccess) return e;
+        const int BT = gemm_i8kq_token_tile(false);
+        const int RN = gemm_i8kq_rows();
+        return launch_gemm_i8kq(type, a, dim3((unsigned)((T + BT - 1) / BT), (unsigned)((N + RN - 1) / RN)), stream);
+    }
     const int BT = gemm_dense_token_tile(type, T);
     const int Tpad = (T + BT - 1) / BT * BT;
     TokWs w;
@@ -526,7 +557,8 @@ static bool id_gemm_ok(int type, int N, int K) {
 // the largest tile the expert-tiled launch takes: the GEMM reads each expert's weights once per this many
 // entries; the decode-order path takes the reference's 16 (src/qmatvec.cpp:612-615)
 int qmatvec_id_batch_tile(int type, int N, int K) {
-    return id_gemm_ok(type, N, K) ? gemm_id_token_tile(type) : ID_DECODE_TILE;
+    if (!id_gemm_ok(type, N, K)) return ID_DECODE_TILE;
+    return kq_int8(type) ? gemm_i8kq_token_tile(true) : gemm_id_token_tile(type);
 }
 
 hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N,
@@ -562,6 +594,19 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
         a.cap = g_cap;  // (tiles mode: output rows come from out_rows on the device; the caller sizes the buffer)
         a.cap_rows = 0;
         return launch_matvec_id(type, a, stream);
+    }
+    if (kq_int8(type)) {  // the activation read in place: input rows are in_rows[] of q
+        GemmArgs a = i8kq_args(W, row_bytes, q, y, N, K);
+        a.n_tiles = n_tiles;
+        a.tile_e = tile_e;
+        a.tile_start = tile_start;
+        a.tile_n = tile_n;
+        a.in_rows = in_rows;
+        a.out_rows = out_rows;
+        expert_scale(W, a.es, a.osc);
+        a.cap = g_cap;  // (tiles mode: rows from out_rows; the caller sizes the buffer)
+        const int RN = gemm_i8kq_rows();
+        return launch_gemm_i8kq(type, a, dim3((unsigned)((N + RN - 1) / RN), (unsigned)max_tiles), stream);
     }
     // every input row the buffer can hold (in_rows index them) goes through the pre-pass; row `rows` is zero
     const int rows = q->max_k / K;
