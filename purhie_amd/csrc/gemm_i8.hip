@@ -504,10 +504,243 @@ __global__ void __launch_bounds__(I8_THREADS, 2) k_gemm_i8kq(GemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- per-block GEMM (Q8_0, MXFP4)
+// The reference's per-block form (src/matvec_q.hip:2566-2973, WStageQ8_0): one int8 MFMA per 32-value block gives
+// the exact int32 block dot of each (token, row), and y += (e_w d_x) dot. The weight scale is per row and block (a
+// per-lane value), d_x per token and block. Weights: Q8_0's int8 values as they are, MXFP4's E2M1 levels doubled
+// (int8 -12..12; the E8M0 decoder's scale is already halved). Stage = two blocks (64 K); geometry, staging and the
+// two-stage-ahead loads as the K-quant GEMM above; the Q8_0 activation (q0, d0) is read in place.
+struct BDst {
+    int8_t *w;   // the stage's values, row 0 (one plane)
+    float *ew;   // the stage's weight scales [2 blocks][I8_N]
+};
+
+template <int TYPE>
+struct I8Blk;
+
+// Q8_0 (34-byte blocks, 2-aligned): quarter p takes block p >> 1, values 16 (p & 1) .. + 15 (bytes 2 + 16 (p & 1)
+// of the block), read as five dwords from the 4-aligned address at or below them
+template <>
+struct I8Blk<TY_Q8_0> {
+    static constexpr int BPB = 34;  // bytes per block
+    struct Raw {
+        uint32_t v[5];
+        uint32_t off, e;
+    };
+    __device__ static void load(const uint8_t *row, int blk0, Raw &r) {
+        const int p = threadIdx.x & 3;
+        const uint8_t *b = row + (blk0 + (p >> 1)) * BPB;
+        const uint8_t *v = b + 2 + 16 * (p & 1);
+        r.off = (uint32_t)((uintptr_t)v & 3u);
+        const uint8_t *va = v - r.off;
+#pragma unroll
+        for (int k = 0; k < 5; ++k) r.v[k] = ld32(va + 4 * k);
+        r.e = *(const uint16_t *)b;
+    }
+    __device__ static void store(const Raw &r, const BDst &o) {
+        const int row = threadIdx.x >> 2, p = threadIdx.x & 3;
+        uint32_t q[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) q[k] = align_bytes(r.v[k + 1], r.v[k], r.off);
+        *(uint4 *)(o.w + row * I8_ROW + 16 * p) = make_uint4(q[0], q[1], q[2], q[3]);
+        if ((p & 1) == 0) o.ew[(p >> 1) * I8_N + row] = h2f(r.e);
+    }
+};
+
+// MXFP4 (17-byte blocks: E8M0 scale, then 16 value bytes: value j < 16 the low nibble of byte 1 + j, j >= 16 the
+// high nibble of byte 1 + j - 16): quarter p takes block p >> 1, values 16 (p & 1) .. + 15
+template <>
+struct I8Blk<TY_MXFP4> {
+    static constexpr int BPB = 17;
+    struct Raw {
+        uint32_t v[5];
+        uint32_t off, e;
+    };
+    __device__ static void load(const uint8_t *row, int blk0, Raw &r) {
+        const int p = threadIdx.x & 3;
+        const uint8_t *b = row + (blk0 + (p >> 1)) * BPB;
+        r.off = (uint32_t)((uintptr_t)b & 3u);
+        const uint8_t *ba = b - r.off;
+#pragma unroll
+        for (int k = 0; k < 5; ++k) r.v[k] = ld32(ba + 4 * k);
+        r.e = 0;
+    }
+    __device__ static void store(const Raw &r, const BDst &o) {
+        const int row = threadIdx.x >> 2, p = threadIdx.x & 3;
+        uint32_t w[5];
+#pragma unroll
+        for (int k = 0; k < 5; ++k) w[k] = align_bytes(k < 4 ? r.v[k + 1] : 0u, r.v[k], r.off);
+        uint32_t q[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t b = align_bytes(w[k + 1], w[k], 1);  // value bytes 4 k .. 4 k + 3
+            q[k] = (p & 1) ? (uint32_t)fp4x4_hi<12>(b) : (uint32_t)fp4x4_lo<12>(b);
+        }
+        *(uint4 *)(o.w + row * I8_ROW + 16 * p) = make_uint4(q[0], q[1], q[2], q[3]);
+        if ((p & 1) == 0) o.ew[(p >> 1) * I8_N + row] = e8m0_half(w[0]);
+    }
+};
+
+template <int TYPE, int WI, int WT, bool MOE, bool CAP>
+__global__ void __launch_bounds__(I8_THREADS, 2) k_gemm_i8blk(GemmArgs a) {
+    using S = I8Blk<TYPE>;
+    constexpr int BT = 32 * WI * WT;
+    static_assert(32 * (4 / WT) == I8_N, "4 waves cover the workgroup's rows");
+    constexpr int XB = BT * I8_ROW, WB = I8_N * I8_ROW;
+    constexpr int OFF_W = 2 * XB, OFF_EW = OFF_W + 2 * WB, OFF_DX = OFF_EW + 2 * 2 * I8_N * 4;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+    int n0, e = 0;
+    TokMap tm;
+    const int32_t *orow = nullptr;
+    if constexpr (MOE) {
+        const int k = blockIdx.y;
+        if (k >= *a.n_tiles) return;
+        e = a.tile_e[k];
+        const int st = a.tile_start[k];
+        tm = {a.in_rows + st, 0, a.tile_n[k], a.zero_row};
+        orow = a.out_rows + st;
+        n0 = blockIdx.x * I8_N;
+    } else {
+        int tt, rt;
+        xcd_tile(tt, rt, I8_GROUP);
+        tm = {nullptr, tt * BT, BT, a.zero_row};
+        n0 = rt * I8_N;
+    }
+    const int K = a.K, nst = K / 64, nb = K / 32;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wt0 = (wave % WT) * 32 * WI, wn0 = (wave / WT) * 32;
+    auto trow = [&](int j) -> long long {
+        if constexpr (MOE) return tm.rows[j < tm.n ? j : 0];
+        const int t = tm.base + j;
+        return t < a.T ? t : a.T - 1;
+    };
+    const int wr = n0 + (tid >> 2);
+    const uint8_t *wrow = a.W + ((long long)e * a.N + (wr < a.N ? wr : a.N - 1)) * a.row_bytes;
+    constexpr int XR = BT / 64;
+    const int8_t *xsrc[XR];
+#pragma unroll
+    for (int i = 0; i < XR; ++i) xsrc[i] = a.xq + trow((tid >> 2) + 64 * i) * K + 16 * (tid & 3);
+    // token scales: thread t < 2 BT stages block t / BT of the stage for token t % BT
+    const bool don = tid < 2 * BT;
+    const float *dsrc = a.dx + trow(tid % BT) * nb + (tid / BT);
+
+    struct Pre {
+        typename S::Raw raw;
+        uint4 xv[XR];
+        float dv;
+    };
+    Pre P0, P1;
+    auto issue = [&](Pre &p, int st) {
+        S::load(wrow, 2 * st, p.raw);
+#pragma unroll
+        for (int i = 0; i < XR; ++i) p.xv[i] = *(const uint4 *)(xsrc[i] + 64 * st);
+        if (don) p.dv = dsrc[2 * st];
+    };
+    auto commit = [&](auto cc, const Pre &p) {
+        constexpr int buf = decltype(cc)::value;
+        int8_t *sx = (int8_t *)smem + buf * XB;
+#pragma unroll
+        for (int i = 0; i < XR; ++i) *(uint4 *)(sx + ((tid >> 2) + 64 * i) * I8_ROW + 16 * (tid & 3)) = p.xv[i];
+        BDst o;
+        o.w = (int8_t *)smem + OFF_W + buf * WB;
+        o.ew = (float *)(smem + OFF_EW) + buf * 2 * I8_N;
+        S::store(p.raw, o);
+        if (don) ((float *)(smem + OFF_DX))[buf * 2 * BT + tid] = p.dv;  // [buf][block][token]
+    };
+
+    v16f acc[WI];
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+    const int fr = lane & 31, fh = 16 * (lane >> 5);
+
+    // stage st (blocks 2 st, 2 st + 1): per block and tile a fresh MFMA, then y += (e_w d_x) dot
+    auto compute = [&](auto cc, int st) {
+        constexpr int buf = decltype(cc)::value;
+        const int8_t *sx = (const int8_t *)smem + buf * XB, *sw = (const int8_t *)smem + OFF_W + buf * WB;
+        const float *ew = (const float *)(smem + OFF_EW) + buf * 2 * I8_N;
+        const float *dx = (const float *)(smem + OFF_DX) + buf * 2 * BT;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int kk = 32 * b + fh;
+            const v4i fb = *(const v4i *)(sw + (wn0 + fr) * I8_ROW + kk);
+            const float e_w = ew[b * I8_N + wn0 + fr];
+#pragma unroll
+            for (int i = 0; i < WI; ++i) {
+                const v4i fa = *(const v4i *)(sx + (wt0 + 32 * i + fr) * I8_ROW + kk);
+                const v16i z = {};
+                const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fb, z, 0, 0, 0);
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int t0 = wt0 + 32 * i + 8 * g + 4 * (lane >> 5);
+                    const float4 x4 = *(const float4 *)(dx + b * BT + t0);
+                    const float xr[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int r = 4 * g + q;
+                        if constexpr (CAP) {
+                            const int tt = t0 + q, n = n0 + wn0 + fr;
+                            long long t = -1;
+                            if constexpr (MOE) t = tt < tm.n ? orow[tt] : -1;
+                            else t = tm.base + tt < a.T ? tm.base + tt : -1;
+                            if (t >= 0 && n < a.N) a.cap[(t * a.N + n) * nb + 2 * st + b] = d[r];
+                        }
+                        acc[i][r] = __builtin_fmaf(e_w * xr[q], (float)d[r], acc[i][r]);
+                    }
+                }
+            }
+        }
+    };
+
+    // stage st: issue st + 2 (set st & 1), compute st, commit st + 1 (set (st + 1) & 1), barrier
+    auto step = [&](auto cc, int st) {
+        constexpr int c = decltype(cc)::value;
+        Pre &pi = pick2<c>(P0, P1);
+        Pre &pc = pick2<1 - c>(P0, P1);
+        if (st + 2 < nst) issue(pi, st + 2);
+        compute(cc, st);
+        if (st + 1 < nst) commit(IC<1 - c>{}, pc);
+        __syncthreads();
+    };
+
+    issue(P0, 0);
+    if (nst > 1) issue(P1, 1);
+    commit(IC<0>{}, P0);
+    __syncthreads();
+    for (int st = 0; st < nst; st += 2) {
+        step(IC<0>{}, st);
+        if (st + 1 < nst) step(IC<1>{}, st + 1);
+    }
+
+    const float sc = a.es ? a.es[e] : a.osc;
+    const int n = n0 + wn0 + fr;
+    if (n < a.N) {
+#pragma unroll
+        for (int i = 0; i < WI; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int tt = wt0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                long long yrow;
+                if constexpr (MOE) {
+                    if (tt >= tm.n) continue;
+                    yrow = (long long)orow[tt] * a.N;
+                } else {
+                    const int t = tm.base + tt;
+                    if (t >= a.T) continue;
+                    yrow = (long long)t * a.ldy;
+                }
+                a.y[yrow + n] = acc[i][r] * sc;
+            }
+    }
+}
+
 // ---------------------------------------------------------------- host side
 
 bool gemm_i8kq_supported(int type) {
-    return type == TY_Q4_K || type == TY_Q5_K || type == TY_Q6_K || type == TY_IQ4_XS;
+    return type == TY_Q4_K || type == TY_Q5_K || type == TY_Q6_K || type == TY_IQ4_XS || type == TY_Q8_0 ||
+           type == TY_MXFP4;
 }
 
 int gemm_i8kq_token_tile(bool moe) { return moe ? I8Geo<1, 2>::BT : I8Geo<2, 2>::BT; }
@@ -537,6 +770,23 @@ static hipError_t launch_i8kq_type(const GemmArgs &a, dim3 grid, hipStream_t str
                  : launch_i8kq_t<TYPE, 2, 2, false, false>(a, grid, stream);
 }
 
+template <int TYPE, int WI, int WT, bool MOE, bool CAP>
+static hipError_t launch_i8blk_t(const GemmArgs &a, dim3 grid, hipStream_t stream) {
+    constexpr int BT = 32 * WI * WT;
+    constexpr int BYTES = 2 * BT * I8_ROW + 2 * I8_N * I8_ROW + 2 * 2 * I8_N * 4 + 2 * 2 * BT * 4;
+    hipLaunchKernelGGL((k_gemm_i8blk<TYPE, WI, WT, MOE, CAP>), grid, dim3(I8_THREADS), BYTES, stream, a);
+    return hipGetLastError();
+}
+
+template <int TYPE>
+static hipError_t launch_i8blk_type(const GemmArgs &a, dim3 grid, hipStream_t stream) {
+    if (a.n_tiles)
+        return a.cap ? launch_i8blk_t<TYPE, 1, 2, true, true>(a, grid, stream)
+                     : launch_i8blk_t<TYPE, 1, 2, true, false>(a, grid, stream);
+    return a.cap ? launch_i8blk_t<TYPE, 2, 2, false, true>(a, grid, stream)
+                 : launch_i8blk_t<TYPE, 2, 2, false, false>(a, grid, stream);
+}
+
 // grid: dense (token tiles of gemm_i8kq_token_tile(false), row tiles of I8_N); MoE (row tiles, tiles)
 hipError_t launch_gemm_i8kq(int type, const GemmArgs &a, dim3 grid, hipStream_t stream) {
     switch (type) {
@@ -544,6 +794,8 @@ hipError_t launch_gemm_i8kq(int type, const GemmArgs &a, dim3 grid, hipStream_t 
     case TY_Q5_K: return launch_i8kq_type<TY_Q5_K>(a, grid, stream);
     case TY_Q6_K: return launch_i8kq_type<TY_Q6_K>(a, grid, stream);
     case TY_IQ4_XS: return launch_i8kq_type<TY_IQ4_XS>(a, grid, stream);
+    case TY_Q8_0: return launch_i8blk_type<TY_Q8_0>(a, grid, stream);
+    case TY_MXFP4: return launch_i8blk_type<TY_MXFP4>(a, grid, stream);
     }
     return hipErrorInvalidDeviceFunction;
 }

@@ -461,7 +461,9 @@ __global__ void __launch_bounds__(GK_THREADS, 2) k_gemm_kq(GemmArgs a) {
 
 // ---------------------------------------------------------------- host launchers
 
-int gemm_cap_unit(int type) { return gemm_kquant(type) ? 256 : 0; }
+// values per captured integer: the int8 K-quant GEMM's super-block isum, the per-block GEMM's block dot (Q8_0,
+// MXFP4); the split GEMM (ROCmFP4, FAST, NVFP4) forms no integer sums
+int gemm_cap_unit(int type) { return gemm_kquant(type) ? 256 : type == TY_Q8_0 || type == TY_MXFP4 ? 32 : 0; }
 
 bool gemm_kquant(int type) { return type == TY_Q4_K || type == TY_Q5_K || type == TY_Q6_K || type == TY_IQ4_XS; }
 

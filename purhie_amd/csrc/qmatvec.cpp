@@ -133,21 +133,23 @@ hipError_t tokens_prep(int type, const qmatvec_q8 *q, int T, int K, int rows, To
     return launch_act_f16(type, q->q0, q->d0, T, K, rows - 1, w.xh, w.dx, stream);
 }
 
-// The K-quant GEMM: the int8-MFMA kernel of gemm_i8.hip, which reads the Q8_K activation in place, or the fp16
-// one of gemm_k.hip (PURHIE_KQ_GEMM=fp16, read once: kept for comparison)
+// The int8-MFMA GEMMs of gemm_i8.hip (K-quants, Q8_0, MXFP4), which read the quantized activation in place, or
+// the fp16 ones of gemm_k.hip / gemm.hip (PURHIE_I8_GEMM=0, read once: kept for comparison)
 bool kq_int8(int type) {
-    static const bool fp16 = getenv("PURHIE_KQ_GEMM") && strcmp(getenv("PURHIE_KQ_GEMM"), "fp16") == 0;
-    return !fp16 && gemm_i8kq_supported(type);
+    static const bool off = getenv("PURHIE_I8_GEMM") && getenv("PURHIE_I8_GEMM")[0] == '0';
+    return !off && gemm_i8kq_supported(type);
 }
 
-// the int8 K-quant GEMM's arguments for the activation q (no staging: it is read where it is)
-GemmArgs i8kq_args(const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N, int K) {
+// the int8 GEMM's arguments for the activation q (no staging: Q8_K for the K-quants, Q8_0 otherwise, read where
+// it is)
+GemmArgs i8kq_args(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N, int K) {
     GemmArgs a{};
     a.W = (const uint8_t *)W;
     a.row_bytes = (long long)row_bytes;
-    a.xq = q->qK;
-    a.dx = q->dK;
-    a.xsum = q->bsK;
+    const bool kq = reads_q8k(type);
+    a.xq = kq ? q->qK : q->q0;
+    a.dx = kq ? q->dK : q->d0;
+    a.xsum = kq ? q->bsK : nullptr;
     a.y = y;
     a.N = N;
     a.K = K;
@@ -167,11 +169,11 @@ int gemm_k_mult(int type) {
 hipError_t gemm_dense(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, long long ldy, int N,
                       int K, int T, hipStream_t stream) {
     if (kq_int8(type)) {
-        GemmArgs a = i8kq_args(W, row_bytes, q, y, N, K);
+        GemmArgs a = i8kq_args(type, W, row_bytes, q, y, N, K);
         a.ldy = ldy;
         a.T = T;
         a.osc = dense_scale(W);
-        if (const hipError_t e = cap_for((long long)T * N * (K / 256), a.cap); e != hipSuccess) return e;
+        if (const hipError_t e = cap_for((long long)T * N * (K / gemm_cap_unit(type)), a.cap); e != hipSuccess) return e;
         const int BT = gemm_i8kq_token_tile(false);
         const int RN = gemm_i8kq_rows();
         return launch_gemm_i8kq(type, a, dim3((unsigned)((T + BT - 1) / BT), (unsigned)((N + RN - 1) / RN)), stream);
@@ -596,7 +598,7 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
         return launch_matvec_id(type, a, stream);
     }
     if (kq_int8(type)) {  // the activation read in place: input rows are in_rows[] of q
-        GemmArgs a = i8kq_args(W, row_bytes, q, y, N, K);
+        GemmArgs a = i8kq_args(type, W, row_bytes, q, y, N, K);
         a.n_tiles = n_tiles;
         a.tile_e = tile_e;
         a.tile_start = tile_start;

@@ -215,12 +215,16 @@ def test_kquant_gemm_isum(Q, oracle, t, N, K, T):
 
 
 def test_capture_units(Q):
-    """the group each decode capture holds is the weight scale's, and the GEMMs without integer sums (the split
-    GEMM of ROCmFP4 / FAST / NVFP4: exact fp16 operands chained through K) say so"""
+    """the group each decode capture holds is the weight scale's; the GEMMs' units: a K-quant super-block, a Q8_0 /
+    MXFP4 block, and none for the split GEMM of ROCmFP4 / FAST / NVFP4 (exact fp16 operands chained through K)"""
     for t, g in {8: 32, 100: 16, 101: 32, 12: 32, 13: 32, 14: 16, 23: 32, 39: 32, 40: 16}.items():
         assert Q.capture_unit(t) == g
     for t in KQ:
         assert Q.capture_unit(t, gemm=True) == 256
+    for t in (8, 39):
+        assert Q.capture_unit(t, gemm=True) == 32
+    for t in (100, 101, 40):
+        assert Q.capture_unit(t, gemm=True) == 0
     assert Q.capture_unit(1) == 0
 
 
@@ -238,3 +242,26 @@ def test_capture_capacity_error(Q):
         rc = L.qmatvec_launch_q8(t, C.c_void_p(dev(W).data_ptr()), Q.row_size(t, K), q.ref, C.c_void_p(y.data_ptr()),
                                  N, K, None)
     assert rc == 1
+
+
+@pytest.mark.parametrize("t,N,K,T", [(8, 300, 1024, 150), (8, 2048, 2048, 40), (39, 256, 2048, 70)])
+def test_block_gemm_dots(Q, oracle, t, N, K, T):
+    """the per-block int8 GEMM (Q8_0, MXFP4; prefill mode): each 32-value block's exact int32 dot, the integer its
+    epilogue scales by e_w d_x"""
+    import torch
+    assert Q.capture_unit(t, gemm=True) == 32
+    W = rand_rows(Q, t, N, K, 81 + t)
+    x = acts(82 + T, T, K)
+    q = quantized(Q, x)
+    cap = cap_buf(T * N * (K // 32))
+    y = torch.zeros((T, N), device="cuda")
+    Q.lib().qmatvec_set_prefill(1)
+    try:
+        with Q.capture(cap):
+            Q.launch_q8_batch(t, dev(W), q, y, N, N, K, T)
+    finally:
+        Q.lib().qmatvec_set_prefill(0)
+    got = host(cap).reshape(T, N, K // 32)
+    for i in range(T):
+        a = oracle.quantize_act(x[i], False)
+        assert np.array_equal(got[i], oracle.block_dots(t, W, N, K, a["q"])), f"token {i}"
