@@ -218,12 +218,11 @@ __device__ inline void xcd_tile(int &tt, int &rt, int group) {
     rt = w / gn;
 }
 
-// Token rows of a GEMM tile: dense tiles take rows base .. base + tile - 1 of the pre-pass output; MoE tiles take
-// their entries' input rows, and the zero row past the last entry
+// Token rows of a GEMM tile: dense tiles take rows base .. base + n - 1 of the activation; MoE tiles take their n
+// entries' input rows
 struct TokMap {
     const int32_t *rows;  // MoE: in_rows + tile_start (null: dense)
-    int base, n, zero_row;
-    __device__ int row(int j) const { return rows ? (j < n ? rows[j] : zero_row) : base + j; }
+    int base, n;
 };
 
 }  // namespace pq

@@ -176,13 +176,13 @@ __device__ __forceinline__ ff4 mfma16(const uint4 a, const uint4 b, ff4 c) {
                                                        0);
 }
 
-// the activations xh: 16-bit values of the weight type. Wave w computes weight rows 64 (w & 1) .. + 63 x tokens
-// 64 (w >> 1) .. + 63 (4 x 4 MFMA tiles). (A 256 x 128 tile with 128 x 64 waves reads fewer LDS bytes per MFMA
-// but was slower: half the workgroups, and one weight row per thread coalesces badly; measured 99 -> 154 us on
-// 4096 x 4096 x 2048.)
-template <int TYPE>
+// the activations: xh, 16-bit values of the weight type, or (XF) the fp32 x, rounded to them while staging. Wave w
+// computes weight rows 64 (w & 1) .. + 63 x tokens 64 (w >> 1) .. + 63 (4 x 4 MFMA tiles). (A 256 x 128 tile with
+// 128 x 64 waves reads fewer LDS bytes per MFMA but was slower: half the workgroups, and one weight row per thread
+// coalesces badly; measured 99 -> 154 us on 4096 x 4096 x 2048.)
+template <int TYPE, bool XF>
 __global__ void __launch_bounds__(256, 2) k_gemm_float(const uint8_t *__restrict__ W, long long rb,
-                                                       const uint16_t *__restrict__ xh, float *__restrict__ y, int N,
+                                                       const void *__restrict__ xv, float *__restrict__ y, int N,
                                                        int K, int T) {
     __shared__ __attribute__((aligned(16))) uint16_t sW[GF_N * GF_ROW];
     __shared__ __attribute__((aligned(16))) uint16_t sX[GF_T * GF_ROW];
@@ -201,15 +201,24 @@ __global__ void __launch_bounds__(256, 2) k_gemm_float(const uint8_t *__restrict
     const int sr = tid >> 1, sp = 32 * (tid & 1);
     const bool wok = n0 + sr < N, xok = t0 + sr < T;
     const uint8_t *wsrc = W + (long long)(wok ? n0 + sr : 0) * rb + 2 * sp;
-    const uint16_t *hsrc = xh + (long long)(xok ? t0 + sr : 0) * K + sp;
+    const long long xoff = (long long)(xok ? t0 + sr : 0) * K + sp;
+    const uint16_t *hsrc = (const uint16_t *)xv + xoff;
+    const float *fsrc = (const float *)xv + xoff;
 
     uint4 gw[4], gx[4];
+    float4 fx[XF ? 8 : 1];
     auto issue = [&](int k0) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const bool in = k0 + sp + 8 * c < K;
             gw[c] = wok && in ? *(const uint4 *)(wsrc + 2 * (long long)(k0 + 8 * c)) : make_uint4(0, 0, 0, 0);
-            gx[c] = xok && in ? *(const uint4 *)(hsrc + k0 + 8 * c) : make_uint4(0, 0, 0, 0);
+            if constexpr (XF) {
+                const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                fx[2 * c] = xok && in ? *(const float4 *)(fsrc + k0 + 8 * c) : z;
+                fx[2 * c + 1] = xok && in ? *(const float4 *)(fsrc + k0 + 8 * c + 4) : z;
+            } else {
+                gx[c] = xok && in ? *(const uint4 *)(hsrc + k0 + 8 * c) : make_uint4(0, 0, 0, 0);
+            }
         }
     };
 
@@ -227,7 +236,15 @@ __global__ void __launch_bounds__(256, 2) k_gemm_float(const uint8_t *__restrict
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             dw[c] = gw[c];
-            dx[c] = gx[c];
+            if constexpr (XF) {
+                const float4 a = fx[2 * c], b = fx[2 * c + 1];
+                dx[c] = make_uint4(bits16<TYPE>(a.x) | bits16<TYPE>(a.y) << 16,
+                                   bits16<TYPE>(a.z) | bits16<TYPE>(a.w) << 16,
+                                   bits16<TYPE>(b.x) | bits16<TYPE>(b.y) << 16,
+                                   bits16<TYPE>(b.z) | bits16<TYPE>(b.w) << 16);
+            } else {
+                dx[c] = gx[c];
+            }
         }
         __syncthreads();
         if (k0 + GF_K < K) issue(k0 + GF_K);  // next stage's loads in flight during the MFMAs
@@ -287,12 +304,11 @@ hipError_t mv_float_t(const uint8_t *W, long long rb, const float *x, float *y, 
     return hipGetLastError();
 }
 
-template <int TYPE>
-hipError_t gemm_float_t(const uint8_t *W, long long rb, const uint16_t *xh, float *y, int N, int K, int T,
-                        hipStream_t s) {
+template <int TYPE, bool XF>
+hipError_t gemm_float_t(const uint8_t *W, long long rb, const void *x, float *y, int N, int K, int T, hipStream_t s) {
     const long long n = (long long)((N + GF_N - 1) / GF_N) * ((T + GF_T - 1) / GF_T);
     if (n > 0x7fffffffLL) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_gemm_float<TYPE>, dim3((unsigned)n), dim3(256), 0, s, W, rb, xh, y, N, K, T);
+    hipLaunchKernelGGL((k_gemm_float<TYPE, XF>), dim3((unsigned)n), dim3(256), 0, s, W, rb, x, y, N, K, T);
     return hipGetLastError();
 }
 
@@ -313,8 +329,17 @@ hipError_t launch_mv_float(int type, bool round, const uint8_t *W, long long rb,
 hipError_t launch_gemm_float(int type, const uint8_t *W, long long rb, const uint16_t *xh, float *y, int N, int K,
                              int T, hipStream_t stream) {
     switch (type) {
-    case QT_F16_: return gemm_float_t<QT_F16_>(W, rb, xh, y, N, K, T, stream);
-    case QT_BF16_: return gemm_float_t<QT_BF16_>(W, rb, xh, y, N, K, T, stream);
+    case QT_F16_: return gemm_float_t<QT_F16_, false>(W, rb, xh, y, N, K, T, stream);
+    case QT_BF16_: return gemm_float_t<QT_BF16_, false>(W, rb, xh, y, N, K, T, stream);
+    }
+    return hipErrorInvalidDeviceFunction;
+}
+
+hipError_t launch_gemm_float_x(int type, const uint8_t *W, long long rb, const float *x, float *y, int N, int K,
+                               int T, hipStream_t stream) {
+    switch (type) {
+    case QT_F16_: return gemm_float_t<QT_F16_, true>(W, rb, x, y, N, K, T, stream);
+    case QT_BF16_: return gemm_float_t<QT_BF16_, true>(W, rb, x, y, N, K, T, stream);
     }
     return hipErrorInvalidDeviceFunction;
 }

@@ -35,7 +35,6 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef short s2 __attribute__((ext_vector_type(2)));
 
-constexpr int I8_S = 64;       // K per stage
 constexpr int I8_ROW = 80;     // LDS bytes per row of a stage (64 + 16: conflict-free 16-byte fragment reads)
 constexpr int I8_N = 64;       // weight rows per workgroup
 constexpr int I8_THREADS = 256;
@@ -291,13 +290,13 @@ __global__ void __launch_bounds__(I8_THREADS, 2) k_gemm_i8kq(GemmArgs a) {
         if (k >= *a.n_tiles) return;
         e = a.tile_e[k];
         const int st = a.tile_start[k];
-        tm = {a.in_rows + st, 0, a.tile_n[k], a.zero_row};
+        tm = {a.in_rows + st, 0, a.tile_n[k]};
         orow = a.out_rows + st;
         n0 = blockIdx.x * I8_N;
     } else {              // grid (token tiles, row tiles), renumbered XCD by XCD
         int tt, rt;
         xcd_tile(tt, rt, I8_GROUP);
-        tm = {nullptr, tt * BT, BT, a.zero_row};
+        tm = {nullptr, tt * BT, BT};
         n0 = rt * I8_N;
     }
     const int K = a.K, nsb = K / 256;
@@ -598,13 +597,13 @@ __global__ void __launch_bounds__(I8_THREADS, 2) k_gemm_i8blk(GemmArgs a) {
         if (k >= *a.n_tiles) return;
         e = a.tile_e[k];
         const int st = a.tile_start[k];
-        tm = {a.in_rows + st, 0, a.tile_n[k], a.zero_row};
+        tm = {a.in_rows + st, 0, a.tile_n[k]};
         orow = a.out_rows + st;
         n0 = blockIdx.x * I8_N;
     } else {
         int tt, rt;
         xcd_tile(tt, rt, I8_GROUP);
-        tm = {nullptr, tt * BT, BT, a.zero_row};
+        tm = {nullptr, tt * BT, BT};
         n0 = rt * I8_N;
     }
     const int K = a.K, nst = K / 64, nb = K / 32;
@@ -741,6 +740,13 @@ __global__ void __launch_bounds__(I8_THREADS, 2) k_gemm_i8blk(GemmArgs a) {
 bool gemm_i8kq_supported(int type) {
     return type == TY_Q4_K || type == TY_Q5_K || type == TY_Q6_K || type == TY_IQ4_XS || type == TY_Q8_0 ||
            type == TY_MXFP4;
+}
+
+int gemm_supported(int type) { return gemm_i8kq_supported(type) || gemm_split(type); }
+
+int gemm_cap_unit(int type) {
+    if (type == TY_Q4_K || type == TY_Q5_K || type == TY_Q6_K || type == TY_IQ4_XS) return 256;
+    return type == TY_Q8_0 || type == TY_MXFP4 ? 32 : 0;
 }
 
 int gemm_i8kq_token_tile(bool moe) { return moe ? I8Geo<1, 2>::BT : I8Geo<2, 2>::BT; }

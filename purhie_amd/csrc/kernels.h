@@ -81,26 +81,21 @@ hipError_t launch_matvec_id_tile(int type, const MvIdArgs &a, hipStream_t stream
 hipError_t launch_block_dots(int type, const uint8_t *W, long long row_bytes, const int8_t *q, int32_t *out, int N,
                              int K, hipStream_t stream);
 
-// Prefill GEMM (fp16 MFMA on exactly decoded operands). Token operand: xh [rows][K] fp16 and dx
-// [rows][K / 32] from launch_act_f16 (row zero_row all zero); dense tiles (n_tiles null) or MoE tiles.
+// Prefill GEMM over the quantized activation, read in place: dense tiles (n_tiles null) or MoE expert tiles.
 struct GemmArgs {
     const uint8_t *W;       // dense: the matrix; MoE: stacked experts
     long long row_bytes;
-    const _Float16 *xh;     // token operand [rows][K] (pre-pass); split GEMM: the hi plane
-    const float *dx;        // block scales [rows][K / 32] (per-block GEMM)
-    const int8_t *xq;       // split GEMM: int8 token rows in the GEMM's K order [rows][K]
-    const _Float16 *xs;     // split GEMM: their block scales dx 2^s [rows][K / 32]
-    const float *ts;        // split GEMM: per-row output factor 2^-s
-    const _Float16 *xb;     // K-quant GEMM: the token's 16-value group sums [rows][K / 16] (dx: dK [rows][K / 256])
-    const int32_t *xsum;    // int8 K-quant GEMM: the Q8_K 16-value sums [rows][K / 16] (xq: qK, dx: dK, read in place)
+    const int8_t *xq;       // int8 activation rows [rows][K]: Q8_K's qK for the K-quants, Q8_0's q0 otherwise
+    const float *dx;        // their scales: dK [rows][K / 256] or d0 [rows][K / 32]
+    const int32_t *xsum;    // K-quants: the Q8_K 16-value sums [rows][K / 16]
     float *y;
     long long ldy;
-    int N, K, T, zero_row;
+    int N, K, T;
     float osc;
     // MoE tiles (n_tiles null: dense)
     const int32_t *n_tiles, *tile_e, *tile_start, *tile_n, *in_rows, *out_rows;
     const float *es;        // per-expert output scales (null: osc)
-    int tt;                 // split GEMM, dense: tokens per workgroup (128, or 64 for short prompts)
+    int tt;                 // split GEMM, dense: tokens per workgroup (gemm_split_token_tile)
     // capture mode (null: off; the integer-exact GEMMs): the exact integer each epilogue scales, per token (dense:
     // t; tiles: the entry's output row) and weight row: cap[(t * N + row) * (K / U) + unit], U = gemm_cap_unit(type)
     int32_t *cap;
@@ -109,38 +104,29 @@ struct GemmArgs {
 int gemm_supported(int type);
 // values per integer the type's GEMM exposes in capture mode (0: its sums are not integers, none captured)
 int gemm_cap_unit(int type);
-int gemm_k_multiple();
-int gemm_token_tile();
-int gemm_id_token_tile(int type);  // the largest MoE expert tile the type's GEMM takes
-int gemm_dense_token_tile(int type, int T);  // tokens per workgroup of the dense GEMM for T tokens
-hipError_t launch_act_f16(int type, const int8_t *q, const float *d, int T, int K, int Tpad, _Float16 *xh, float *dxp,
-                          hipStream_t stream);
-hipError_t launch_gemm(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);
-// the split-activation GEMM (ROCmFP4, FAST): pre-pass of `rows` rows (T real, the rest zero) and the kernel
+// the split-activation GEMM (gemm_split.hip: ROCmFP4, ROCmFP4_FAST, NVFP4; Q8_0 activation, xq = q0, dx = d0):
+// dense grid (tokens / gemm_split_token_tile(false, T), rows / gemm_split_rows()), MoE grid (rows /
+// gemm_split_rows(), tiles) with tiles of up to gemm_split_token_tile(true, 0) entries; K a multiple of
+// gemm_split_k_multiple()
 bool gemm_split(int type);
 int gemm_split_k_multiple();
-int gemm_rows_per_wg(int type);  // weight rows per GEMM workgroup (token tiles: gemm_token_tile())
-hipError_t launch_act_split(int type, const int8_t *q, const float *d, int T, int K, int rows, int8_t *xq,
-                            _Float16 *xs, float *ts, hipStream_t stream);
+int gemm_split_rows();
+int gemm_split_token_tile(bool moe, int T);
 hipError_t launch_gemm_split(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);
 
 // Float activations over F32 / F16 / BF16 weights (type ids 0, 1, 30): the decode matvec for T tokens (round:
 // the activations rounded to the 16-bit weight type), the F16 / BF16 MFMA GEMM on activations rounded to 16 bits
-// (xh), and that rounding (n % 8 == 0)
+// (xh; or x itself, rounded while staging: launch_gemm_float_x), and that rounding (n % 8 == 0)
 hipError_t launch_mv_float(int type, bool round, const uint8_t *W, long long rb, const float *x, float *y, int N, int K,
                            int T, hipStream_t stream);
 hipError_t launch_gemm_float(int type, const uint8_t *W, long long rb, const uint16_t *xh, float *y, int N, int K,
                              int T, hipStream_t stream);
+hipError_t launch_gemm_float_x(int type, const uint8_t *W, long long rb, const float *x, float *y, int N, int K,
+                               int T, hipStream_t stream);
 hipError_t launch_round_half(int type, const float *x, uint16_t *xh, long long n, hipStream_t stream);
-// the K-quant GEMM (Q4_K, Q6_K): pre-pass of the Q8_K activation (`rows` rows, T real) and the kernel
-bool gemm_kquant(int type);
-constexpr int GEMM_KQ_ROWS = 128;  // weight rows per K-quant GEMM workgroup
-hipError_t launch_act_q8k(const int8_t *q, const float *dK, const int32_t *bs, int T, int K, int rows, _Float16 *xh,
-                          _Float16 *xb, float *xd, hipStream_t stream);
-hipError_t launch_gemm_kquant(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);
-// the int8-MFMA K-quant GEMM (gemm_i8.hip): the Q8_K activation read in place (xq = qK, dx = dK, xsum = bsK);
-// dense grid (tokens / gemm_i8kq_token_tile(false), rows / gemm_i8kq_rows()), MoE grid (rows / gemm_i8kq_rows(), tiles) with
-// tiles of up to gemm_i8kq_token_tile(true) entries
+// the int8-MFMA GEMM (gemm_i8.hip: Q4_K, Q5_K, Q6_K, IQ4_XS with the Q8_K activation, xq = qK, dx = dK, xsum =
+// bsK; Q8_0, MXFP4 with the Q8_0 one, xq = q0, dx = d0): dense grid (tokens / gemm_i8kq_token_tile(false), rows /
+// gemm_i8kq_rows()), MoE grid (rows / gemm_i8kq_rows(), tiles) with tiles of up to gemm_i8kq_token_tile(true) entries
 bool gemm_i8kq_supported(int type);
 int gemm_i8kq_token_tile(bool moe);
 int gemm_i8kq_rows();  // weight rows per workgroup

@@ -92,57 +92,9 @@ bool mfma_on() {
 // expert tiles in the decode order: the tile the engine's grouping may use there (the reference's QMV_MM_TB)
 constexpr int ID_DECODE_TILE = 16;
 
-size_t align16z(size_t n) { return (n + 15) & ~(size_t)15; }
-
-// The GEMM's token operand in a stream-ordered allocation (freed on the same stream after the GEMM): for
-// ROCmFP4 / FAST the int8 rows in the GEMM's K order, their block scales times the row's power of two (fp16) and
-// the per-row factors; for Q8_0 the int8 rows as fp16 and
-// their block scales; for Q4_K / Q6_K the Q8_K rows as fp16, their group sums as fp16 and dK. `rows` rows are
-// converted (the first T from q, the rest zero: padding and the zero row MoE tiles point past their entries).
-struct TokWs {
-    void *mem = nullptr;
-    _Float16 *xh = nullptr, *xb = nullptr, *xs = nullptr;
-    int8_t *xq = nullptr;
-    float *dx = nullptr, *ts = nullptr;
-};
-
-hipError_t tokens_prep(int type, const qmatvec_q8 *q, int T, int K, int rows, TokWs &w, hipStream_t stream) {
-    const size_t plane = align16z((size_t)rows * K * 2);
-    if (gemm_kquant(type)) {
-        const size_t sums = align16z((size_t)rows * (K / 16) * 2);
-        hipError_t e = hipMallocAsync(&w.mem, plane + sums + (size_t)rows * (K / 256) * 4, stream);
-        if (e != hipSuccess) return e;
-        w.xh = (_Float16 *)w.mem;
-        w.xb = (_Float16 *)((char *)w.mem + plane);
-        w.dx = (float *)((char *)w.mem + plane + sums);
-        return launch_act_q8k(q->qK, q->dK, q->bsK, T, K, rows, w.xh, w.xb, w.dx, stream);
-    }
-    if (gemm_split(type)) {
-        const size_t vals = align16z((size_t)rows * K), scales = align16z((size_t)rows * (K / 32) * 2);
-        hipError_t e = hipMallocAsync(&w.mem, vals + scales + (size_t)rows * 4, stream);
-        if (e != hipSuccess) return e;
-        w.xq = (int8_t *)w.mem;
-        w.xs = (_Float16 *)((char *)w.mem + vals);
-        w.ts = (float *)((char *)w.mem + vals + scales);
-        return launch_act_split(type, q->q0, q->d0, T, K, rows, w.xq, w.xs, w.ts, stream);
-    }
-    hipError_t e = hipMallocAsync(&w.mem, plane + (size_t)rows * (K / 32) * 4, stream);
-    if (e != hipSuccess) return e;
-    w.xh = (_Float16 *)w.mem;
-    w.dx = (float *)((char *)w.mem + plane);
-    return launch_act_f16(type, q->q0, q->d0, T, K, rows - 1, w.xh, w.dx, stream);
-}
-
-// The int8-MFMA GEMMs of gemm_i8.hip (K-quants, Q8_0, MXFP4), which read the quantized activation in place, or
-// the fp16 ones of gemm_k.hip / gemm.hip (PURHIE_I8_GEMM=0, read once: kept for comparison)
-bool kq_int8(int type) {
-    static const bool off = getenv("PURHIE_I8_GEMM") && getenv("PURHIE_I8_GEMM")[0] == '0';
-    return !off && gemm_i8kq_supported(type);
-}
-
-// the int8 GEMM's arguments for the activation q (no staging: Q8_K for the K-quants, Q8_0 otherwise, read where
-// it is)
-GemmArgs i8kq_args(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N, int K) {
+// The GEMM's arguments for the activation q, read where it is: Q8_K (qK, dK, bsK) for the K-quants, Q8_0 (q0, d0)
+// for the others
+GemmArgs gemm_args(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N, int K) {
     GemmArgs a{};
     a.W = (const uint8_t *)W;
     a.row_bytes = (long long)row_bytes;
@@ -156,60 +108,26 @@ GemmArgs i8kq_args(int type, const void *W, size_t row_bytes, const qmatvec_q8 *
     return a;
 }
 
-hipError_t gemm_launch(int type, const GemmArgs &a, dim3 grid, hipStream_t stream) {
-    if (gemm_kquant(type)) return launch_gemm_kquant(type, a, grid, stream);
-    return gemm_split(type) ? launch_gemm_split(type, a, grid, stream) : launch_gemm(type, a, grid, stream);
-}
-
-// K multiple the GEMM of a type needs
+// K multiple the GEMM of a type needs (the int8 per-block GEMM takes 64; 128 keeps the shapes it serves)
 int gemm_k_mult(int type) {
-    return gemm_kquant(type) ? 256 : gemm_split(type) ? gemm_split_k_multiple() : gemm_k_multiple();
+    if (gemm_split(type)) return gemm_split_k_multiple();
+    return type == TY_Q8_0 || type == TY_MXFP4 ? 128 : 256;
 }
 
 hipError_t gemm_dense(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, long long ldy, int N,
                       int K, int T, hipStream_t stream) {
-    if (kq_int8(type)) {
-        GemmArgs a = i8kq_args(type, W, row_bytes, q, y, N, K);
-        a.ldy = ldy;
-        a.T = T;
-        a.osc = dense_scale(W);
-        if (const hipError_t e = cap_for((long long)T * N * (K / gemm_cap_unit(type)), a.cap); e != hipSuccess) return e;
-        const int BT = gemm_i8kq_token_tile(false);
-        const int RN = gemm_i8kq_rows();
-        return launch_gemm_i8kq(type, a, dim3((unsigned)((T + BT - 1) / BT), (unsigned)((N + RN - 1) / RN)), stream);
-    }
-    const int BT = gemm_dense_token_tile(type, T);
-    const int Tpad = (T + BT - 1) / BT * BT;
-    TokWs w;
-    hipError_t e = tokens_prep(type, q, T, K, Tpad + 1, w, stream);
-    if (e == hipSuccess) {
-        GemmArgs a{};
-        a.W = (const uint8_t *)W;
-        a.row_bytes = (long long)row_bytes;
-        a.xh = w.xh;
-        a.dx = w.dx;
-        a.xq = w.xq;
-        a.xs = w.xs;
-        a.xb = w.xb;
-        a.ts = w.ts;
-        a.y = y;
-        a.ldy = ldy;
-        a.N = N;
-        a.K = K;
-        a.T = T;
-        a.zero_row = Tpad;
-        a.osc = dense_scale(W);
+    GemmArgs a = gemm_args(type, W, row_bytes, q, y, N, K);
+    a.ldy = ldy;
+    a.T = T;
+    a.osc = dense_scale(W);
+    if (gemm_split(type)) {
+        const int BT = gemm_split_token_tile(false, T), RN = gemm_split_rows();
         a.tt = BT;
-        if (gemm_cap_unit(type)) e = cap_for((long long)T * N * (K / gemm_cap_unit(type)), a.cap);
-        const int RN = gemm_rows_per_wg(type);
-        if (e == hipSuccess)
-            e = gemm_launch(type, a, dim3((unsigned)(Tpad / BT), (unsigned)((N + RN - 1) / RN)), stream);
+        return launch_gemm_split(type, a, dim3((unsigned)((T + BT - 1) / BT), (unsigned)((N + RN - 1) / RN)), stream);
     }
-    if (w.mem) {
-        const hipError_t f = hipFreeAsync(w.mem, stream);
-        if (e == hipSuccess) e = f;
-    }
-    return e;
+    if (const hipError_t e = cap_for((long long)T * N * (K / gemm_cap_unit(type)), a.cap); e != hipSuccess) return e;
+    const int BT = gemm_i8kq_token_tile(false), RN = gemm_i8kq_rows();
+    return launch_gemm_i8kq(type, a, dim3((unsigned)((T + BT - 1) / BT), (unsigned)((N + RN - 1) / RN)), stream);
 }
 
 }  // namespace
@@ -281,27 +199,18 @@ hipError_t qmatvec_launch_batch(int type, const void *W, size_t row_bytes, const
     return qmatvec_launch_batch_h(type, W, row_bytes, x, nullptr, 0, y, N, K, T, stream);
 }
 
-// F16 / BF16 batches the GEMM takes: x rounded to 16 bits first, into the caller's scratch buffer xh when it holds
-// T K values, else into one from the stream-ordered pool (the GEMM reads 16-bit activations: half the bytes of
-// rounding fp32 ones while staging, measured 2x faster); every other batch through the decode kernel, token by
-// token in its order
+// F16 / BF16 batches the GEMM takes: x rounded to 16 bits first into the caller's scratch buffer xh when it holds
+// T K values (the GEMM then reads 16-bit activations: half the bytes of rounding fp32 ones while staging, measured
+// 2x faster), else the GEMM reading x and rounding it while staging (the reference's matmul_wmma_f, src/qmatvec.cpp:
+// 341-352); every other batch through the decode kernel, token by token in its order. Nothing is allocated.
 hipError_t qmatvec_launch_batch_h(int type, const void *W, size_t row_bytes, const float *x, uint16_t *xh,
                                   size_t xh_bytes, float *y, int N, int K, int T, hipStream_t stream) {
     if (qmatvec_half_supported(type, W, row_bytes, N, K, T) && x && y && al16(x) && (!xh || al16(xh))) {
-        const size_t need = (size_t)T * K * 2;
-        void *own = nullptr;
-        if (!xh || xh_bytes < need) {
-            const hipError_t e = hipMallocAsync(&own, need, stream);
-            if (e != hipSuccess) return e;
-            xh = (uint16_t *)own;
+        if (xh && xh_bytes >= (size_t)T * K * 2) {
+            const hipError_t e = qmatvec_round_half(type, x, xh, (long long)T * K, stream);
+            return e != hipSuccess ? e : qmatvec_launch_batch_hx(type, W, row_bytes, xh, y, N, K, T, stream);
         }
-        hipError_t e = qmatvec_round_half(type, x, xh, (long long)T * K, stream);
-        if (e == hipSuccess) e = qmatvec_launch_batch_hx(type, W, row_bytes, xh, y, N, K, T, stream);
-        if (own) {
-            const hipError_t f = hipFreeAsync(own, stream);
-            if (e == hipSuccess) e = f;
-        }
-        return e;
+        return launch_gemm_float_x(type, (const uint8_t *)W, (long long)row_bytes, x, y, N, K, T, stream);
     }
     return float_rows(type, true, W, row_bytes, x, y, N, K, T, stream);
 }
@@ -560,7 +469,7 @@ static bool id_gemm_ok(int type, int N, int K) {
 // entries; the decode-order path takes the reference's 16 (src/qmatvec.cpp:612-615)
 int qmatvec_id_batch_tile(int type, int N, int K) {
     if (!id_gemm_ok(type, N, K)) return ID_DECODE_TILE;
-    return kq_int8(type) ? gemm_i8kq_token_tile(true) : gemm_id_token_tile(type);
+    return gemm_split(type) ? gemm_split_token_tile(true, 0) : gemm_i8kq_token_tile(true);
 }
 
 hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N,
@@ -597,53 +506,22 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
         a.cap_rows = 0;
         return launch_matvec_id(type, a, stream);
     }
-    if (kq_int8(type)) {  // the activation read in place: input rows are in_rows[] of q
-        GemmArgs a = i8kq_args(type, W, row_bytes, q, y, N, K);
-        a.n_tiles = n_tiles;
-        a.tile_e = tile_e;
-        a.tile_start = tile_start;
-        a.tile_n = tile_n;
-        a.in_rows = in_rows;
-        a.out_rows = out_rows;
-        expert_scale(W, a.es, a.osc);
-        a.cap = g_cap;  // (tiles mode: rows from out_rows; the caller sizes the buffer)
-        const int RN = gemm_i8kq_rows();
-        return launch_gemm_i8kq(type, a, dim3((unsigned)((N + RN - 1) / RN), (unsigned)max_tiles), stream);
+    // the activation read in place: input rows are in_rows[] of q
+    GemmArgs a = gemm_args(type, W, row_bytes, q, y, N, K);
+    a.n_tiles = n_tiles;
+    a.tile_e = tile_e;
+    a.tile_start = tile_start;
+    a.tile_n = tile_n;
+    a.in_rows = in_rows;
+    a.out_rows = out_rows;
+    expert_scale(W, a.es, a.osc);
+    if (gemm_split(type)) {
+        const int RN = gemm_split_rows();
+        return launch_gemm_split(type, a, dim3((unsigned)((N + RN - 1) / RN), (unsigned)max_tiles), stream);
     }
-    // every input row the buffer can hold (in_rows index them) goes through the pre-pass; row `rows` is zero
-    const int rows = q->max_k / K;
-    TokWs w;
-    hipError_t e = tokens_prep(type, q, rows, K, rows + 1, w, stream);
-    if (e == hipSuccess) {
-        GemmArgs a{};
-        a.W = (const uint8_t *)W;
-        a.row_bytes = (long long)row_bytes;
-        a.xh = w.xh;
-        a.dx = w.dx;
-        a.xq = w.xq;
-        a.xs = w.xs;
-        a.xb = w.xb;
-        a.ts = w.ts;
-        a.y = y;
-        a.N = N;
-        a.K = K;
-        a.zero_row = rows;
-        a.n_tiles = n_tiles;
-        a.tile_e = tile_e;
-        a.tile_start = tile_start;
-        a.tile_n = tile_n;
-        a.in_rows = in_rows;
-        a.out_rows = out_rows;
-        expert_scale(W, a.es, a.osc);
-        if (gemm_cap_unit(type)) a.cap = g_cap;  // (tiles mode: rows from out_rows; the caller sizes the buffer)
-        const int RN = gemm_rows_per_wg(type);
-        e = gemm_launch(type, a, dim3((unsigned)((N + RN - 1) / RN), (unsigned)max_tiles), stream);
-    }
-    if (w.mem) {
-        const hipError_t f = hipFreeAsync(w.mem, stream);
-        if (e == hipSuccess) e = f;
-    }
-    return e;
+    a.cap = g_cap;  // (tiles mode: rows from out_rows; the caller sizes the buffer)
+    const int RN = gemm_i8kq_rows();
+    return launch_gemm_i8kq(type, a, dim3((unsigned)((N + RN - 1) / RN), (unsigned)max_tiles), stream);
 }
 
 hipError_t qmatvec_debug_capture(int32_t *out, size_t n_ints) {
