@@ -60,6 +60,21 @@ int purhie_moe_shared_as_slot(const purhie_moe_weights *w, int T);
 hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qmatvec_q8 *q8_xn, int T, float *out,
                           void *ws, size_t ws_bytes, hipStream_t stream);
 
+/* Bytes of the static workspace purhie_moe_ffn_noalloc uses on each GPU (32 MiB). */
+#define PURHIE_MOE_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* purhie_moe_ffn with the library's own workspace instead of the caller's. No counterpart in the reference: for
+ * callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The workspace is a static device array of PURHIE_MOE_SCRATCH_BYTES on each GPU, held from the library's load
+ * until the process ends; its address is looked up once per device, on the first call with that device current.
+ * Returns hipErrorInvalidValue when purhie_moe_workspace_bytes(w, T) exceeds PURHIE_MOE_SCRATCH_BYTES (at n_embd
+ * 2048, 128 experts of n_ff_exp 768, top 8, no shared expert: above 215 tokens) or for any argument
+ * purhie_moe_ffn rejects. Every call on one GPU shares that GPU's array and leaves its contents behind (each call
+ * writes every region before reading it): calls that overlap on one GPU (other streams, other threads) race.
+ * Nothing is allocated. */
+hipError_t purhie_moe_ffn_noalloc(const purhie_moe_weights *w, const float *xn, const qmatvec_q8 *q8_xn, int T,
+                                  float *out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

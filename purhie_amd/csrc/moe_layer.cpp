@@ -7,6 +7,11 @@
 #include "../../include/quant_types.h"
 
 #include <algorithm>
+#include <mutex>
+
+// purhie_moe_ffn_noalloc's workspace: one static device array on each GPU the library runs on (the runtime places it
+// when it loads the code object on that device; it stays until the process ends)
+static __device__ __align__(256) unsigned char scratch[PURHIE_MOE_SCRATCH_BYTES];
 
 namespace {
 
@@ -109,6 +114,30 @@ Layout layout(const purhie_moe_weights *w, int T, char *base) {
     return L;
 }
 
+// scratch's address on the current device, looked up with hipGetSymbolAddress on the first call with that device
+// current and kept per device (each GPU holds its own copy of the array at its own address). The array's name is a
+// host-side stand-in, never passed to a kernel or a copy.
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void *g_scratch[MAX_DEVICES];
+
+hipError_t scratch_ptr(void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return hipSuccess;
+}
+
 }  // namespace
 
 extern "C" {
@@ -209,6 +238,15 @@ hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qm
                                    stream));
     return gpu_moe_combine(L.down, L.wts, L.shout, sg, out, NU, E, T, stream);
 #undef PQ_TRY
+}
+
+hipError_t purhie_moe_ffn_noalloc(const purhie_moe_weights *w, const float *xn, const qmatvec_q8 *q8_xn, int T,
+                                  float *out, hipStream_t stream) {
+    if (!valid(w, T) || layout(w, T, nullptr).bytes > PURHIE_MOE_SCRATCH_BYTES) return hipErrorInvalidValue;
+    void *ws = nullptr;
+    const hipError_t e = scratch_ptr(&ws);
+    if (e != hipSuccess) return e;
+    return purhie_moe_ffn(w, xn, q8_xn, T, out, ws, PURHIE_MOE_SCRATCH_BYTES, stream);
 }
 
 }  // extern "C"

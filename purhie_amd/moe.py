@@ -26,6 +26,7 @@ def lib():
             "gpu_moe_group": [vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp],
             "purhie_moe_shared_as_slot": [C.POINTER(MoeWeights), i32],
             "purhie_moe_ffn": [C.POINTER(MoeWeights), vp, pq8, i32, vp, vp, C.c_size_t, vp],
+            "purhie_moe_ffn_noalloc": [C.POINTER(MoeWeights), vp, pq8, i32, vp, vp],
         }.items():
             f = getattr(L, name)
             f.restype, f.argtypes = i32, args
@@ -57,6 +58,14 @@ def ffn(w, xn, q8, T, out, ws, stream=None):
     """purhie_moe_ffn: out [T][n_embd] from xn [T][n_embd] and its quantized form q8 (a Q.Q8), ws a device
     uint8 tensor of at least workspace_bytes(w, T) bytes"""
     _check("purhie_moe_ffn", lib().purhie_moe_ffn(C.byref(w), _p(xn), q8.ref, T, _p(out), _p(ws), ws.numel(), stream))
+
+
+def ffn_noalloc(w, xn, q8, T, out, stream=None):
+    """purhie_moe_ffn_noalloc: as ffn, with the library's static per-GPU workspace (SCRATCH_BYTES)"""
+    _check("purhie_moe_ffn_noalloc", lib().purhie_moe_ffn_noalloc(C.byref(w), _p(xn), q8.ref, T, _p(out), stream))
+
+
+SCRATCH_BYTES = 32 << 20  # PURHIE_MOE_SCRATCH_BYTES
 
 
 def workspace_bytes(w, T):
