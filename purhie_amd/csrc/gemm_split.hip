@@ -9,15 +9,16 @@
 // puts the token's largest |X| just under 2^14. hi + lo carries X to 2^-22 relative (the lo rounding), the products
 // with the fp16 weights are exact in fp32, and the f16 MFMAs accumulate straight through K with no per-block
 // epilogue: y = (sum_k W[n][k] (hi + lo)[t][k]) 2^-s. A per-block fp32 epilogue would cost one VALU fma per output
-// per block, as many VALU cycles as the block's MFMAs take; the second plane costs MFMA cycles instead, with the
-// VALU left for staging.
+// per block, as many VALU cycles as the block's MFMAs take; the second plane costs MFMA cycles instead. (Measured on
+// gfx950: a wave's VALU instructions are free beside its MFMAs up to two per v_mfma_f32_16x16x32_f16; each further
+// one costs about its own 4 cycles.)
 //
-// Workgroup: 512 threads (8 waves) over 256 weight rows x TT tokens, K in stages of 64 (two 32-value blocks),
-// double-buffered in LDS with one barrier per stage; every global load is issued two stages before its LDS store.
-// Staging: thread t decodes block (t & 1) of weight row t / 2 through a byte -> (level, level) table, times the
-// block's scales, into fp16; the token rows go to LDS as fp16 integers in the weight's K order (per 32-block,
-// position 2j <- value j, 2j + 1 <- value j + 16: one weight byte holds values j and j + 16), with each (token,
-// block) scale ds. Each wave makes the hi and lo fragments of its token tiles from them and runs the MFMAs.
+// Workgroup: 256 threads (4 waves of 128 rows x TT / 2 tokens), two per CU, over 256 weight rows x TT tokens; K in
+// stages of one 32-value block, double-buffered in LDS with one barrier per stage; every global load is issued two
+// stages before its LDS store. Staging per stage: thread t decodes block s of weight row n0 + t into fp16, and
+// converts TT / 8 consecutive int8 values of one token row to fp16 integers, with the (token, block) scale ds.
+// Each wave makes the hi and lo fragments of its token tiles and runs the MFMAs at raised wave priority, so that
+// the other workgroup's staging on the same SIMD fills the VALU slots beside them.
 #include "device.h"
 #include "kernels.h"
 
@@ -29,45 +30,52 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int SP_THREADS = 512;
-constexpr int SP_ROWS = 256;         // weight rows per workgroup
-constexpr int SP_K = 64;             // K per stage
-constexpr int SP_ROW = SP_K + 8;     // halves per LDS row (16 bytes of padding: conflict-free 16-byte fragment reads)
-constexpr int SP_T = 256;            // tokens per workgroup, dense
+constexpr int SP_ROWS = 256;         // weight rows per workgroup (one a staging thread)
+constexpr int SP_T = 128;            // tokens per workgroup, dense
 constexpr int SP_T_SMALL = 64;       // MoE expert tiles (a few dozen entries on average) and prompts of <= 64 tokens
+constexpr int SP_ROW = 40;           // halves per LDS row: 32 values + 16 bytes of padding (conflict-free reads)
 constexpr int SP_GROUP = 4;          // token tiles advancing together over the row tiles (XCD order)
 
-// wave layout: WC waves along the tokens, 8 / WC along the rows; each wave RT x CT tiles of 16 x 16
+// waves: WC along the tokens, 4 / WC along the rows, each RT x CT tiles of 16 x 16; VN token values a staging
+// thread converts per stage, TPR staging threads a token row
 template <int TT>
 struct SpGeo {
-    static constexpr int WC = TT >= 256 ? 4 : 2;
-    static constexpr int WR = 8 / WC;
+    static constexpr int WC = TT >= 128 ? TT / 64 : 1;
+    static constexpr int WR = 4 / WC;
     static constexpr int RT = SP_ROWS / (16 * WR);
     static constexpr int CT = TT / (16 * WC);
-    static constexpr int TPR = SP_THREADS / TT;  // staging threads per token row
-    static constexpr int VJ = 32 / TPR;          // (j, j + 16) value pairs a staging thread converts per stage
-    static_assert(RT * 16 * WR == SP_ROWS && CT * 16 * WC == TT && VJ >= 4, "tile geometry");
+    static constexpr int VN = TT / 8;
+    static constexpr int TPR = 32 / VN;
+    static_assert(WR * WC == 4 && RT * 16 * WR == SP_ROWS && CT * 16 * WC == TT && VN >= 8 && VN <= 16,
+                  "tile geometry");
 };
 
-// one 32-value FP4 block: 16 code bytes (4 words, byte i: codes of values i low and i + 16 high) and the two
-// half-block scales -> 16 half2 (value i, value i + 16) in LDS through the byte -> (level, level) table; the scales
-// are fp16 values (UE4M3 at half scale lies in [2^-10, 240]) and a level times one is exact
-__device__ __forceinline__ void fp4_block_to_lds(const uint32_t qs[4], float e0, float e1, const uint32_t *lut,
-                                                 _Float16 *dst) {
-    h2 sc;
-    sc.x = (_Float16)e0;
-    sc.y = (_Float16)e1;
-    uint32_t o[16];
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const h2 c = __builtin_bit_cast(h2, lut[(qs[k] >> (8 * j)) & 0xffu]);
-            o[4 * k + j] = __builtin_bit_cast(uint32_t, c * sc);  // v_pk_mul_f16: exact products
-        }
-    uint4 *d4 = (uint4 *)dst;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) d4[m] = make_uint4(o[4 * m], o[4 * m + 1], o[4 * m + 2], o[4 * m + 3]);
+// Four FP4 codes in the low nibbles of w and four in the high nibbles, as fp16 values times their scales, two
+// half2 each (lo: the low nibbles' values in byte order, scaled by slo; hi: the high nibbles', by shi). The codebook's
+// fp16 values have a zero low byte, so v_perm_b32 looks the high bytes of four magnitudes up in an 8-byte table
+// (TOP 10: ROCmFP4's levels {0, 1, 2, 3, 4, 6, 8, 10}; TOP 12: E2M1 doubled), the sign bits are or-ed in, two more
+// byte selections make the half2, and a packed fp16 multiply applies the scale (exact: a level times a UE4M3
+// half-scale value has at most 8 significant bits). (v_cvt_scalef32_pk_f16_fp8 would fold the scale in, but it applies
+// only the scale's power of two.)
+template <int TOP>
+__device__ __forceinline__ void fp4_word(uint32_t w, h2 slo, h2 shi, uint32_t lo[2], uint32_t hi[2]) {
+    constexpr uint32_t TLO = 0x42403c00u, THI = TOP == 10 ? 0x49484644u : 0x4a484644u;
+    const uint32_t ml = __builtin_amdgcn_perm(THI, TLO, w & 0x07070707u) | ((w << 4) & 0x80808080u);
+    const uint32_t mh = __builtin_amdgcn_perm(THI, TLO, (w >> 4) & 0x07070707u) | (w & 0x80808080u);
+    auto h = [](uint32_t m, uint32_t sel, h2 sc) {
+        return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, m, sel)) * sc);
+    };
+    lo[0] = h(ml, 0x010c000cu, slo);
+    lo[1] = h(ml, 0x030c020cu, slo);
+    hi[0] = h(mh, 0x010c000cu, shi);
+    hi[1] = h(mh, 0x030c020cu, shi);
+}
+
+__device__ __forceinline__ h2 h2of(float v) {
+    h2 r;
+    r.x = (_Float16)v;  // exact: a UE4M3 half-scale value is an fp16 value
+    r.y = r.x;
+    return r;
 }
 
 // one thread's weight block per stage: raw global words, then the decode into 32 fp16 values in LDS
@@ -79,64 +87,74 @@ struct SpW {
         uint32_t w[5];
         uint32_t off;
     };
-    // block 2 s + h of the row: five words from the 4-aligned address at or below it (they end at most 3 bytes
+    // 32-value block kb of the row: five words from the 4-aligned address at or below it (they end at most 3 bytes
     // past the block, inside the 4-aligned word that holds its last byte)
-    __device__ static void load(const uint8_t *row, int s, int h, Raw &r) {
-        const uint8_t *b = row + (long long)(2 * s + h) * BB;
+    __device__ static void load(const uint8_t *row, int kb, Raw &r) {
+        const uint8_t *b = row + (long long)kb * BB;
         r.off = (uint32_t)((uintptr_t)b & 3u);
         const uint8_t *al = b - r.off;
 #pragma unroll
         for (int k = 0; k < 5; ++k) r.w[k] = ld32(al + 4 * k);
     }
-    __device__ static void decode(const Raw &r, const uint32_t *lut, _Float16 *dst) {
-        uint32_t v[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) v[k] = align_bytes(r.w[k + 1], r.w[k], r.off);
+    // byte i of the codes holds values i (low nibble, scale e0) and i + 16 (high, scale e1): the block's 32 values
+    // in order into dst
+    __device__ static void decode(const Raw &r, _Float16 *dst) {
         const uint32_t sc = r.w[4] >> (8 * r.off);  // the scale bytes at block offset 16 (and 17)
-        const float e0 = ue4m3_half(sc);
-        const float e1 = TYPE == TY_FP4 ? ue4m3_half(sc >> 8) : e0;
-        fp4_block_to_lds(v, e0, e1, lut, dst);
+        const h2 e0 = h2of(ue4m3_half(sc));
+        const h2 e1 = TYPE == TY_FP4 ? h2of(ue4m3_half(sc >> 8)) : e0;
+        uint32_t lo[4][2], hi[4][2];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) fp4_word<TOP>(align_bytes(r.w[k + 1], r.w[k], r.off), e0, e1, lo[k], hi[k]);
+        uint4 *d4 = (uint4 *)dst;
+        d4[0] = make_uint4(lo[0][0], lo[0][1], lo[1][0], lo[1][1]);
+        d4[1] = make_uint4(lo[2][0], lo[2][1], lo[3][0], lo[3][1]);
+        d4[2] = make_uint4(hi[0][0], hi[0][1], hi[1][0], hi[1][1]);
+        d4[3] = make_uint4(hi[2][0], hi[2][1], hi[3][0], hi[3][1]);
     }
 };
 
 // NVFP4: 36-byte blocks of 64 values (4 UE4M3 scale bytes, then four 16-value sub-blocks of 8 bytes, byte i: values
-// i low, 8 + i high). Stage s is block s; half h (sub-blocks 2h, 2h + 1) is regrouped into the ROCmFP4 byte order of
-// a 32-value block (byte i: value i low, value 16 + i high) with the two sub-block scales as its half-block scales.
+// i low, 8 + i high). 32-value block kb is half h = kb & 1 (sub-blocks 2h, 2h + 1, each with its scale) of block
+// kb / 2.
 template <>
 struct SpW<TY_NVFP4> {
     static constexpr int TOP = 12;
     struct Raw {
         uint32_t sc, v[4];
     };
-    __device__ static void load(const uint8_t *row, int s, int h, Raw &r) {
-        const uint8_t *b = row + (long long)s * 36;
+    __device__ static void load(const uint8_t *row, int kb, Raw &r) {
+        const int h = kb & 1;
+        const uint8_t *b = row + (long long)(kb >> 1) * 36;
         r.sc = ld32(b) >> (16 * h);
 #pragma unroll
         for (int k = 0; k < 4; ++k) r.v[k] = ld32(b + 4 + 16 * h + 4 * k);
     }
-    __device__ static void decode(const Raw &r, const uint32_t *lut, _Float16 *dst) {
-        uint32_t q[4];
+    __device__ static void decode(const Raw &r, _Float16 *dst) {
+        uint32_t lo[4][2], hi[4][2];
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const uint32_t lo = r.v[k], hi = r.v[2 + k];
-            q[k] = (lo & 0x0f0f0f0fu) | ((hi & 0x0f0f0f0fu) << 4);
-            q[2 + k] = ((lo >> 4) & 0x0f0f0f0fu) | (hi & 0xf0f0f0f0u);
+        for (int k = 0; k < 4; ++k) {
+            const h2 e = h2of(nv_scale(r.sc >> (8 * (k >> 1))));
+            fp4_word<TOP>(r.v[k], e, e, lo[k], hi[k]);
         }
-        fp4_block_to_lds(q, nv_scale(r.sc), nv_scale(r.sc >> 8), lut, dst);
+        uint4 *d4 = (uint4 *)dst;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {  // sub-block q: values 16 q + (0 .. 7) low nibbles, 16 q + (8 .. 15) high
+            d4[2 * q] = make_uint4(lo[2 * q][0], lo[2 * q][1], lo[2 * q + 1][0], lo[2 * q + 1][1]);
+            d4[2 * q + 1] = make_uint4(hi[2 * q][0], hi[2 * q][1], hi[2 * q + 1][0], hi[2 * q + 1][1]);
+        }
     }
 };
 
-// four (value j, value j + 16) pairs of int8 from words a (values j .. j + 3) and b (values j + 16 .. j + 19) as four
-// fp16 pairs: the byte b ^ 0x80 under 0x64 is the fp16 1024 + 128 + b, minus 1152
-__device__ __forceinline__ void pairs_to_h2(uint32_t a, uint32_t b, uint32_t *o) {
+// four int8 values (a word) as two fp16 pairs in order: the byte b ^ 0x80 under 0x64 is the fp16 1024 + 128 + b,
+// minus 1152
+__device__ __forceinline__ void i8_to_h2(uint32_t a, uint32_t *o) {
     h2 bias;
     bias.x = (_Float16)1152.0f;
     bias.y = (_Float16)1152.0f;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const uint32_t w = __builtin_amdgcn_perm(b, a, 0x0c040c00u + 0x00010001u * (uint32_t)m) ^ 0x64806480u;
-        o[m] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, w) - bias);
-    }
+    const uint32_t w0 = __builtin_amdgcn_perm(0u, a, 0x0c010c00u) ^ 0x64806480u;
+    const uint32_t w1 = __builtin_amdgcn_perm(0u, a, 0x0c030c02u) ^ 0x64806480u;
+    o[0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, w0) - bias);
+    o[1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, w1) - bias);
 }
 
 template <int N>
@@ -153,12 +171,11 @@ __device__ __forceinline__ Words<N> load_words(const int8_t *p) {
         r.w[1] = v.y;
         r.w[2] = v.z;
         r.w[3] = v.w;
-    } else if constexpr (N == 2) {
+    } else {
+        static_assert(N == 2, "8 or 16 bytes");
         const uint2 v = *(const uint2 *)p;
         r.w[0] = v.x;
         r.w[1] = v.y;
-    } else {
-        r.w[0] = *(const uint32_t *)p;
     }
     return r;
 }
@@ -173,15 +190,14 @@ __device__ __forceinline__ T &pick2(T &a, T &b) {
 }
 
 template <int TYPE, int TT, bool MOE>
-__global__ void __launch_bounds__(SP_THREADS, 1) k_gemm_split(GemmArgs a) {
+__global__ void __launch_bounds__(256, 2) k_gemm_split(GemmArgs a) {
     using S = SpW<TYPE>;
     using G = SpGeo<TT>;
-    constexpr int TPR = G::TPR, VJ = G::VJ, NW = VJ / 4;
-    __shared__ __attribute__((aligned(16))) _Float16 sW0[SP_ROWS * SP_ROW], sW1[SP_ROWS * SP_ROW];
-    __shared__ __attribute__((aligned(16))) _Float16 sX0[TT * SP_ROW], sX1[TT * SP_ROW];
-    __shared__ uint16_t sD0[TT * 2], sD1[TT * 2];  // ds of (token, block of the stage), fp16 bits
-    __shared__ float sT[TT];                       // 2^-s per token
-    __shared__ uint32_t lut[256];
+    constexpr int ROW = SP_ROW, VN = G::VN, TPR = G::TPR, NW = VN / 4;
+    __shared__ __attribute__((aligned(16))) _Float16 sW0[SP_ROWS * ROW], sW1[SP_ROWS * ROW];
+    __shared__ __attribute__((aligned(16))) _Float16 sX0[TT * ROW], sX1[TT * ROW];
+    __shared__ uint16_t sD0[TT], sD1[TT];  // ds of (token, the stage's block), fp16 bits
+    __shared__ float sT[TT];               // 2^-s per token
 
     int n0, e = 0;
     const int32_t *rows = nullptr, *orow = nullptr;
@@ -209,39 +225,31 @@ __global__ void __launch_bounds__(SP_THREADS, 1) k_gemm_split(GemmArgs a) {
         return t < a.T ? t : a.T - 1;
     };
 
-    const int K = a.K, nst = K / SP_K, nb = K / 32;
+    const int K = a.K, nb = K / 32;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid < 256) {
-        const int lo = fp4_level<S::TOP>(tid & 15), hi = fp4_level<S::TOP>(tid >> 4);
-        h2 v;
-        v.x = (_Float16)(float)lo;
-        v.y = (_Float16)(float)hi;
-        lut[tid] = __builtin_bit_cast(uint32_t, v);
-    }
 
-    // staging roles. Weights: block wh = tid & 1 of row n0 + tid / 2 (rows past the end repeat the last; their
-    // outputs are not stored). Tokens: row xr = tid / TPR, pairs j0 .. j0 + VJ - 1 of block xb of each stage.
-    const int wr = n0 + (tid >> 1), wh = tid & 1;
+    // staging roles. Weights: row n0 + tid (rows past the end repeat the last; their outputs are not stored).
+    // Tokens: row xr = tid / TPR, values x0 .. x0 + VN - 1 of each block.
+    const int wr = n0 + tid;
     const uint8_t *wrow = a.W + ((long long)e * a.N + (wr < a.N ? wr : a.N - 1)) * a.row_bytes;
-    const int xr = tid / TPR, xp = tid % TPR, xb = xp / (TPR / 2), j0 = (xp % (TPR / 2)) * VJ;
+    const int xr = tid / TPR, xp = tid % TPR, x0 = VN * xp;
     const long long xrow = trow(xr);
-    const int8_t *xsrc = a.xq + xrow * K + 32 * xb + j0;
-    const float *dsrc = a.dx + xrow * nb + xb;
+    const int8_t *xsrc = a.xq + xrow * K + x0;
+    const float *dsrc = a.dx + xrow * nb;
 
     struct Pre {
         typename S::Raw raw;
-        Words<NW> qa, qb;
+        Words<NW> q;
         float d;
     };
     Pre P0, P1;
     auto issue = [&](Pre &p, int s) {
-        S::load(wrow, s, wh, p.raw);
-        p.qa = load_words<NW>(xsrc + SP_K * s);
-        p.qb = load_words<NW>(xsrc + SP_K * s + 16);
-        p.d = dsrc[2 * s];
+        S::load(wrow, s, p.raw);
+        p.q = load_words<NW>(xsrc + 32 * s);
+        p.d = dsrc[s];  // (every thread of the row: no branch in the loop)
     };
     issue(P0, 0);
-    if (nst > 1) issue(P1, 1);
+    issue(P1, 1);
 
     // the token's power of two: 127 max_b d0[b] = f 2^e with f in [0.5, 1), s = 14 - e (clamped so that 2^s and
     // 2^-s stay normal floats); the TPR threads of a row split its blocks and meet by shuffles
@@ -264,14 +272,14 @@ __global__ void __launch_bounds__(SP_THREADS, 1) k_gemm_split(GemmArgs a) {
         constexpr int c = decltype(cc)::value;
         _Float16 *sw = pick2<c>(sW0, sW1), *sx = pick2<c>(sX0, sX1);
         uint16_t *sd = pick2<c>(sD0, sD1);
-        S::decode(p.raw, lut, sw + (tid >> 1) * SP_ROW + 32 * wh);
-        uint32_t o[VJ];
+        S::decode(p.raw, sw + tid * ROW);
+        uint32_t o[VN / 2];
 #pragma unroll
-        for (int k = 0; k < NW; ++k) pairs_to_h2(p.qa.w[k], p.qb.w[k], o + 4 * k);
-        uint4 *dst = (uint4 *)(sx + xr * SP_ROW + 32 * xb + 2 * j0);
+        for (int k = 0; k < NW; ++k) i8_to_h2(p.q.w[k], o + 2 * k);
+        uint4 *dst = (uint4 *)(sx + xr * ROW + x0);
 #pragma unroll
-        for (int k = 0; k < VJ / 4; ++k) dst[k] = make_uint4(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
-        if (j0 == 0) sd[xr * 2 + xb] = __builtin_bit_cast(uint16_t, (_Float16)(p.d * up));
+        for (int k = 0; k < VN / 8; ++k) dst[k] = make_uint4(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
+        sd[xr] = __builtin_bit_cast(uint16_t, (_Float16)(p.d * up));  // (the row's TPR threads: one value)
     };
 
     constexpr int RT = G::RT, CT = G::CT;
@@ -282,22 +290,21 @@ __global__ void __launch_bounds__(SP_THREADS, 1) k_gemm_split(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < CT; ++j) acc[i][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // the stage's MFMAs: per block, each token tile's hi and lo fragments, then its RT hi and RT lo products
+    // the stage's MFMAs: each token tile's hi and lo fragments, then its RT hi and RT lo products
     auto compute = [&](auto cc) {
         constexpr int c = decltype(cc)::value;
         const _Float16 *sw = pick2<c>(sW0, sW1), *sx = pick2<c>(sX0, sX1);
         const uint16_t *sd = pick2<c>(sD0, sD1);
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            const int kk = 32 * b + 8 * (lane >> 4);
+        {
+            const int kk = 8 * (lane >> 4);
             h8 fa[RT];
 #pragma unroll
-            for (int i = 0; i < RT; ++i) fa[i] = *(const h8 *)(sw + (wr0 + 16 * i + (lane & 15)) * SP_ROW + kk);
+            for (int i = 0; i < RT; ++i) fa[i] = *(const h8 *)(sw + (wr0 + 16 * i + (lane & 15)) * ROW + kk);
 #pragma unroll
             for (int j = 0; j < CT; ++j) {
                 const int tr = wc0 + 16 * j + (lane & 15);
-                const uint4 x = *(const uint4 *)(sx + tr * SP_ROW + kk);
-                const uint32_t ds = sd[tr * 2 + b];
+                const uint4 x = *(const uint4 *)(sx + tr * ROW + kk);
+                const uint32_t ds = sd[tr];
                 const h2 dd = __builtin_bit_cast(h2, ds | (ds << 16));
                 const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
                 uint32_t hv[4], lv[4];
@@ -322,22 +329,31 @@ __global__ void __launch_bounds__(SP_THREADS, 1) k_gemm_split(GemmArgs a) {
 
     // stage s (parity c) is in LDS buffer c and its register set is free: issue stage s + 2 into it, compute stage
     // s, commit stage s + 1 (register set 1 - c) into buffer 1 - c, whose stage s - 1 every wave finished before the
-    // previous barrier
-    auto step = [&](auto cc, int s) {
+    // previous barrier. The steady loop has no conditions, so that the staging work (decode, LDS stores, global
+    // loads) and the MFMAs of a step share one basic block and can be interleaved.
+    auto step = [&](auto cc, auto iss, auto com, int s) {
         constexpr int c = decltype(cc)::value;
-        if (s + 2 < nst) issue(pick2<c>(P0, P1), s + 2);
+        if constexpr (decltype(com)::value) commit(IC<1 - c>{}, pick2<1 - c>(P0, P1));
+        if constexpr (decltype(iss)::value) issue(pick2<c>(P0, P1), s + 2);
+        __builtin_amdgcn_sched_barrier(0);  // (measured: the staging ahead of the MFMAs, not mixed in, is faster)
+        __builtin_amdgcn_s_setprio(1);      // the MFMA phase ahead of the other workgroup's staging on this SIMD
         compute(cc);
-        if (s + 1 < nst) commit(IC<1 - c>{}, pick2<1 - c>(P0, P1));
+        __builtin_amdgcn_s_setprio(0);
         __syncthreads();
     };
 
-    __syncthreads();  // the table
     commit(IC<0>{}, P0);
     __syncthreads();
-    for (int s = 0; s < nst; s += 2) {
-        step(IC<0>{}, s);
-        if (s + 1 < nst) step(IC<1>{}, s + 1);
+    // the stage count nb is even (the host's K multiple is 64): the loop's steps all issue and commit, the last two
+    // only finish
+    const int nst = nb;
+    int s = 0;
+    for (; s + 2 < nst; s += 2) {
+        step(IC<0>{}, IC<1>{}, IC<1>{}, s);
+        step(IC<1>{}, IC<1>{}, IC<1>{}, s + 1);
     }
+    step(IC<0>{}, IC<0>{}, IC<1>{}, s);
+    step(IC<1>{}, IC<0>{}, IC<0>{}, s + 1);
 
     // store: lane holds rows 4 (lane / 16) .. + 3 of each 16 x 16 tile, token column lane % 16
     const float sc = a.es ? a.es[e] : a.osc;
@@ -366,10 +382,10 @@ __global__ void __launch_bounds__(SP_THREADS, 1) k_gemm_split(GemmArgs a) {
 
 template <int TYPE>
 hipError_t launch_t(const GemmArgs &a, dim3 grid, hipStream_t stream) {
-    if (a.n_tiles) hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, true>), grid, dim3(SP_THREADS), 0, stream, a);
+    if (a.n_tiles) hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, true>), grid, dim3(256), 0, stream, a);
     else if (a.tt == SP_T_SMALL)
-        hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, false>), grid, dim3(SP_THREADS), 0, stream, a);
-    else hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T, false>), grid, dim3(SP_THREADS), 0, stream, a);
+        hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, false>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T, false>), grid, dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -377,7 +393,7 @@ hipError_t launch_t(const GemmArgs &a, dim3 grid, hipStream_t stream) {
 
 bool gemm_split(int type) { return type == TY_FP4 || type == TY_FAST || type == TY_NVFP4; }
 
-int gemm_split_k_multiple() { return SP_K; }
+int gemm_split_k_multiple() { return 64; }
 
 int gemm_split_rows() { return SP_ROWS; }
 
