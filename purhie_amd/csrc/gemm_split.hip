@@ -30,24 +30,23 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int SP_ROWS = 256;         // weight rows per workgroup (one a staging thread)
+constexpr int SP_ROWS = 256;         // weight rows per workgroup, dense prompts of more than SP_T_SMALL tokens
+constexpr int SP_ROWS_SMALL = 128;   // the same for MoE expert tiles and short prompts (twice the workgroups)
 constexpr int SP_T = 128;            // tokens per workgroup, dense
 constexpr int SP_T_SMALL = 64;       // MoE expert tiles (a few dozen entries on average) and prompts of <= 64 tokens
 constexpr int SP_ROW = 40;           // halves per LDS row: 32 values + 16 bytes of padding (conflict-free reads)
 constexpr int SP_GROUP = 4;          // token tiles advancing together over the row tiles (XCD order)
 
-// waves: WC along the tokens, 4 / WC along the rows, each RT x CT tiles of 16 x 16; VN token values a staging
-// thread converts per stage, TPR staging threads a token row
-template <int TT>
+// a workgroup of 256 threads (4 waves: 2 along the rows, 2 along the tokens, each RT x CT tiles of 16 x 16) over
+// ROWS weight rows x TT tokens; per stage, PW staging threads decode a row's block (each 4 / PW of its code words)
+// and VN token values go to each thread, TPR threads a token row
+template <int TT, int ROWS>
 struct SpGeo {
-    static constexpr int WC = TT >= 128 ? TT / 64 : 1;
-    static constexpr int WR = 4 / WC;
-    static constexpr int RT = SP_ROWS / (16 * WR);
-    static constexpr int CT = TT / (16 * WC);
+    static constexpr int RT = ROWS / 32, CT = TT / 32;
+    static constexpr int PW = 256 / ROWS;
     static constexpr int VN = TT / 8;
     static constexpr int TPR = 32 / VN;
-    static_assert(WR * WC == 4 && RT * 16 * WR == SP_ROWS && CT * 16 * WC == TT && VN >= 8 && VN <= 16,
-                  "tile geometry");
+    static_assert((ROWS == 256 || ROWS == 128) && (TT == 128 || TT == 64), "tile geometry");
 };
 
 // Four FP4 codes in the low nibbles of w and four in the high nibbles, as fp16 values times their scales, two
@@ -96,20 +95,24 @@ struct SpW {
 #pragma unroll
         for (int k = 0; k < 5; ++k) r.w[k] = ld32(al + 4 * k);
     }
-    // byte i of the codes holds values i (low nibble, scale e0) and i + 16 (high, scale e1): the block's 32 values
-    // in order into dst
-    __device__ static void decode(const Raw &r, _Float16 *dst) {
+    // byte i of the codes holds values i (low nibble, scale e0) and i + 16 (high, scale e1). Part p of P decodes
+    // code words 4 p / P .. (word k: values 4k .. 4k + 3 and 16 + 4k .. 16 + 4k + 3) into dst, the block's 32
+    // values in order.
+    template <int P>
+    __device__ static void decode(const Raw &r, _Float16 *dst, int p) {
         const uint32_t sc = r.w[4] >> (8 * r.off);  // the scale bytes at block offset 16 (and 17)
         const h2 e0 = h2of(ue4m3_half(sc));
         const h2 e1 = TYPE == TY_FP4 ? h2of(ue4m3_half(sc >> 8)) : e0;
-        uint32_t lo[4][2], hi[4][2];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) fp4_word<TOP>(align_bytes(r.w[k + 1], r.w[k], r.off), e0, e1, lo[k], hi[k]);
-        uint4 *d4 = (uint4 *)dst;
-        d4[0] = make_uint4(lo[0][0], lo[0][1], lo[1][0], lo[1][1]);
-        d4[1] = make_uint4(lo[2][0], lo[2][1], lo[3][0], lo[3][1]);
-        d4[2] = make_uint4(hi[0][0], hi[0][1], hi[1][0], hi[1][1]);
-        d4[3] = make_uint4(hi[2][0], hi[2][1], hi[3][0], hi[3][1]);
+        for (int k = 0; k < 4 / P; k += 2) {
+            const int k0 = 4 / P * p + k;
+            uint32_t lo[2][2], hi[2][2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                fp4_word<TOP>(align_bytes(r.w[k0 + j + 1], r.w[k0 + j], r.off), e0, e1, lo[j], hi[j]);
+            *(uint4 *)(dst + 4 * k0) = make_uint4(lo[0][0], lo[0][1], lo[1][0], lo[1][1]);
+            *(uint4 *)(dst + 16 + 4 * k0) = make_uint4(hi[0][0], hi[0][1], hi[1][0], hi[1][1]);
+        }
     }
 };
 
@@ -129,18 +132,19 @@ struct SpW<TY_NVFP4> {
 #pragma unroll
         for (int k = 0; k < 4; ++k) r.v[k] = ld32(b + 4 + 16 * h + 4 * k);
     }
-    __device__ static void decode(const Raw &r, _Float16 *dst) {
-        uint32_t lo[4][2], hi[4][2];
+    // sub-block q (code words 2q, 2q + 1; word k: values 4k' .. 4k' + 3 low nibbles, 8 + 4k' .. high, k' = k & 1)
+    // with its own scale; part p of P decodes sub-blocks 2 p / P ..
+    template <int P>
+    __device__ static void decode(const Raw &r, _Float16 *dst, int p) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const h2 e = h2of(nv_scale(r.sc >> (8 * (k >> 1))));
-            fp4_word<TOP>(r.v[k], e, e, lo[k], hi[k]);
-        }
-        uint4 *d4 = (uint4 *)dst;
+        for (int k = 0; k < 4 / P; k += 2) {
+            const int k0 = 4 / P * p + k, q = k0 >> 1;
+            const h2 e = h2of(nv_scale(r.sc >> (8 * q)));
+            uint32_t lo[2][2], hi[2][2];
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {  // sub-block q: values 16 q + (0 .. 7) low nibbles, 16 q + (8 .. 15) high
-            d4[2 * q] = make_uint4(lo[2 * q][0], lo[2 * q][1], lo[2 * q + 1][0], lo[2 * q + 1][1]);
-            d4[2 * q + 1] = make_uint4(hi[2 * q][0], hi[2 * q][1], hi[2 * q + 1][0], hi[2 * q + 1][1]);
+            for (int j = 0; j < 2; ++j) fp4_word<TOP>(r.v[k0 + j], e, e, lo[j], hi[j]);
+            *(uint4 *)(dst + 16 * q) = make_uint4(lo[0][0], lo[0][1], lo[1][0], lo[1][1]);
+            *(uint4 *)(dst + 16 * q + 8) = make_uint4(hi[0][0], hi[0][1], hi[1][0], hi[1][1]);
         }
     }
 };
@@ -189,12 +193,13 @@ __device__ __forceinline__ T &pick2(T &a, T &b) {
     else return a;
 }
 
-template <int TYPE, int TT, bool MOE>
-__global__ void __launch_bounds__(256, 2) k_gemm_split(GemmArgs a) {
+template <int TYPE, int TT, int ROWS, bool MOE>
+__global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_split(GemmArgs a) {
     using S = SpW<TYPE>;
-    using G = SpGeo<TT>;
+    using G = SpGeo<TT, ROWS>;
+    constexpr int PW = G::PW;
     constexpr int ROW = SP_ROW, VN = G::VN, TPR = G::TPR, NW = VN / 4;
-    __shared__ __attribute__((aligned(16))) _Float16 sW0[SP_ROWS * ROW], sW1[SP_ROWS * ROW];
+    __shared__ __attribute__((aligned(16))) _Float16 sW0[ROWS * ROW], sW1[ROWS * ROW];
     __shared__ __attribute__((aligned(16))) _Float16 sX0[TT * ROW], sX1[TT * ROW];
     __shared__ uint16_t sD0[TT], sD1[TT];  // ds of (token, the stage's block), fp16 bits
     __shared__ float sT[TT];               // 2^-s per token
@@ -210,12 +215,12 @@ __global__ void __launch_bounds__(256, 2) k_gemm_split(GemmArgs a) {
         rows = a.in_rows + st;
         orow = a.out_rows + st;
         tn = a.tile_n[k];
-        n0 = blockIdx.x * SP_ROWS;
+        n0 = blockIdx.x * ROWS;
     } else {  // grid (token tiles, row tiles), renumbered XCD by XCD
         int tt, rt;
         xcd_tile(tt, rt, SP_GROUP);
         tbase = tt * TT;
-        n0 = rt * SP_ROWS;
+        n0 = rt * ROWS;
     }
     // token row of tile position j: real rows for j < n (dense: < T), else a repeat of a valid row whose outputs are
     // not stored
@@ -228,9 +233,9 @@ __global__ void __launch_bounds__(256, 2) k_gemm_split(GemmArgs a) {
     const int K = a.K, nb = K / 32;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-    // staging roles. Weights: row n0 + tid (rows past the end repeat the last; their outputs are not stored).
-    // Tokens: row xr = tid / TPR, values x0 .. x0 + VN - 1 of each block.
-    const int wr = n0 + tid;
+    // staging roles. Weights: row n0 + tid / PW, part tid % PW of its block (rows past the end repeat the last;
+    // their outputs are not stored). Tokens: row xr = tid / TPR, values x0 .. x0 + VN - 1 of each block.
+    const int wr = n0 + tid / PW, wp = tid % PW;
     const uint8_t *wrow = a.W + ((long long)e * a.N + (wr < a.N ? wr : a.N - 1)) * a.row_bytes;
     const int xr = tid / TPR, xp = tid % TPR, x0 = VN * xp;
     const long long xrow = trow(xr);
@@ -272,7 +277,7 @@ __global__ void __launch_bounds__(256, 2) k_gemm_split(GemmArgs a) {
         constexpr int c = decltype(cc)::value;
         _Float16 *sw = pick2<c>(sW0, sW1), *sx = pick2<c>(sX0, sX1);
         uint16_t *sd = pick2<c>(sD0, sD1);
-        S::decode(p.raw, sw + tid * ROW);
+        S::template decode<PW>(p.raw, sw + (tid / PW) * ROW, wp);
         uint32_t o[VN / 2];
 #pragma unroll
         for (int k = 0; k < NW; ++k) i8_to_h2(p.q.w[k], o + 2 * k);
@@ -283,7 +288,7 @@ __global__ void __launch_bounds__(256, 2) k_gemm_split(GemmArgs a) {
     };
 
     constexpr int RT = G::RT, CT = G::CT;
-    const int wr0 = (wave / G::WC) * RT * 16, wc0 = (wave % G::WC) * CT * 16;
+    const int wr0 = (wave >> 1) * RT * 16, wc0 = (wave & 1) * CT * 16;
     f4 acc[RT][CT];
 #pragma unroll
     for (int i = 0; i < RT; ++i)
@@ -382,10 +387,10 @@ __global__ void __launch_bounds__(256, 2) k_gemm_split(GemmArgs a) {
 
 template <int TYPE>
 hipError_t launch_t(const GemmArgs &a, dim3 grid, hipStream_t stream) {
-    if (a.n_tiles) hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, true>), grid, dim3(256), 0, stream, a);
+    if (a.n_tiles) hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, SP_ROWS, true>), grid, dim3(256), 0, stream, a);
     else if (a.tt == SP_T_SMALL)
-        hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, false>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T, false>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, SP_ROWS_SMALL, false>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T, SP_ROWS, false>), grid, dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -395,7 +400,7 @@ bool gemm_split(int type) { return type == TY_FP4 || type == TY_FAST || type == 
 
 int gemm_split_k_multiple() { return 64; }
 
-int gemm_split_rows() { return SP_ROWS; }
+int gemm_split_rows(bool moe, int T) { return !moe && T <= SP_T_SMALL ? SP_ROWS_SMALL : SP_ROWS; }
 
 int gemm_split_token_tile(bool moe, int T) { return moe || T <= SP_T_SMALL ? SP_T_SMALL : SP_T; }
 

@@ -105,12 +105,12 @@ int gemm_supported(int type);
 // values per integer the type's GEMM exposes in capture mode (0: its sums are not integers, none captured)
 int gemm_cap_unit(int type);
 // the split-activation GEMM (gemm_split.hip: ROCmFP4, ROCmFP4_FAST, NVFP4; Q8_0 activation, xq = q0, dx = d0):
-// dense grid (tokens / gemm_split_token_tile(false, T), rows / gemm_split_rows()), MoE grid (rows /
-// gemm_split_rows(), tiles) with tiles of up to gemm_split_token_tile(true, 0) entries; K a multiple of
+// dense grid (tokens / gemm_split_token_tile(false, T), rows / gemm_split_rows(false, T)), MoE grid (rows /
+// gemm_split_rows(true, 0), tiles) with tiles of up to gemm_split_token_tile(true, 0) entries; K a multiple of
 // gemm_split_k_multiple()
 bool gemm_split(int type);
 int gemm_split_k_multiple();
-int gemm_split_rows();
+int gemm_split_rows(bool moe, int T);  // weight rows per workgroup
 int gemm_split_token_tile(bool moe, int T);
 hipError_t launch_gemm_split(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);
 

@@ -121,7 +121,7 @@ hipError_t gemm_dense(int type, const void *W, size_t row_bytes, const qmatvec_q
     a.T = T;
     a.osc = dense_scale(W);
     if (gemm_split(type)) {
-        const int BT = gemm_split_token_tile(false, T), RN = gemm_split_rows();
+        const int BT = gemm_split_token_tile(false, T), RN = gemm_split_rows(false, T);
         a.tt = BT;
         return launch_gemm_split(type, a, dim3((unsigned)((T + BT - 1) / BT), (unsigned)((N + RN - 1) / RN)), stream);
     }
@@ -516,7 +516,7 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
     a.out_rows = out_rows;
     expert_scale(W, a.es, a.osc);
     if (gemm_split(type)) {
-        const int RN = gemm_split_rows();
+        const int RN = gemm_split_rows(true, 0);
         return launch_gemm_split(type, a, dim3((unsigned)((N + RN - 1) / RN), (unsigned)max_tiles), stream);
     }
     a.cap = g_cap;  // (tiles mode: rows from out_rows; the caller sizes the buffer)
