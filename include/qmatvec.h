@@ -167,6 +167,17 @@ hipError_t qmatvec_launch_q8_id_x(int type, const void *W, const void *W2, const
                                   size_t row_bytes, const int32_t *ids, int n_used, int x_per_slot,
                                   const qmatvec_q8 *q, float *y, float *y2, int N, int K, int T, hipStream_t stream);
 
+/* No counterpart in the reference (it launches gpu_moe_router, then qmatvec_launch_q8_id_pair): the expert gate /
+ * up pair of a decode step with the routing folded in. logits [T][n_expert]: every workgroup routes its token as
+ * gpu_moe_router does (softmax, the n_used largest in descending order, weights divided by their sum; no shared
+ * gate), ids [T][n_used] and wts [T][n_used] receive the same values as that launch's, and y / y2 the pair
+ * launch's with x_per_slot = 0: bit-identical to the two launches, one launch fewer. Shapes the one-unit-per-lane
+ * kernel does not take, n_expert > 256 or the per-wave decode path run the two launches. */
+hipError_t qmatvec_launch_q8_id_pair_routed(int type, const void *W, const void *W2, size_t row_bytes,
+                                            const float *logits, int n_expert, int32_t *ids, float *wts, int n_used,
+                                            const qmatvec_q8 *q, float *y, float *y2, int N, int K, int T,
+                                            hipStream_t stream);
+
 /* No counterpart in the reference (it launches gpu_swiglu, then qmatvec_launch_q8_id with x_per_slot = 1): the
  * expert down matvec of a decode step with the SwiGLU launch folded in. Entry (t, slot) reads row t * n_used +
  * slot of g and u (K floats each), quantizes SwiGLU(g, u) = g / (1 + exp(-g)) * u to Q8_0 in the kernel and

@@ -68,6 +68,13 @@ struct MvIdArgs {
     // cap[((m * cap_rows + o) * N + row) * (K / G) + group] (cap_rows: T * n_used, or 0 in tiles mode)
     int32_t *cap;
     long long cap_rows;
+    // routing in the launch (route_logits set; tile kernel, 256-thread tiles, route_ne <= 256, no tiles mode):
+    // every workgroup routes its token from route_logits [T][route_ne] as the router kernel does, and the first
+    // workgroup of each token writes its ids and weights to route_ids / route_wts [T][n_used] (ids is unused)
+    const float *route_logits;
+    int route_ne;
+    int32_t *route_ids;
+    float *route_wts;
 };
 hipError_t launch_matvec_id(int type, const MvIdArgs &a, hipStream_t stream);
 bool matvec_id_swiglu_supported(int type, int K);
@@ -144,5 +151,6 @@ struct MvTune {
 };
 const MvTune &mv_tune();
 void mv_tune_set_tile(int on);
+bool mv_tile_on();  // the tile kernels on (the tuning's value, or the last mv_tune_set_tile)
 
 }  // namespace pq

@@ -775,6 +775,8 @@ void mv_tune_set_tile(int on) { __atomic_store_n(&g_tune.tile, on ? 1 : 0, __ATO
 // the tile kernels where they take the shape, unless PURHIE_MV_TILE=0 or the test hook switched them off
 static bool tile_enabled() { return __atomic_load_n(&g_tune.tile, __ATOMIC_RELAXED) != 0; }
 
+bool mv_tile_on() { return tile_enabled(); }
+
 template <int TYPE, int NT, int L>
 static hipError_t launch_tl(const MvArgs &a, hipStream_t stream) {
     const int rows_per_wg = (MV_THREADS / 64) * (64 / L);

@@ -17,12 +17,10 @@
 //                  are deterministic; the order of the entries inside an expert's run is not, and nothing
 //                  depends on it (every entry's value is computed alone).
 #include "q8dev.h"
+#include "moe_dev.h"
 #include "moe_ops.h"
 
 namespace pq {
-
-constexpr int MOE_MAX_EXPERTS = 1024;
-constexpr int MOE_MAX_USED = 64;
 
 __global__ void __launch_bounds__(256) k_swiglu(const float *__restrict__ g, const float *__restrict__ u,
                                                 float *__restrict__ out, int n, Q8Ptrs o, int quantize) {
@@ -121,113 +119,15 @@ __global__ void __launch_bounds__(256) k_add_rmsnorm_rows(const float *__restric
     }
 }
 
-// sum / max over the 256 threads of a workgroup (4 waves), the result in every thread
-__device__ __forceinline__ float wg_sum(float v, float *red) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
-}
-
-__device__ __forceinline__ float wg_max(float v, float *red) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-}
-
 __global__ void __launch_bounds__(256) k_moe_router(const float *__restrict__ logits, const float *__restrict__ x,
                                                     const float *__restrict__ w_sh, int *__restrict__ ids,
                                                     float *__restrict__ wts, float *__restrict__ sg, int n_expert,
                                                     int n_used, int n, int ids_stride) {
-    constexpr int PER = MOE_MAX_EXPERTS / 256;  // experts per thread: tid + 256 j
-    __shared__ unsigned long long key[MOE_MAX_EXPERTS];
-    __shared__ float red[4];
-    __shared__ float selw[MOE_MAX_USED];
-    __shared__ float wsum;
-    const int t = blockIdx.x, tid = threadIdx.x;
-    const float *l = logits + (long long)t * n_expert;
-
-    // the logits once into registers, and the shared expert's dot product, before any wait
-    float lv[PER];
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const int e = tid + 256 * j;
-        lv[j] = e < n_expert ? l[e] : -INFINITY;
-    }
-    float dsum = 0.0f;
-    if (w_sh) {  // (uniform)
-        const float *xt = x + (long long)t * n;
-        for (int i = tid; i < n; i += 256) dsum = fmaf(xt[i], w_sh[i], dsum);
-    }
-
-    float mx = lv[0];
-#pragma unroll
-    for (int j = 1; j < PER; ++j) mx = fmaxf(mx, lv[j]);
-    mx = wg_max(mx, red);
-    float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const int e = tid + 256 * j;
-        lv[j] = e < n_expert ? expf(lv[j] - mx) : 0.0f;
-        sum += lv[j];
-    }
-    sum = wg_sum(sum, red);
-    const float inv = 1.0f / sum;
-
-    // top n_used by rank: expert e's rank is the number of experts ahead of it, those with a larger probability
-    // or an equal one at a lower index (the order of the reference's rounds of argmax). One 64-bit key per
-    // expert orders both at once: high word the probability's bits plus one (probabilities are >= 0, so their
-    // bits order as the values; a NaN gets 0 and ranks below every number), low word ~e. Keys are distinct, so
-    // the ranks are too.
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const int e = tid + 256 * j;
-        if (e < n_expert) {
-            const float p = lv[j] * inv;
-            lv[j] = p;
-            const uint32_t hi = p == p ? __float_as_uint(p) + 1u : 0u;
-            key[e] = ((unsigned long long)hi << 32) | (uint32_t)~e;
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const int e = tid + 256 * j;
-        if (256 * j < n_expert) {  // (uniform)
-            if (e < n_expert) {
-                const unsigned long long k = key[e];
-                int r = 0;
-                int f = 0;
-                for (; f + 2 <= n_expert; f += 2) {
-                    const ulonglong2 u = *(const ulonglong2 *)(key + f);
-                    r += (u.x > k) + (u.y > k);
-                }
-                if (f < n_expert) r += key[f] > k;
-                if (r < n_used) {
-                    ids[(long long)t * ids_stride + r] = e;
-                    selw[r] = lv[j];
-                }
-            }
-        }
-    }
-    if (tid == n_used && ids_stride > n_used) ids[(long long)t * ids_stride + n_used] = -1;  // the shared slot
-    if (w_sh) {  // (uniform) the shared expert's gate
-        dsum = wg_sum(dsum, red);
-        if (tid == 0) sg[t] = 1.0f / (1.0f + expf(-dsum));
-    }
-    __syncthreads();
-    if (tid == 0) {  // the sum in slot order, as the reference's loop
-        float ws = 0.0f;
-        for (int r = 0; r < n_used; ++r) ws += selw[r];
-        wsum = fmaxf(ws, 6.103515625e-5f);
-    }
-    __syncthreads();
-    if (tid < n_used) wts[(long long)t * n_used + tid] = selw[tid] / wsum;
+    __shared__ RouterLds<MOE_MAX_EXPERTS / 256> s;
+    const int t = blockIdx.x;
+    route_token(logits + (long long)t * n_expert, w_sh ? x + (long long)t * n : nullptr, w_sh,
+                ids + (long long)t * ids_stride, wts + (long long)t * n_used, w_sh ? sg + t : nullptr, n_expert, n_used,
+                n, ids_stride, s);
 }
 
 __global__ void __launch_bounds__(256) k_moe_combine(const float *__restrict__ down, const float *__restrict__ wts,

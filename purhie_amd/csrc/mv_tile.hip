@@ -28,6 +28,7 @@
 // tokens share it.
 #include "device.h"
 #include "kernels.h"
+#include "moe_dev.h"
 
 namespace pq {
 
@@ -726,11 +727,26 @@ __global__ void __launch_bounds__(THR) k_mv_tile(MvArgs a, TileArgs ta) {
 
 // MoE: grid (tiles, n_used * nmat, T); slot j of token t uses expert ids[t * n_used + j] (-1: Wx). Tiles mode:
 // grid (tiles, tile, max_tiles) over moe_group's expert tiles, one entry per block.
-template <int TYPE, int THR, bool SW = false, bool CAP = false>
+template <int TYPE, int THR, bool SW = false, bool CAP = false, bool ROUTE = false>
 __global__ void __launch_bounds__(THR) k_mv_tile_id(MvIdArgs a, TileArgs ta) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     IdEntry en;
-    if (!id_entry(a, en)) return;  // (uniform: before any barrier)
+    if constexpr (ROUTE) {  // the token's experts from its logits (every workgroup; the first one stores them)
+        static_assert(THR == 256, "the router's reductions take 256 threads");
+        __shared__ RouterLds<1> rs;
+        const int t = blockIdx.z, slot = (int)blockIdx.y % a.n_used;
+        const bool first = blockIdx.x == 0 && blockIdx.y == 0;
+        route_token(a.route_logits + (long long)t * a.route_ne, nullptr, nullptr,
+                    first ? a.route_ids + (long long)t * a.n_used : nullptr,
+                    first ? a.route_wts + (long long)t * a.n_used : nullptr, nullptr, a.route_ne, a.n_used, 0, a.n_used,
+                    rs);
+        en.m = (int)blockIdx.y >= a.n_used ? 1 : 0;
+        en.e = rs.selid[slot];
+        en.out_row = (long long)t * a.n_used + slot;
+        en.in_row = a.x_per_slot ? en.out_row : t;
+    } else if (!id_entry(a, en)) {
+        return;  // (uniform: before any barrier)
+    }
     const int m = en.m, e = en.e;
     const long long in_row = en.in_row;
     const int K = a.K;
@@ -857,6 +873,14 @@ static hipError_t tile_id_thr(const MvIdArgs &a, hipStream_t stream) {
         }
     } else if (a.sw_g) {
         return hipErrorInvalidDeviceFunction;
+    }
+    if (a.route_logits) {
+        if constexpr (THR == 256) {
+            if (a.cap || a.n_tiles) return hipErrorNotSupported;
+            hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, false, false, true>), grid, dim3(THR), lds, stream, a, ta);
+            return hipGetLastError();
+        }
+        return hipErrorNotSupported;
     }
     if (a.cap) hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, false, true>), grid, dim3(THR), lds, stream, a, ta);
     else hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR>), grid, dim3(THR), lds, stream, a, ta);

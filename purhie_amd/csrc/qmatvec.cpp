@@ -3,6 +3,7 @@
 // Host-side dispatch keeps the reference's src/qmatvec.cpp contract (argument checks, error codes, buffer
 // layout of qmatvec_q8); the launch geometry is this library's own (wave64 kernels, lanes per row chosen per
 // shape, activation staged in LDS). The output-scale registry is out_scale.cpp.
+#include "../../include/moe_ops.h"
 #include "../../include/qmatvec.h"
 #include "../../include/quant_types.h"
 #include "kernels.h"
@@ -365,6 +366,50 @@ hipError_t qmatvec_launch_q8_id_x(int type, const void *W, const void *W2, const
     a.cap_rows = (long long)T * n_used;
     if (const hipError_t e = cap_for(a.nmat * a.cap_rows * N * (K / cap_group(type)), a.cap); e != hipSuccess) return e;
     return launch_matvec_id(type, a, stream);
+}
+
+hipError_t qmatvec_launch_q8_id_pair_routed(int type, const void *W, const void *W2, size_t row_bytes,
+                                            const float *logits, int n_expert, int32_t *ids, float *wts, int n_used,
+                                            const qmatvec_q8 *q, float *y, float *y2, int N, int K, int T,
+                                            hipStream_t stream) {
+    if (!qmatvec_q8_supported(type, K)) return hipErrorInvalidDeviceFunction;
+    const uintptr_t am = w_align(type) - 1;
+    if (!logits || !ids || !wts || !W || !W2 || !q || !y || !y2 || T <= 0 || n_used <= 0 || n_expert < n_used ||
+        N <= 0 || row_bytes != qt_row_size(type, K) || (((uintptr_t)W | (uintptr_t)W2) & am) != 0 ||
+        (long long)T * K > q->max_k)
+        return hipErrorInvalidValue;
+    auto two_launches = [&]() {
+        const hipError_t e = gpu_moe_router(logits, nullptr, nullptr, ids, wts, nullptr, n_expert, n_used, 0, T,
+                                            stream, 0);
+        return e != hipSuccess ? e : qmatvec_launch_q8_id_pair(type, W, W2, row_bytes, ids, n_used, 0, q, y, y2, N,
+                                                               K, T, stream);
+    };
+    if (n_expert > 256 || n_used > 64 || !mv_tile_on()) return two_launches();
+    MvIdArgs a{};
+    a.W[0] = (const uint8_t *)W;
+    a.W[1] = (const uint8_t *)W2;
+    a.y[0] = y;
+    a.y[1] = y2;
+    const void *ws[2] = {W, W2};
+    for (int m = 0; m < 2; ++m) {
+        expert_scale(ws[m], a.es[m], a.s[m]);
+        a.sx[m] = 1.0f;
+    }
+    a.row_bytes = (long long)row_bytes;
+    act_ptrs(type, q, a.q, a.d, a.bs);
+    a.n_used = n_used;
+    a.x_per_slot = 0;
+    a.N = N;
+    a.K = K;
+    a.T = T;
+    a.nmat = 2;
+    a.L = matvec_lanes(type, K, (long long)N * n_used * 2 * T);
+    a.route_logits = logits;
+    a.route_ne = n_expert;
+    a.route_ids = ids;
+    a.route_wts = wts;
+    const hipError_t e = launch_matvec_id_tile(type, a, stream);
+    return e == hipErrorNotSupported ? two_launches() : e;
 }
 
 int qmatvec_q8_id_swiglu_supported(int type, int K) {

@@ -73,6 +73,8 @@ def lib():
             "qmatvec_launch_q8_batch": (i32, [i32, vp, sz, pq8, vp, ll, i32, i32, i32, vp]),
             "qmatvec_launch_q8_id": (i32, [i32, vp, sz, vp, i32, i32, pq8, vp, i32, i32, i32, vp]),
             "qmatvec_launch_q8_id_pair": (i32, [i32, vp, vp, sz, vp, i32, i32, pq8, vp, vp, i32, i32, i32, vp]),
+            "qmatvec_launch_q8_id_pair_routed": (i32, [i32, vp, vp, sz, vp, i32, vp, vp, i32, pq8, vp, vp, i32, i32, i32,
+                                                       vp]),
             "qmatvec_launch_q8_id_x": (i32, [i32, vp, vp, vp, vp, sz, vp, i32, i32, pq8, vp, vp, i32, i32, i32, vp]),
             "qmatvec_id_batch_tile": (i32, [i32, i32, i32]),
             "qmatvec_q8_id_batch_supported": (i32, [i32, i32]),

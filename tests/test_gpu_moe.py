@@ -186,3 +186,53 @@ def test_add_rmsnorm_bad_arguments(M):
     assert L.gpu_add_rmsnorm(p(x), p(x), p(x), None, p(x), 256, 1, 1e-6, None, None) == 1  # x_out aliases x_in
     assert L.gpu_add_rmsnorm(p(x), None, None, None, p(x), 200, 1, 1e-6, q.ref, None) == 1  # n % 256
     assert L.gpu_add_rmsnorm(p(x), None, None, None, p(x), 256, 2, 1e-6, q.ref, None) == 1  # T n > max_k
+
+
+@pytest.mark.parametrize("kpath", ["tile", "wave"])
+@pytest.mark.parametrize("t,T,E,n_used,N,K", [(100, 1, 128, 8, 768, 2048), (12, 1, 128, 8, 768, 2048),
+                                              (100, 3, 256, 8, 512, 1024), (40, 2, 64, 4, 256, 1024),
+                                              (100, 1, 300, 8, 256, 1024)])
+def test_routed_pair_same_bits(M, oracle, kpath, t, T, E, n_used, N, K):
+    """qmatvec_launch_q8_id_pair_routed (routing inside the gate / up pair launch) gives gpu_moe_router's ids and
+    weights and qmatvec_launch_q8_id_pair's outputs bit for bit: on the tile kernel (n_expert <= 256) and through
+    the two launches it falls back to (n_expert 300, the per-wave path)"""
+    import ctypes as C
+    import torch
+    from purhie_amd import qmatvec as Q
+    prev = Q.decode_path(1 if kpath == "tile" else 0)
+    try:
+        g = torch.Generator(device="cuda")
+        g.manual_seed(E * 31 + K)
+        W = torch.empty((E * N, Q.row_size(t, K)), dtype=torch.uint8, device="cuda")
+        W2 = torch.empty_like(W)
+        for w in (W, W2):
+            Q.encode_device(t, torch.randn((E * N, K), generator=g, device="cuda") * 0.02, w, E * N, K)
+        logits = synth.gaussian(950 + E, T * E).reshape(T, E)
+        if T >= 2:
+            logits[1, 3] = logits[1, 7] = logits[1].max() + 0.5  # equal leaders
+        lg = dev(logits)
+        x = dev(synth.gaussian(951, T * K))
+        q = Q.Q8(((T * K + 255) // 256) * 256)
+        Q.quantize(x, T * K, q)
+        p = lambda a: C.c_void_p(a.data_ptr())
+        L = Q.lib()
+        outs = []
+        for routed in (False, True):
+            ids = torch.full((T, n_used), -9, dtype=torch.int32, device="cuda")
+            wts = torch.full((T, n_used), float("nan"), device="cuda")
+            y = torch.full((T * n_used, N), float("nan"), device="cuda")
+            y2 = torch.full((T * n_used, N), float("nan"), device="cuda")
+            rb = Q.row_size(t, K)
+            if routed:
+                assert L.qmatvec_launch_q8_id_pair_routed(t, p(W), p(W2), rb, p(lg), E, p(ids), p(wts), n_used, q.ref,
+                                                          p(y), p(y2), N, K, T, None) == 0
+            else:
+                M.router(lg, ids, wts, E, n_used, T)
+                assert L.qmatvec_launch_q8_id_pair(t, p(W), p(W2), rb, p(ids), n_used, 0, q.ref, p(y), p(y2), N, K, T,
+                                                   None) == 0
+            outs.append([host(a) for a in (ids, wts, y, y2)])
+        for a, b in zip(*outs):
+            assert np.isfinite(a.astype(np.float64)).all()
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    finally:
+        Q.decode_path(prev)
