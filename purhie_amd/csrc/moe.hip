@@ -22,18 +22,36 @@
 
 namespace pq {
 
+// bpw 256-value blocks per workgroup (8 for large n: one block per workgroup spends its time starting workgroups),
+// one value per thread each, the next block's inputs loaded before the current one is quantized
 __global__ void __launch_bounds__(256) k_swiglu(const float *__restrict__ g, const float *__restrict__ u,
-                                                float *__restrict__ out, int n, Q8Ptrs o, int quantize) {
+                                                float *__restrict__ out, int n, Q8Ptrs o, int quantize, int bpw) {
     __shared__ Q8Shared sh;
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    const bool active = i < n;
-    float v = 0.0f;
-    if (active) {
-        const float a = g[i];
-        v = a / (1.0f + expf(-a)) * u[i];
-        out[i] = v;
+    const int b0 = blockIdx.x * bpw, t = threadIdx.x;
+    const int nb = (n + 255) / 256, bn = nb - b0 < bpw ? nb - b0 : bpw;
+    float ga = 0.0f, ua = 0.0f;
+    if (b0 * 256 + t < n) {
+        ga = g[b0 * 256 + t];
+        ua = u[b0 * 256 + t];
     }
-    if (quantize) q8_quantize_value(v, active, blockIdx.x, sh, o);  // (uniform)
+    for (int k = 0; k < bn; ++k) {  // (uniform)
+        const int i = (b0 + k) * 256 + t;
+        const bool active = i < n;
+        const float a = ga, ub = ua;
+        if (k + 1 < bn && i + 256 < n) {
+            ga = g[i + 256];
+            ua = u[i + 256];
+        }
+        float v = 0.0f;
+        if (active) {
+            v = a / (1.0f + expf(-a)) * ub;
+            out[i] = v;
+        }
+        if (quantize) {  // (uniform)
+            if (k) __syncthreads();  // the previous block's reads of sh are done
+            q8_quantize_value(v, active, b0 + k, sh, o);
+        }
+    }
 }
 
 // ---------------------------------------------------------------- add + RMSNorm, the matvec inputs' producer
@@ -234,7 +252,9 @@ hipError_t gpu_swiglu(const float *g, const float *u, float *out, int n, const q
         if (n % 32 != 0 || n > q8->max_k) return hipErrorInvalidValue;
         o = Q8Ptrs{q8->q0, q8->d0, q8->qK, q8->dK, q8->bsK, q8->s0};
     }
-    hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, g, u, out, n, o, q8 ? 1 : 0);
+    const int nb = (n + 255) / 256, bpw = nb >= 4096 ? 8 : 1;
+    hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((nb + bpw - 1) / bpw)), dim3(256), 0, stream, g, u, out, n, o,
+                       q8 ? 1 : 0, bpw);
     return hipGetLastError();
 }
 
