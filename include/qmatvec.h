@@ -198,6 +198,16 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
                                       const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
                                       const int32_t *out_rows, hipStream_t stream);
 
+/* No counterpart in the reference (its engine calls qmatvec_launch_q8_id_batch for the experts' gate, then their
+ * up projection, src/qwen_model.cpp:1060-1071): both over the same expert tiles in one launch, W into y and W2
+ * into y2 (the same type, shape and row_bytes). Each output is bit-identical to the single launch's; one launch
+ * instead of two lets the two matrices' workgroups share the chip. */
+hipError_t qmatvec_launch_q8_id_batch_pair(int type, const void *W, const void *W2, size_t row_bytes,
+                                           const qmatvec_q8 *q, float *y, float *y2, int N, int K, int max_tiles,
+                                           int tile, const int32_t *n_tiles, const int32_t *tile_e,
+                                           const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
+                                           const int32_t *out_rows, hipStream_t stream);
+
 /* outside this path (as qmatvec_launch above): the split-Q8_0 LM head, the low-rank and the float MoE entries
  * (src/qmatvec.h:74-75,145-147,179-180,195-199): *_supported 0, hipErrorInvalidDeviceFunction */
 hipError_t qmatvec_launch_q8_0s(const int8_t *qs, const uint16_t *d, const qmatvec_q8 *q, float *y, int N, int K,

@@ -292,7 +292,7 @@ __global__ void __launch_bounds__(I8_THREADS, 2) k_gemm_i8kq(GemmArgs a) {
         const int st = a.tile_start[k];
         tm = {a.in_rows + st, 0, a.tile_n[k]};
         orow = a.out_rows + st;
-        n0 = blockIdx.x * I8_N;
+        n0 = moe_row_tile(a) * I8_N;
     } else {              // grid (token tiles, row tiles), renumbered XCD by XCD
         int tt, rt;
         xcd_tile(tt, rt, I8_GROUP);
@@ -599,7 +599,7 @@ __global__ void __launch_bounds__(I8_THREADS, 2) k_gemm_i8blk(GemmArgs a) {
         const int st = a.tile_start[k];
         tm = {a.in_rows + st, 0, a.tile_n[k]};
         orow = a.out_rows + st;
-        n0 = blockIdx.x * I8_N;
+        n0 = moe_row_tile(a) * I8_N;
     } else {
         int tt, rt;
         xcd_tile(tt, rt, I8_GROUP);

@@ -14,8 +14,9 @@
 // one costs about its own 4 cycles.)
 //
 // Workgroup: 256 threads (4 waves of 128 rows x TT / 2 tokens), two per CU, over 256 weight rows x TT tokens; K in
-// stages of one 32-value block, double-buffered in LDS with one barrier per stage; every global load is issued two
-// stages before its LDS store. Staging per stage: thread t decodes block s of weight row n0 + t into fp16, and
+// stages of one 32-value block, double-buffered in LDS with one barrier per stage; every global load is issued PD
+// stages before its LDS store (2 for the dense 128-token tiles, whose registers allow no more; 4 for the 64-token
+// tiles: MoE expert tiles, prefill of config 4's sizes 339 -> 327 us). Staging per stage: thread t decodes block s of weight row n0 + t into fp16, and
 // converts TT / 8 consecutive int8 values of one token row to fp16 integers, with the (token, block) scale ds.
 // Each wave makes the hi and lo fragments of its token tiles and runs the MFMAs at raised wave priority, so that
 // the other workgroup's staging on the same SIMD fills the VALU slots beside them.
@@ -36,6 +37,9 @@ constexpr int SP_T = 128;            // tokens per workgroup, dense
 constexpr int SP_T_SMALL = 64;       // MoE expert tiles (a few dozen entries on average) and prompts of <= 64 tokens
 constexpr int SP_ROW = 40;           // halves per LDS row: 32 values + 16 bytes of padding (conflict-free reads)
 constexpr int SP_GROUP = 4;          // token tiles advancing together over the row tiles (XCD order)
+constexpr int SP_PD = 2;             // prefetch distance (stages), dense 128-token tiles
+constexpr int SP_PD_SMALL = 4;       // the same, dense 64-token tiles
+constexpr int SP_PD_MOE = 4;         // the same, MoE expert tiles
 
 // a workgroup of 256 threads (4 waves: 2 along the rows, 2 along the tokens, each RT x CT tiles of 16 x 16) over
 // ROWS weight rows x TT tokens; per stage, PW staging threads decode a row's block (each 4 / PW of its code words)
@@ -193,8 +197,11 @@ __device__ __forceinline__ T &pick2(T &a, T &b) {
     else return a;
 }
 
-template <int TYPE, int TT, int ROWS, bool MOE>
+// PD: the prefetch distance in stages (2 or 4): stage s's global loads are issued PD stages before its LDS store,
+// into one of PD register sets
+template <int TYPE, int TT, int ROWS, bool MOE, int PD>
 __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_split(GemmArgs a) {
+    static_assert(PD == 2 || PD == 4, "prefetch distance");
     using S = SpW<TYPE>;
     using G = SpGeo<TT, ROWS>;
     constexpr int PW = G::PW;
@@ -215,7 +222,7 @@ __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_spl
         rows = a.in_rows + st;
         orow = a.out_rows + st;
         tn = a.tile_n[k];
-        n0 = blockIdx.x * ROWS;
+        n0 = moe_row_tile(a) * ROWS;
     } else {  // grid (token tiles, row tiles), renumbered XCD by XCD
         int tt, rt;
         xcd_tile(tt, rt, SP_GROUP);
@@ -247,14 +254,17 @@ __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_spl
         Words<NW> q;
         float d;
     };
-    Pre P0, P1;
+    Pre P[PD];
+    // stage s's loads; a stage past the end loads the last one again (the steady loop has no conditions: those
+    // copies are committed into the idle LDS buffer after the last compute and never read)
     auto issue = [&](Pre &p, int s) {
+        s = s < nb ? s : nb - 1;
         S::load(wrow, s, p.raw);
         p.q = load_words<NW>(xsrc + 32 * s);
         p.d = dsrc[s];  // (every thread of the row: no branch in the loop)
     };
-    issue(P0, 0);
-    issue(P1, 1);
+#pragma unroll
+    for (int i = 0; i < PD; ++i) issue(P[i], i);
 
     // the token's power of two: 127 max_b d0[b] = f 2^e with f in [0.5, 1), s = 14 - e (clamped so that 2^s and
     // 2^-s stay normal floats); the TPR threads of a row split its blocks and meet by shuffles
@@ -332,33 +342,39 @@ __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_spl
         }
     };
 
-    // stage s (parity c) is in LDS buffer c and its register set is free: issue stage s + 2 into it, compute stage
-    // s, commit stage s + 1 (register set 1 - c) into buffer 1 - c, whose stage s - 1 every wave finished before the
-    // previous barrier. The steady loop has no conditions, so that the staging work (decode, LDS stores, global
-    // loads) and the MFMAs of a step share one basic block and can be interleaved.
-    auto step = [&](auto cc, auto iss, auto com, int s) {
-        constexpr int c = decltype(cc)::value;
-        if constexpr (decltype(com)::value) commit(IC<1 - c>{}, pick2<1 - c>(P0, P1));
-        if constexpr (decltype(iss)::value) issue(pick2<c>(P0, P1), s + 2);
+    // step s (s = s0 + u, s0 a multiple of the unroll U, itself a multiple of PD): stage s is in LDS buffer s & 1
+    // and its register set s % PD is free (committed by step s - 1). Commit stage s + 1 (register set (s + 1) % PD)
+    // into buffer 1 - (s & 1), whose stage s - 1 every wave finished before the previous barrier; issue stage
+    // s + PD into set s % PD; compute stage s. The steady loop has no conditions, so that the staging work (decode,
+    // LDS stores, global loads) and the MFMAs of a step share one basic block and can be interleaved.
+    constexpr int U = PD;
+    auto step = [&](auto uu, int s0) {
+        constexpr int u = decltype(uu)::value, c = u & 1;
+        commit(IC<1 - c>{}, P[(u + 1) % PD]);
+        issue(P[u % PD], s0 + u + PD);
         __builtin_amdgcn_sched_barrier(0);  // (measured: the staging ahead of the MFMAs, not mixed in, is faster)
         __builtin_amdgcn_s_setprio(1);      // the MFMA phase ahead of the other workgroup's staging on this SIMD
-        compute(cc);
+        compute(IC<c>{});
         __builtin_amdgcn_s_setprio(0);
         __syncthreads();
     };
 
-    commit(IC<0>{}, P0);
+    commit(IC<0>{}, P[0]);
     __syncthreads();
-    // the stage count nb is even (the host's K multiple is 64): the loop's steps all issue and commit, the last two
-    // only finish
-    const int nst = nb;
+    // the stage count nb is even (the host's K multiple is 64): groups of U steps, then (U = 4) one pair
     int s = 0;
-    for (; s + 2 < nst; s += 2) {
-        step(IC<0>{}, IC<1>{}, IC<1>{}, s);
-        step(IC<1>{}, IC<1>{}, IC<1>{}, s + 1);
+    for (; s + U <= nb; s += U) {
+        step(IC<0>{}, s);
+        step(IC<1>{}, s);
+        if constexpr (U == 4) {
+            step(IC<2>{}, s);
+            step(IC<3>{}, s);
+        }
     }
-    step(IC<0>{}, IC<0>{}, IC<1>{}, s);
-    step(IC<1>{}, IC<0>{}, IC<0>{}, s + 1);
+    if (U == 4 && s < nb) {
+        step(IC<0>{}, s);
+        step(IC<1>{}, s);
+    }
 
     // store: lane holds rows 4 (lane / 16) .. + 3 of each 16 x 16 tile, token column lane % 16
     const float sc = a.es ? a.es[e] : a.osc;
@@ -387,10 +403,12 @@ __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_spl
 
 template <int TYPE>
 hipError_t launch_t(const GemmArgs &a, dim3 grid, hipStream_t stream) {
-    if (a.n_tiles) hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, SP_ROWS, true>), grid, dim3(256), 0, stream, a);
+    if (a.n_tiles)
+        hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, SP_ROWS, true, SP_PD_MOE>), grid, dim3(256), 0, stream, a);
     else if (a.tt == SP_T_SMALL)
-        hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, SP_ROWS_SMALL, false>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T, SP_ROWS, false>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, SP_ROWS_SMALL, false, SP_PD_SMALL>), grid, dim3(256), 0,
+                           stream, a);
+    else hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T, SP_ROWS, false, SP_PD>), grid, dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -102,11 +102,32 @@ struct GemmArgs {
     // MoE tiles (n_tiles null: dense)
     const int32_t *n_tiles, *tile_e, *tile_start, *tile_n, *in_rows, *out_rows;
     const float *es;        // per-expert output scales (null: osc)
+    // MoE pair (W2 non-null): a second matrix of the same shape over the same tiles (the experts' gate and up) in
+    // one grid: row-tile columns 0 .. rt - 1 are W's, rt .. 2 rt - 1 are W2's (output y2, scales es2 / osc2)
+    const uint8_t *W2;
+    float *y2;
+    const float *es2;
+    float osc2;
+    int rt;
     int tt;                 // split GEMM, dense: tokens per workgroup (gemm_split_token_tile)
     // capture mode (null: off; the integer-exact GEMMs): the exact integer each epilogue scales, per token (dense:
     // t; tiles: the entry's output row) and weight row: cap[(t * N + row) * (K / U) + unit], U = gemm_cap_unit(type)
     int32_t *cap;
 };
+
+// a MoE GEMM workgroup's row-tile column (blockIdx.x), with a switched to the pair's second matrix when the column
+// lies in its half of the grid
+__device__ inline int moe_row_tile(GemmArgs &a) {
+    int bx = blockIdx.x;
+    if (a.W2 && bx >= a.rt) {
+        bx -= a.rt;
+        a.W = a.W2;
+        a.y = a.y2;
+        a.es = a.es2;
+        a.osc = a.osc2;
+    }
+    return bx;
+}
 
 int gemm_supported(int type);
 // values per integer the type's GEMM exposes in capture mode (0: its sums are not integers, none captured)

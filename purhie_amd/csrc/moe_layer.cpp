@@ -203,10 +203,9 @@ hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qm
     // src/qwen_model.cpp:1137-1166
     if (L.grouped) {
         PQ_TRY(gpu_moe_group(L.ids, T, NU, NE, L.tile, L.tok, L.pair, L.ntiles, L.te, L.ts, L.tn, stream));
-        PQ_TRY(qmatvec_launch_q8_id_batch(w->type_gate_up, w->gate_exps, w->rb_gate_up, q8_xn, L.g, FE, E, L.max_tiles,
-                                          L.tile, L.ntiles, L.te, L.ts, L.tn, L.tok, L.pair, stream));
-        PQ_TRY(qmatvec_launch_q8_id_batch(w->type_gate_up, w->up_exps, w->rb_gate_up, q8_xn, L.u, FE, E, L.max_tiles,
-                                          L.tile, L.ntiles, L.te, L.ts, L.tn, L.tok, L.pair, stream));
+        PQ_TRY(qmatvec_launch_q8_id_batch_pair(w->type_gate_up, w->gate_exps, w->up_exps, w->rb_gate_up, q8_xn, L.g,
+                                               L.u, FE, E, L.max_tiles, L.tile, L.ntiles, L.te, L.ts, L.tn, L.tok,
+                                               L.pair, stream));
     } else {
         PQ_TRY(qmatvec_launch_q8_id_pair(w->type_gate_up, w->gate_exps, w->up_exps, w->rb_gate_up, L.ids, NU, 0, q8_xn,
                                          L.g, L.u, FE, E, T, stream));

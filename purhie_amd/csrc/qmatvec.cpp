@@ -517,6 +517,34 @@ int qmatvec_id_batch_tile(int type, int N, int K) {
     return gemm_split(type) ? gemm_split_token_tile(true, 0) : gemm_i8kq_token_tile(true);
 }
 
+// the expert-tiled GEMM over W (and W2, the pair's second matrix, or null), the activation read in place: input
+// rows are in_rows[] of q
+static hipError_t id_gemm(int type, const void *W, const void *W2, size_t row_bytes, const qmatvec_q8 *q, float *y,
+                          float *y2, int N, int K, int max_tiles, const int32_t *n_tiles, const int32_t *tile_e,
+                          const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
+                          const int32_t *out_rows, hipStream_t stream) {
+    GemmArgs a = gemm_args(type, W, row_bytes, q, y, N, K);
+    a.n_tiles = n_tiles;
+    a.tile_e = tile_e;
+    a.tile_start = tile_start;
+    a.tile_n = tile_n;
+    a.in_rows = in_rows;
+    a.out_rows = out_rows;
+    expert_scale(W, a.es, a.osc);
+    const bool split = gemm_split(type);
+    const int RN = split ? gemm_split_rows(true, 0) : gemm_i8kq_rows(), rt = (N + RN - 1) / RN;
+    if (W2) {
+        a.W2 = (const uint8_t *)W2;
+        a.y2 = y2;
+        expert_scale(W2, a.es2, a.osc2);
+        a.rt = rt;
+    }
+    const dim3 grid((unsigned)(W2 ? 2 * rt : rt), (unsigned)max_tiles);
+    if (split) return launch_gemm_split(type, a, grid, stream);
+    a.cap = W2 ? nullptr : g_cap;  // (tiles mode: rows from out_rows; the caller sizes the buffer)
+    return launch_gemm_i8kq(type, a, grid, stream);
+}
+
 hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N,
                                       int K, int max_tiles, int tile, const int32_t *n_tiles, const int32_t *tile_e,
                                       const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
@@ -551,22 +579,30 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
         a.cap_rows = 0;
         return launch_matvec_id(type, a, stream);
     }
-    // the activation read in place: input rows are in_rows[] of q
-    GemmArgs a = gemm_args(type, W, row_bytes, q, y, N, K);
-    a.n_tiles = n_tiles;
-    a.tile_e = tile_e;
-    a.tile_start = tile_start;
-    a.tile_n = tile_n;
-    a.in_rows = in_rows;
-    a.out_rows = out_rows;
-    expert_scale(W, a.es, a.osc);
-    if (gemm_split(type)) {
-        const int RN = gemm_split_rows(true, 0);
-        return launch_gemm_split(type, a, dim3((unsigned)((N + RN - 1) / RN), (unsigned)max_tiles), stream);
+    return id_gemm(type, W, nullptr, row_bytes, q, y, nullptr, N, K, max_tiles, n_tiles, tile_e, tile_start, tile_n,
+                   in_rows, out_rows, stream);
+}
+
+// the gate and up projections of the experts over the same tiles in one expert-tiled GEMM launch (no counterpart in
+// the reference, whose engine runs qmatvec_launch_q8_id_batch twice): the same outputs bit for bit
+hipError_t qmatvec_launch_q8_id_batch_pair(int type, const void *W, const void *W2, size_t row_bytes,
+                                           const qmatvec_q8 *q, float *y, float *y2, int N, int K, int max_tiles,
+                                           int tile, const int32_t *n_tiles, const int32_t *tile_e,
+                                           const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
+                                           const int32_t *out_rows, hipStream_t stream) {
+    if (!qmatvec_q8_id_batch_supported(type, K)) return hipErrorInvalidDeviceFunction;
+    if (!q || !W2 || !y2 || max_tiles <= 0 || tile <= 0 || tile > qmatvec_id_batch_tile(type, N, K) || N <= 0 ||
+        row_bytes != qt_row_size(type, K) || (((uintptr_t)W | (uintptr_t)W2) & (w_align(type) - 1)) != 0)
+        return hipErrorInvalidValue;
+    if (!id_gemm_ok(type, N, K) || g_cap) {  // the decode-order kernels, or a capture: two launches
+        const hipError_t e = qmatvec_launch_q8_id_batch(type, W, row_bytes, q, y, N, K, max_tiles, tile, n_tiles,
+                                                        tile_e, tile_start, tile_n, in_rows, out_rows, stream);
+        return e != hipSuccess ? e
+                               : qmatvec_launch_q8_id_batch(type, W2, row_bytes, q, y2, N, K, max_tiles, tile, n_tiles,
+                                                            tile_e, tile_start, tile_n, in_rows, out_rows, stream);
     }
-    a.cap = g_cap;  // (tiles mode: rows from out_rows; the caller sizes the buffer)
-    const int RN = gemm_i8kq_rows();
-    return launch_gemm_i8kq(type, a, dim3((unsigned)((N + RN - 1) / RN), (unsigned)max_tiles), stream);
+    return id_gemm(type, W, W2, row_bytes, q, y, y2, N, K, max_tiles, n_tiles, tile_e, tile_start, tile_n, in_rows,
+                   out_rows, stream);
 }
 
 hipError_t qmatvec_debug_capture(int32_t *out, size_t n_ints) {

@@ -80,6 +80,8 @@ def lib():
             "qmatvec_q8_id_batch_supported": (i32, [i32, i32]),
             "qmatvec_launch_q8_id_batch": (i32, [i32, vp, sz, pq8, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp,
                                                  vp]),
+            "qmatvec_launch_q8_id_batch_pair": (i32, [i32, vp, vp, sz, pq8, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp,
+                                                      vp, vp, vp]),
             "qmatvec_debug_block_dots": (i32, [i32, vp, sz, pq8, vp, i32, i32, vp]),
             "qmatvec_debug_capture": (i32, [vp, sz]),
             "qmatvec_debug_capture_unit": (i32, [i32, i32]),

@@ -121,6 +121,49 @@ def test_moe_tiled_gemm(Q, oracle, t, N, K):
             parity.check(f"expert-tiled GEMM {Q.NAMES[t]}", got[tt * n_used + j], want, mag, ref, TOL)
 
 
+@pytest.mark.parametrize("t,N,K", [(100, 768, 2048), (101, 256, 1024), (40, 768, 2048), (8, 512, 1024),
+                                   (39, 256, 1024), (12, 768, 2048), (13, 512, 1024), (14, 256, 768),
+                                   (23, 512, 1024), (100, 200, 512)])
+def test_moe_tiled_gemm_pair(Q, oracle, t, N, K):
+    """qmatvec_launch_q8_id_batch_pair (gate and up over the same expert tiles in one launch): each output bit for
+    bit the single launch's, with per-expert output scales registered on the second matrix only"""
+    import ctypes as C
+    import torch
+    E, n_used, T = 12, 4, 56
+    L = Q.lib()
+    Wg = dev(oracle.quantize(t, synth.gaussian(80 + t, E * N * K, 0, 0.02).reshape(E * N, K)))
+    Wu = dev(oracle.quantize(t, synth.gaussian(81 + t, E * N * K, 0, 0.02).reshape(E * N, K)))
+    ids = (synth.splitmix64(82, T * n_used) % np.uint64(E)).astype(np.int32).reshape(T, n_used)
+    tile = L.qmatvec_id_batch_tile(t, N, K)
+    g = oracle.moe_group(ids, E, tile)
+    x = acts(83, T, K)
+    q = Q.Q8(((T * K + 255) // 256) * 256)
+    Q.quantize(dev(x.reshape(-1)), T * K, q)
+    p = lambda a: C.c_void_p(a.data_ptr())
+    bufs = [dev(np.array([g["n_tiles"]], np.int32)), dev(g["tile_e"]), dev(g["tile_start"]), dev(g["tile_n"]),
+            dev(g["tok_rows"]), dev(g["pair_rows"])]
+    rb, mt = Q.row_size(t, K), g["n_tiles"] + 2
+    nan = lambda: torch.full((T * n_used, N), float("nan"), dtype=torch.float32, device="cuda")
+    es = torch.tensor([0.5 + 0.125 * e for e in range(E)], dtype=torch.float32).pin_memory()
+    owner = C.c_void_p(0x7F)
+    assert L.qmatvec_set_out_scale(owner, p(Wu), Wu.numel(), p(es), E) == 0
+    try:
+        yg, yu = nan(), nan()
+        assert L.qmatvec_launch_q8_id_batch(t, p(Wg), rb, q.ref, p(yg), N, K, mt, tile, *[p(b) for b in bufs],
+                                            None) == 0
+        assert L.qmatvec_launch_q8_id_batch(t, p(Wu), rb, q.ref, p(yu), N, K, mt, tile, *[p(b) for b in bufs],
+                                            None) == 0
+        pg, pu = nan(), nan()
+        assert L.qmatvec_launch_q8_id_batch_pair(t, p(Wg), p(Wu), rb, q.ref, p(pg), p(pu), N, K, mt, tile,
+                                                 *[p(b) for b in bufs], None) == 0
+        a, b, c, d = host(yg), host(yu), host(pg), host(pu)
+    finally:
+        L.qmatvec_drop_out_scales(owner)
+    assert np.isfinite(a).all() and np.isfinite(b).all()
+    assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
+    assert np.array_equal(b.view(np.uint32), d.view(np.uint32))
+
+
 @pytest.fixture(params=["tile", "wave"])
 def kpath(request, monkeypatch):
     """the decode kernels under test: the one-unit-per-lane tile kernels or the per-wave kernels"""
