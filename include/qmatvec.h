@@ -208,6 +208,20 @@ hipError_t qmatvec_launch_q8_id_batch_pair(int type, const void *W, const void *
                                            const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
                                            const int32_t *out_rows, hipStream_t stream);
 
+/* No counterpart in the reference (its engine runs the experts' gate and up GEMMs, then gpu_swiglu with the
+ * down projection's quantization, src/qwen_model.cpp:1150-1156): the pair above with SwiGLU(gate, up) =
+ * g / (1 + exp(-g)) u and its Q8_0 quantization in the GEMM's epilogue. Entry j's row out_rows[j] of h gets the
+ * bits gpu_swiglu's quantizer writes there: q0, d0, and s0 where h binds it (the Q8_K side is not written, so the
+ * consumer reads Q8_0). The gate and up outputs are not stored. For the types whose GEMM folds the activation scale
+ * into its operands (ROCmFP4, ROCmFP4_FAST, NVFP4) with N a multiple of 128; _supported says whether a launch
+ * takes the shape (else hipErrorInvalidDeviceFunction, before anything runs). */
+int qmatvec_q8_id_batch_swiglu_supported(int type, int N, int K);
+hipError_t qmatvec_launch_q8_id_batch_swiglu(int type, const void *W, const void *W2, size_t row_bytes,
+                                             const qmatvec_q8 *q, const qmatvec_q8 *h, int N, int K, int max_tiles,
+                                             int tile, const int32_t *n_tiles, const int32_t *tile_e,
+                                             const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
+                                             const int32_t *out_rows, hipStream_t stream);
+
 /* outside this path (as qmatvec_launch above): the split-Q8_0 LM head, the low-rank and the float MoE entries
  * (src/qmatvec.h:74-75,145-147,179-180,195-199): *_supported 0, hipErrorInvalidDeviceFunction */
 hipError_t qmatvec_launch_q8_0s(const int8_t *qs, const uint16_t *d, const qmatvec_q8 *q, float *y, int N, int K,

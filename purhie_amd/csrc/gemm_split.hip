@@ -197,11 +197,93 @@ __device__ __forceinline__ T &pick2(T &a, T &b) {
     else return a;
 }
 
+// The SwiGLU pair's epilogue. The up waves (2, 3) put u = acc sc_u 2^-s into sU (their token half, [token][129]
+// floats, within the LDS weight buffer the finished loop no longer reads); after a barrier each gate wave (0, 1) takes
+// g = acc sc_g 2^-s of the same (row, token), v = g / (1 + exp(-g)) u (the arithmetic of gpu_swiglu), and quantizes
+// each 32-row block of a token as the activation quantizer does: am = max |v| over the block (8 values in each of the
+// 4 lanes of the token's column), q = rint(v 127 / am), d = fp16(am / 127), s0 = fp16(d sum q). The lane's 4
+// consecutive rows of a tile are 4 consecutive bytes of q. Output row of entry j: out_rows[j]; padding entries store
+// nothing.
+template <int RT, int CT>
+__device__ __forceinline__ void swiglu_epilogue(const GemmArgs &a, const f4 (&acc)[RT][CT], int e, int n0, int tn,
+                                                const int32_t *orow, const float *sT, float *sU, int wave, int lane) {
+    static_assert(RT == 8, "128 rows a wave: four 32-row blocks");
+    constexpr int UP = 129;
+    if (wave >= 2) {
+        const float sc = a.es2 ? a.es2[e] : a.osc2;
+#pragma unroll
+        for (int j = 0; j < CT; ++j) {
+            const int tl = 16 * j + (lane & 15), tt = 16 * CT * (wave & 1) + tl;
+            const float f = sc * sT[tt];
+#pragma unroll
+            for (int i = 0; i < RT; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sU[tl * UP + 16 * i + 4 * (lane >> 4) + r] = acc[i][j][r] * f;
+        }
+    }
+    __syncthreads();
+    if (wave >= 2) return;
+    const float sc = a.es ? a.es[e] : a.osc;
+    const int N = a.N;
+#pragma unroll
+    for (int j = 0; j < CT; ++j) {
+        const int tl = 16 * j + (lane & 15), tt = 16 * CT * (wave & 1) + tl;
+        const bool store = tt < tn;
+        const long long hrow = store ? (long long)orow[tt] : 0;
+        const float f = sc * sT[tt];
+#pragma unroll
+        for (int b = 0; b < RT / 2; ++b) {
+            float v[8];
+            float am = 0.0f;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = 16 * (2 * b + h) + 4 * (lane >> 4) + r;
+                    const float g = acc[2 * b + h][j][r] * f, u = sU[tl * UP + row];
+                    v[4 * h + r] = g / (1.0f + expf(-g)) * u;
+                    am = fmaxf(am, fabsf(v[4 * h + r]));
+                }
+            am = fmaxf(am, __shfl_xor(am, 16, 64));
+            am = fmaxf(am, __shfl_xor(am, 32, 64));
+            const float id0 = am != 0.0f ? 127.0f / am : 0.0f;
+            uint32_t qw[2] = {0u, 0u};
+            int qs = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int q = (int)rintf(v[k] * id0);
+                qs += q;
+                qw[k >> 2] |= (uint32_t)(q & 0xff) << (8 * (k & 3));
+            }
+            qs += __shfl_xor(qs, 16, 64);
+            qs += __shfl_xor(qs, 32, 64);
+            if (store) {
+                int8_t *q0 = a.hq + hrow * N + n0 + 32 * b + 4 * (lane >> 4);
+                *(uint32_t *)q0 = qw[0];
+                *(uint32_t *)(q0 + 16) = qw[1];
+                if ((lane >> 4) == 0) {
+                    const float d = am / 127.0f;
+                    const long long bi = hrow * (N / 32) + (n0 + 32 * b) / 32;
+                    a.hd[bi] = __half2float(__float2half(d));
+                    if (a.hs) {
+                        float p = d * (float)qs;
+                        __asm__ volatile("" : "+v"(p));  // (fp16 of the fp32 product, as the quantizer)
+                        a.hs[bi] = __float_as_int(__half2float(__float2half(p)));
+                    }
+                }
+            }
+        }
+    }
+}
+
 // PD: the prefetch distance in stages (2 or 4): stage s's global loads are issued PD stages before its LDS store,
-// into one of PD register sets
-template <int TYPE, int TT, int ROWS, bool MOE, int PD>
+// into one of PD register sets. SWP (MoE, the gate / up pair): the workgroup's rows are rows n0 .. n0 + ROWS / 2 - 1
+// of W (gate, waves 0 and 1) and the same rows of W2 (up, waves 2 and 3), and the epilogue writes
+// SwiGLU(gate, up) = g / (1 + exp(-g)) u quantized to Q8_0 (hq, hd, hs) instead of the two outputs.
+template <int TYPE, int TT, int ROWS, bool MOE, int PD, bool SWP = false>
 __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_split(GemmArgs a) {
     static_assert(PD == 2 || PD == 4, "prefetch distance");
+    static_assert(!SWP || (MOE && ROWS == 256 && TT == 64), "the SwiGLU pair: MoE tiles of 256 rows x 64 tokens");
     using S = SpW<TYPE>;
     using G = SpGeo<TT, ROWS>;
     constexpr int PW = G::PW;
@@ -222,7 +304,7 @@ __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_spl
         rows = a.in_rows + st;
         orow = a.out_rows + st;
         tn = a.tile_n[k];
-        n0 = moe_row_tile(a) * ROWS;
+        n0 = SWP ? (int)blockIdx.x * (ROWS / 2) : moe_row_tile(a) * ROWS;
     } else {  // grid (token tiles, row tiles), renumbered XCD by XCD
         int tt, rt;
         xcd_tile(tt, rt, SP_GROUP);
@@ -242,8 +324,9 @@ __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_spl
 
     // staging roles. Weights: row n0 + tid / PW, part tid % PW of its block (rows past the end repeat the last;
     // their outputs are not stored). Tokens: row xr = tid / TPR, values x0 .. x0 + VN - 1 of each block.
-    const int wr = n0 + tid / PW, wp = tid % PW;
-    const uint8_t *wrow = a.W + ((long long)e * a.N + (wr < a.N ? wr : a.N - 1)) * a.row_bytes;
+    const int wr = n0 + (SWP ? (tid / PW) % (ROWS / 2) : tid / PW), wp = tid % PW;
+    const uint8_t *wrow = (SWP && tid / PW >= ROWS / 2 ? a.W2 : a.W) +
+                          ((long long)e * a.N + (wr < a.N ? wr : a.N - 1)) * a.row_bytes;
     const int xr = tid / TPR, xp = tid % TPR, x0 = VN * xp;
     const long long xrow = trow(xr);
     const int8_t *xsrc = a.xq + xrow * K + x0;
@@ -376,6 +459,11 @@ __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_spl
         step(IC<1>{}, s);
     }
 
+    if constexpr (SWP) {
+        swiglu_epilogue<RT, CT>(a, acc, e, n0, tn, orow, sT, (float *)(wave & 1 ? sW1 : sW0), wave, lane);
+        return;
+    }
+
     // store: lane holds rows 4 (lane / 16) .. + 3 of each 16 x 16 tile, token column lane % 16
     const float sc = a.es ? a.es[e] : a.osc;
 #pragma unroll
@@ -403,7 +491,10 @@ __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_spl
 
 template <int TYPE>
 hipError_t launch_t(const GemmArgs &a, dim3 grid, hipStream_t stream) {
-    if (a.n_tiles)
+    if (a.n_tiles && a.hq)
+        hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, SP_ROWS, true, SP_PD_MOE, true>), grid, dim3(256), 0, stream,
+                           a);
+    else if (a.n_tiles)
         hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, SP_ROWS, true, SP_PD_MOE>), grid, dim3(256), 0, stream, a);
     else if (a.tt == SP_T_SMALL)
         hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, SP_ROWS_SMALL, false, SP_PD_SMALL>), grid, dim3(256), 0,
@@ -421,6 +512,8 @@ int gemm_split_k_multiple() { return 64; }
 int gemm_split_rows(bool moe, int T) { return !moe && T <= SP_T_SMALL ? SP_ROWS_SMALL : SP_ROWS; }
 
 int gemm_split_token_tile(bool moe, int T) { return moe || T <= SP_T_SMALL ? SP_T_SMALL : SP_T; }
+
+int gemm_split_swiglu_rows() { return SP_ROWS / 2; }
 
 hipError_t launch_gemm_split(int type, const GemmArgs &a, dim3 grid, hipStream_t stream) {
     switch (type) {

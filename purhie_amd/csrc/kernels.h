@@ -109,6 +109,11 @@ struct GemmArgs {
     const float *es2;
     float osc2;
     int rt;
+    // MoE pair with SwiGLU (hq set; split GEMM): the entries' SwiGLU(y, y2) rows quantized to Q8_0 instead of y and
+    // y2: values hq [rows][N], scales hd [rows][N / 32], block sums hs (null: not written)
+    int8_t *hq;
+    float *hd;
+    int32_t *hs;
     int tt;                 // split GEMM, dense: tokens per workgroup (gemm_split_token_tile)
     // capture mode (null: off; the integer-exact GEMMs): the exact integer each epilogue scales, per token (dense:
     // t; tiles: the entry's output row) and weight row: cap[(t * N + row) * (K / U) + unit], U = gemm_cap_unit(type)
@@ -140,6 +145,8 @@ bool gemm_split(int type);
 int gemm_split_k_multiple();
 int gemm_split_rows(bool moe, int T);  // weight rows per workgroup
 int gemm_split_token_tile(bool moe, int T);
+// the MoE gate / up pair with SwiGLU (GemmArgs hq set): rows of each matrix per workgroup, grid (N / this, tiles)
+int gemm_split_swiglu_rows();
 hipError_t launch_gemm_split(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);
 
 // Float activations over F32 / F16 / BF16 weights (type ids 0, 1, 30): the decode matvec for T tokens (round:

@@ -200,12 +200,21 @@ hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qm
         return gpu_moe_combine(L.down, L.wts, L.down + (size_t)NU * E, sg, out, NU, E, 1, stream);
     }
 
-    // src/qwen_model.cpp:1137-1166
+    // src/qwen_model.cpp:1137-1166. Grouped, with a down projection that reads Q8_0: SwiGLU and its quantization in
+    // the gate / up GEMM's epilogue (the same bits as gpu_swiglu's, one launch and the g / u round trip fewer)
+    bool swiglu_done = false;
     if (L.grouped) {
         PQ_TRY(gpu_moe_group(L.ids, T, NU, NE, L.tile, L.tok, L.pair, L.ntiles, L.te, L.ts, L.tn, stream));
-        PQ_TRY(qmatvec_launch_q8_id_batch_pair(w->type_gate_up, w->gate_exps, w->up_exps, w->rb_gate_up, q8_xn, L.g,
-                                               L.u, FE, E, L.max_tiles, L.tile, L.ntiles, L.te, L.ts, L.tn, L.tok,
-                                               L.pair, stream));
+        if (!qx.qK && qmatvec_q8_id_batch_swiglu_supported(w->type_gate_up, FE, E)) {
+            PQ_TRY(qmatvec_launch_q8_id_batch_swiglu(w->type_gate_up, w->gate_exps, w->up_exps, w->rb_gate_up, q8_xn,
+                                                     &qx, FE, E, L.max_tiles, L.tile, L.ntiles, L.te, L.ts, L.tn,
+                                                     L.tok, L.pair, stream));
+            swiglu_done = true;
+        } else {
+            PQ_TRY(qmatvec_launch_q8_id_batch_pair(w->type_gate_up, w->gate_exps, w->up_exps, w->rb_gate_up, q8_xn,
+                                                   L.g, L.u, FE, E, L.max_tiles, L.tile, L.ntiles, L.te, L.ts, L.tn,
+                                                   L.tok, L.pair, stream));
+        }
     } else {
         PQ_TRY(qmatvec_launch_q8_id_pair(w->type_gate_up, w->gate_exps, w->up_exps, w->rb_gate_up, L.ids, NU, 0, q8_xn,
                                          L.g, L.u, FE, E, T, stream));
@@ -219,7 +228,7 @@ hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qm
     }
     if (fuse) PQ_TRY(fused(nullptr, L.down, NU, T));
     if (!fuse) {
-        PQ_TRY(gpu_swiglu(L.g, L.u, L.act, T * NU * FE, &qx, stream));
+        if (!swiglu_done) PQ_TRY(gpu_swiglu(L.g, L.u, L.act, T * NU * FE, &qx, stream));
         if (L.grouped)
             PQ_TRY(qmatvec_launch_q8_id_batch(w->type_down, w->down_exps, w->rb_down, &qx, L.down, E, FE, L.max_tiles,
                                               L.tile, L.ntiles, L.te, L.ts, L.tn, L.pair, L.pair, stream));

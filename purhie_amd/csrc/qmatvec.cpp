@@ -605,6 +605,42 @@ hipError_t qmatvec_launch_q8_id_batch_pair(int type, const void *W, const void *
                    out_rows, stream);
 }
 
+// the pair with SwiGLU and its Q8_0 quantization in the epilogue (no counterpart in the reference: its engine runs
+// the two GEMMs, then gpu_swiglu): h's rows out_rows[] get the bits gpu_swiglu's quantizer would write (q0, d0, and
+// s0 where h binds it; the Q8_K side is not written)
+int qmatvec_q8_id_batch_swiglu_supported(int type, int N, int K) {
+    return qmatvec_q8_id_batch_supported(type, K) && id_gemm_ok(type, N, K) && gemm_split(type) &&
+                   N % gemm_split_swiglu_rows() == 0
+               ? 1
+               : 0;
+}
+
+hipError_t qmatvec_launch_q8_id_batch_swiglu(int type, const void *W, const void *W2, size_t row_bytes,
+                                             const qmatvec_q8 *q, const qmatvec_q8 *h, int N, int K, int max_tiles,
+                                             int tile, const int32_t *n_tiles, const int32_t *tile_e,
+                                             const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
+                                             const int32_t *out_rows, hipStream_t stream) {
+    if (!qmatvec_q8_id_batch_swiglu_supported(type, N, K)) return hipErrorInvalidDeviceFunction;
+    if (!q || !h || !h->q0 || !h->d0 || !W || !W2 || max_tiles <= 0 || tile <= 0 ||
+        tile > qmatvec_id_batch_tile(type, N, K) || row_bytes != qt_row_size(type, K) ||
+        (((uintptr_t)W | (uintptr_t)W2) & (w_align(type) - 1)) != 0)
+        return hipErrorInvalidValue;
+    GemmArgs a = gemm_args(type, W, row_bytes, q, nullptr, N, K);
+    a.n_tiles = n_tiles;
+    a.tile_e = tile_e;
+    a.tile_start = tile_start;
+    a.tile_n = tile_n;
+    a.in_rows = in_rows;
+    a.out_rows = out_rows;
+    expert_scale(W, a.es, a.osc);
+    a.W2 = (const uint8_t *)W2;
+    expert_scale(W2, a.es2, a.osc2);
+    a.hq = h->q0;
+    a.hd = h->d0;
+    a.hs = h->s0;
+    return launch_gemm_split(type, a, dim3((unsigned)(N / gemm_split_swiglu_rows()), (unsigned)max_tiles), stream);
+}
+
 hipError_t qmatvec_debug_capture(int32_t *out, size_t n_ints) {
     g_cap = out;
     g_cap_n = out ? n_ints : 0;

@@ -76,6 +76,9 @@ def lib():
             "qmatvec_launch_q8_id_pair_routed": (i32, [i32, vp, vp, sz, vp, i32, vp, vp, i32, pq8, vp, vp, i32, i32, i32,
                                                        vp]),
             "qmatvec_launch_q8_id_x": (i32, [i32, vp, vp, vp, vp, sz, vp, i32, i32, pq8, vp, vp, i32, i32, i32, vp]),
+            "qmatvec_q8_id_batch_swiglu_supported": (i32, [i32, i32, i32]),
+            "qmatvec_launch_q8_id_batch_swiglu": (i32, [i32, vp, vp, sz, pq8, pq8, i32, i32, i32, i32, vp, vp, vp, vp,
+                                                        vp, vp, vp]),
             "qmatvec_id_batch_tile": (i32, [i32, i32, i32]),
             "qmatvec_q8_id_batch_supported": (i32, [i32, i32]),
             "qmatvec_launch_q8_id_batch": (i32, [i32, vp, sz, pq8, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp,

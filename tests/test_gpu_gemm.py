@@ -164,6 +164,63 @@ def test_moe_tiled_gemm_pair(Q, oracle, t, N, K):
     assert np.array_equal(b.view(np.uint32), d.view(np.uint32))
 
 
+@pytest.mark.parametrize("t,N,K", [(100, 768, 2048), (101, 256, 1024), (40, 768, 2048), (100, 384, 512)])
+def test_moe_tiled_gemm_swiglu(Q, oracle, t, N, K):
+    """qmatvec_launch_q8_id_batch_swiglu (the gate / up pair with SwiGLU and its Q8_0 quantization in the epilogue):
+    q0, d0 and s0 of every entry's row bit for bit those of the pair launch followed by gpu_swiglu, with per-expert
+    output scales on both matrices and tiles with padding entries"""
+    import ctypes as C
+    import torch
+    from purhie_amd import moe as M
+    E, n_used, T = 12, 4, 56
+    L = Q.lib()
+    assert L.qmatvec_q8_id_batch_swiglu_supported(t, N, K) == 1
+    Wg = dev(oracle.quantize(t, synth.gaussian(90 + t, E * N * K, 0, 0.02).reshape(E * N, K)))
+    Wu = dev(oracle.quantize(t, synth.gaussian(91 + t, E * N * K, 0, 0.02).reshape(E * N, K)))
+    ids = (synth.splitmix64(92, T * n_used) % np.uint64(E)).astype(np.int32).reshape(T, n_used)
+    tile = L.qmatvec_id_batch_tile(t, N, K)
+    g = oracle.moe_group(ids, E, tile)
+    x = acts(93, T, K)
+    q = Q.Q8(((T * K + 255) // 256) * 256)
+    Q.quantize(dev(x.reshape(-1)), T * K, q)
+    p = lambda a: C.c_void_p(a.data_ptr())
+    bufs = [dev(np.array([g["n_tiles"]], np.int32)), dev(g["tile_e"]), dev(g["tile_start"]), dev(g["tile_n"]),
+            dev(g["tok_rows"]), dev(g["pair_rows"])]
+    rb, mt, R = Q.row_size(t, K), g["n_tiles"] + 2, T * n_used
+    owners = (C.c_void_p(0x81), C.c_void_p(0x82))
+    es = [torch.tensor([0.5 + 0.125 * ((e * (m + 3)) % E) for e in range(E)], dtype=torch.float32).pin_memory()
+          for m in range(2)]
+    for o, W, s in zip(owners, (Wg, Wu), es):
+        assert L.qmatvec_set_out_scale(o, p(W), W.numel(), p(s), E) == 0
+    try:
+        yg = torch.full((R, N), float("nan"), device="cuda")
+        yu = torch.full((R, N), float("nan"), device="cuda")
+        assert L.qmatvec_launch_q8_id_batch_pair(t, p(Wg), p(Wu), rb, q.ref, p(yg), p(yu), N, K, mt, tile,
+                                                 *[p(b) for b in bufs], None) == 0
+        want = Q.Q8(R * N)
+        h = torch.zeros(R * N, device="cuda")
+        assert M.lib().gpu_swiglu(p(yg), p(yu), p(h), R * N, want.ref, None) == 0
+        got = Q.Q8(R * N)
+        got.mem.fill_(0x5A)  # every byte the launch owns must be written
+        assert L.qmatvec_launch_q8_id_batch_swiglu(t, p(Wg), p(Wu), rb, q.ref, got.ref, N, K, mt, tile,
+                                                   *[p(b) for b in bufs], None) == 0
+        torch.cuda.synchronize()
+    finally:
+        for o in owners:
+            L.qmatvec_drop_out_scales(o)
+    a, b = want.views(R * N), got.views(R * N)
+    assert torch.isfinite(a["d0"]).all() and (a["d0"] != 0).any()
+    for f in ("q0", "d0", "s0"):
+        assert torch.equal(a[f].view(torch.uint8), b[f].view(torch.uint8)), f
+
+
+def test_moe_tiled_gemm_swiglu_refused(Q):
+    L = Q.lib()
+    assert L.qmatvec_q8_id_batch_swiglu_supported(12, 768, 2048) == 0  # a K-quant: no split GEMM
+    assert L.qmatvec_q8_id_batch_swiglu_supported(100, 200, 2048) == 0  # N % 128
+    assert L.qmatvec_q8_id_batch_swiglu_supported(100, 768, 2048) == 1
+
+
 @pytest.fixture(params=["tile", "wave"])
 def kpath(request, monkeypatch):
     """the decode kernels under test: the one-unit-per-lane tile kernels or the per-wave kernels"""
