@@ -22,6 +22,7 @@
 //     or finishes a super-block. K stages of 64 double-buffered in LDS with one barrier a stage; each stage's
 //     global loads are issued two stages ahead (two register sets). The dense grid is renumbered XCD by XCD
 //     (xcd_tile). MoE expert tiles: 64 tokens x 64 rows (4 waves of 32 x 32).
+#include <atomic>
 #include <type_traits>
 
 #include "device.h"
@@ -757,11 +758,16 @@ template <int TYPE, int WI, int WT, bool MOE, bool CAP>
 static hipError_t launch_i8kq_t(const GemmArgs &a, dim3 grid, hipStream_t stream) {
     using G = I8Geo<WI, WT>;
     auto k = k_gemm_i8kq<TYPE, WI, WT, MOE, CAP>;
-    static bool attr = false;  // (per instantiation, once: the tile's LDS is above the default 64 KiB)
-    if (!attr) {
+    // the tile's LDS is above the default 64 KiB: the attribute is set once per instantiation and device (a
+    // second setting, from a racing thread, is harmless)
+    static std::atomic<unsigned long long> set_on{0};
+    int dev = 0;
+    if (const hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+    const unsigned long long bit = dev < 64 ? 1ull << dev : 0ull;  // (past 64 devices: set at every launch)
+    if (!bit || !(set_on.load(std::memory_order_acquire) & bit)) {
         const hipError_t e = hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, G::BYTES);
         if (e != hipSuccess) return e;
-        attr = true;
+        set_on.fetch_or(bit, std::memory_order_release);
     }
     hipLaunchKernelGGL(k, grid, dim3(I8_THREADS), G::BYTES, stream, a);
     return hipGetLastError();
