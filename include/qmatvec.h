@@ -8,7 +8,8 @@
  * with no internal synchronisation. Errors: hipErrorInvalidDeviceFunction (no kernel for this type /
  * shape), hipErrorInvalidValue (bad shape, alignment, capacity); launch errors pass through.
  *
- * Types with int8 kernels: Q8_0 (8), Q4_K (12), Q6_K (14), Q4_0_ROCMFP4 (100), Q4_0_ROCMFP4_FAST (101).
+ * Types with int8 kernels: Q8_0 (8), Q4_K (12), Q5_K (13), Q6_K (14), IQ4_XS (23), MXFP4 (39), NVFP4 (40),
+ * Q4_0_ROCMFP4 (100), Q4_0_ROCMFP4_FAST (101). No launch allocates device memory.
  */
 #ifndef PURHIE_QMATVEC_H
 #define PURHIE_QMATVEC_H
@@ -45,8 +46,8 @@ int qmatvec_supported(int type);
  * the fp32 activations as they are. Same arguments, checks and error codes as the reference's.
  *   qmatvec_launch_bf16f    BF16 weights (row_bytes = 2 K), fp32 activations not rounded, T rows
  *   qmatvec_launch          one row of x; type F32 / F16 / BF16, row_bytes = qt_row_size(type, K)
- *   qmatvec_launch_batch    T rows; F16 / BF16 batches qmatvec_half_supported takes go to the MFMA GEMM (the
- *                           16-bit copy of x in a stream-ordered pool buffer), the rest to the decode kernel
+ *   qmatvec_launch_batch    T rows; F16 / BF16 batches qmatvec_half_supported takes go to the MFMA GEMM (which
+ *                           rounds x while staging it: nothing allocated), the rest to the decode kernel
  *   qmatvec_launch_batch_h  the same with the caller's scratch xh (16-byte aligned, xh_bytes >= 2 T K) for the copy
  *   qmatvec_half_supported  F16 / BF16, GEMMs on, T >= 32 (any T in prefill mode), N >= 64, K % 8 == 0,
  *                           row_bytes >= 2 K and a multiple of 16, W 16-byte aligned
