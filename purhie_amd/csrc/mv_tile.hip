@@ -602,8 +602,10 @@ struct SwStager {
 // One tile: rows [row0, row0 + nr) of one matrix (contiguous, nb units each, nr * nb <= THR). SW: the activation
 // is SwiGLU(sg, su) quantized here (NT 1, a Q8_0-activation type), else q / d / bs staged as they are. CAP
 // (capture mode): every unit's integer group dots are added into cap (row r's groups at cap + r * K / G, token t
-// cap_ts further on; r counted as row0 is).
-template <int TYPE, int NT, int THR, class Rows, bool SW = false, bool CAP = false>
+// cap_ts further on; r counted as row0 is). NP < NT (tokens whose activation does not fit the tile's LDS at once):
+// the activation is staged NP tokens at a time into the same LDS while each lane keeps its unit's weights in
+// registers, so the weights are still read once; every token's arithmetic is the single-token one.
+template <int TYPE, int NT, int THR, class Rows, bool SW = false, bool CAP = false, int NP = NT>
 __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int row0, int nr, int K, int nb, int lg,
                                           const int8_t *q, const float *d, const int32_t *bs,
                                           const float *sg = nullptr, const float *su = nullptr,
@@ -611,9 +613,10 @@ __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int r
     using P = Tu<TYPE>;
     using TL = TileLds<TYPE>;
     static_assert(!SW || (NT == 1 && P::ACT == 32 && P::SUMS == 0), "SwiGLU staging: one token, Q8_0 activation");
-    const TL L(K, NT, THR);
+    static_assert(NT % NP == 0 && (!SW || NP == NT), "staging passes of NP tokens");
+    const TL L(K, NP, THR);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    Stager<TYPE, NT, THR> st;
+    Stager<TYPE, NP, THR> st;
     SwStager<TYPE, THR> sws;
     if constexpr (SW) sws.issue(sg, su, K);
     else st.issue(L, q, d, bs, K);
@@ -661,13 +664,31 @@ __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int r
     x.nd = L.nd;
     x.ns = L.ns;
     float acc[NT];
-    if constexpr (CAP) {
-        constexpr int G = cap_group(TYPE);
-        const DotCap dc{tid < nu ? cap + (long long)(row0 + u / nb) * (K / G) + (long long)k * (P::VALS / G) : nullptr,
-                        cap_ts};
-        P::template compute<NT>(w, aux, x, acc, dc);
-    } else {
-        P::template compute<NT>(w, aux, x, acc, NoCap{});
+#pragma unroll
+    for (int pass = 0; pass < NT / NP; ++pass) {
+        if (pass > 0) {  // (uniform) the next NP tokens' activation, once every wave has read the previous pass's
+            __syncthreads();
+            const int8_t *qp = q + (long long)pass * NP * K;
+            const float *dp = d + (long long)pass * NP * L.nd;
+            const int32_t *bp = bs ? bs + (long long)pass * NP * (K / 16) : nullptr;
+            Stager<TYPE, NP, THR> sp;
+            sp.issue(L, qp, dp, bp, K);
+            sp.commit(L, smem, qp, dp, bp, K);
+            __syncthreads();
+        }
+        float ap[NP];
+        if constexpr (CAP) {
+            constexpr int G = cap_group(TYPE);
+            const DotCap dc{tid < nu ? cap + (long long)(row0 + u / nb) * (K / G) + (long long)k * (P::VALS / G) +
+                                           (long long)pass * NP * cap_ts
+                                     : nullptr,
+                            cap_ts};
+            P::template compute<NP>(w, aux, x, ap, dc);
+        } else {
+            P::template compute<NP>(w, aux, x, ap, NoCap{});
+        }
+#pragma unroll
+        for (int t = 0; t < NP; ++t) acc[pass * NP + t] = ap[t];
     }
 
     // partials into the wave's own region (its units were read above; LDS is in order within a wave)
@@ -711,7 +732,7 @@ static TileArgs tile_args(int nb, int thr) {
     return ta;
 }
 
-template <int TYPE, int NT, int THR, bool CAP = false>
+template <int TYPE, int NT, int THR, bool CAP = false, int NP = NT>
 __global__ void __launch_bounds__(THR) k_mv_tile(MvArgs a, TileArgs ta) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const DenseRows rows{a};
@@ -721,8 +742,9 @@ __global__ void __launch_bounds__(THR) k_mv_tile(MvArgs a, TileArgs ta) {
     const int row0 = rows.base(m) + (bx - first) * ta.R;
     const int end = DenseRows::pick(m, a.bound[0], a.bound[1], a.bound[2], a.bound[3]);
     const int nr = end - row0 < ta.R ? end - row0 : ta.R;
-    tile_body<TYPE, NT, THR, DenseRows, false, CAP>(smem, rows, row0, nr, a.K, ta.nb, ta.lg, a.q, a.d, a.bs, nullptr,
-                                                    nullptr, a.cap, (long long)a.Nt * (a.K / cap_group(TYPE)));
+    tile_body<TYPE, NT, THR, DenseRows, false, CAP, NP>(smem, rows, row0, nr, a.K, ta.nb, ta.lg, a.q, a.d, a.bs,
+                                                        nullptr, nullptr, a.cap,
+                                                        (long long)a.Nt * (a.K / cap_group(TYPE)));
 }
 
 // MoE: grid (tiles, n_used * nmat, T); slot j of token t uses expert ids[t * n_used + j] (-1: Wx). Tiles mode:
@@ -773,12 +795,21 @@ static bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)
 // in 64 KiB, and the operands are aligned for the wide reads: weight matrices 16 bytes with rows a multiple
 // of 16 (Q4_K, ROCmFP4) or 8 (Q8_0, ROCmFP4_FAST) bytes (Q6_K: any even row), activation values 16 bytes,
 // scales 4, Q4_K's paired group sums 8.
+// Tokens a tile stages at a time: all NT when their activation fits the tile's 64 KiB of LDS, else the largest
+// divisor of NT that does (passes over the same weights), 0 when none does
+template <int TYPE>
+static int tile_pass(int K, int NT) {
+    for (int np = NT; np >= 1; --np)
+        if (NT % np == 0 && TileLds<TYPE>(K, np, TL_THREADS).bytes <= 65536) return np;
+    return 0;
+}
+
 template <int TYPE>
 static bool tile_takes(int K, int NT, const uint8_t *const *W, int nW, long long row_bytes, const void *q,
                        const void *d, const void *bs) {
     using P = Tu<TYPE>;
     if (K <= 0 || K % P::VALS || K / P::VALS > TL_THREADS) return false;
-    if (TileLds<TYPE>(K, NT, TL_THREADS).bytes > 65536) return false;
+    if (tile_pass<TYPE>(K, NT) == 0) return false;
     for (int i = 0; i < nW; ++i)
         if (!aligned(W[i], 16)) return false;
     if (row_bytes % (P::LEAD == 0 ? 16 : P::LEAD == 8 ? 8 : 2)) return false;
@@ -804,7 +835,7 @@ static int tile_threads(int nb, long long rows) {
     return thr;
 }
 
-template <int TYPE, int NT, int THR>
+template <int TYPE, int NT, int THR, int NP = NT>
 static hipError_t tile_dense_thr(const MvArgs &a, hipStream_t stream) {
     TileArgs ta = tile_args(a.K / Tu<TYPE>::VALS, THR);
     int tiles = 0, lo = 0;
@@ -814,9 +845,10 @@ static hipError_t tile_dense_thr(const MvArgs &a, hipStream_t stream) {
         ta.tp[i] = tiles;
         lo = a.bound[i] > lo ? a.bound[i] : lo;
     }
-    const size_t lds = (size_t)TileLds<TYPE>(a.K, NT, THR).bytes;
-    if (a.cap) hipLaunchKernelGGL((k_mv_tile<TYPE, NT, THR, true>), dim3((unsigned)tiles), dim3(THR), lds, stream, a, ta);
-    else hipLaunchKernelGGL((k_mv_tile<TYPE, NT, THR>), dim3((unsigned)tiles), dim3(THR), lds, stream, a, ta);
+    const size_t lds = (size_t)TileLds<TYPE>(a.K, NP, THR).bytes;
+    if (a.cap)
+        hipLaunchKernelGGL((k_mv_tile<TYPE, NT, THR, true, NP>), dim3((unsigned)tiles), dim3(THR), lds, stream, a, ta);
+    else hipLaunchKernelGGL((k_mv_tile<TYPE, NT, THR, false, NP>), dim3((unsigned)tiles), dim3(THR), lds, stream, a, ta);
     return hipGetLastError();
 }
 
@@ -825,6 +857,13 @@ static hipError_t tile_dense(const MvArgs &a, hipStream_t stream) {
     int nW = 1;
     while (nW < 4 && a.bound[nW - 1] < a.Nt) ++nW;
     if (!tile_takes<TYPE>(a.K, NT, a.W, nW, a.row_bytes, a.q, a.d, a.bs)) return hipErrorNotSupported;
+    // staging passes (a large K at several tokens): whole 256-thread tiles, whose rows are many
+    if constexpr (NT > 1) {
+        const int np = tile_pass<TYPE>(a.K, NT);
+        if (np == 1) return tile_dense_thr<TYPE, NT, 256, 1>(a, stream);
+        if constexpr (NT == 4)
+            if (np == 2) return tile_dense_thr<TYPE, NT, 256, 2>(a, stream);
+    }
     switch (tile_threads(a.K / Tu<TYPE>::VALS, a.Nt)) {
     case 64: return tile_dense_thr<TYPE, NT, 64>(a, stream);
     case 128: return tile_dense_thr<TYPE, NT, 128>(a, stream);

@@ -72,7 +72,10 @@ def cap_buf(n):
 DECODE = [(8, 3072, 1024, 1), (12, 9728, 2560, 1), (12, 2560, 9728, 1), (12, 9728, 2560, 4), (12, 2560, 9728, 4),
           (100, 768, 2048, 1), (100, 2048, 768, 1), (100, 17408 // 8, 5120, 2), (101, 768, 2048, 3),
           (14, 2048, 1024, 1), (14, 3072, 1024, 4), (13, 1024, 2560, 2), (23, 1024, 2560, 1), (39, 768, 2048, 2),
-          (40, 768, 2048, 1), (8, 2048, 3072, 4)]
+          (40, 768, 2048, 1), (8, 2048, 3072, 4),
+          # tokens whose activation passes the tile's LDS: staged a few at a time (Q8_0 two passes of 2, Q6_K three
+          # of 1, ROCmFP4 two of 1)
+          (8, 512, 8192, 4), (14, 300, 5120, 3), (100, 256, 12288, 2)]
 
 
 @pytest.mark.parametrize("t,N,K,T", DECODE)
