@@ -173,9 +173,10 @@ int matvec_lanes(int type, int K, long long rows);
 // Decode tuning, read from the environment once per process: PURHIE_MV_TILE=0 sends every shape to the per-wave
 // kernels (tile 0; qmatvec_debug_decode_path changes it at run time), PURHIE_MV_THREADS fixes the tile kernel's
 // workgroup size (64 / 128 / 256, else 0 = chosen per launch), PURHIE_MV_LANES the per-wave kernels' lanes per row
-// (8 .. 64, a power of two, else 0 = chosen per shape)
+// (8 .. 64, a power of two, else 0 = chosen per shape), PURHIE_MV_BALANCE=0 keeps the tile kernel's rows a tile at
+// their most (balance 0) instead of fewer where that lightens the most loaded CU
 struct MvTune {
-    int tile, threads, lanes;
+    int tile, threads, lanes, balance;
 };
 const MvTune &mv_tune();
 void mv_tune_set_tile(int on);

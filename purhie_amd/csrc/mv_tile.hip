@@ -835,9 +835,57 @@ static int tile_threads(int nb, long long rows) {
     return thr;
 }
 
+// CUs of the current device (read once per device)
+static int device_cus() {
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = __atomic_load_n(&cus[dev], __ATOMIC_RELAXED);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        __atomic_store_n(&cus[dev], n, __ATOMIC_RELAXED);
+    }
+    return n;
+}
+
+// Rows a 256-thread tile takes: at most 256 / nb, and fewer where that lightens the most loaded CU. Every tile of a
+// launch is resident at once, so the launch lasts about as long as the CU with the most tiles; its rows,
+// ceil(tiles / CUs) R, are what is minimised, over tile counts that stay resident (LDS: resident tiles a CU <=
+// 160 KiB / lds). Config 2's pair launch: 25 rows a tile, 780 tiles, 4 on some CUs = 100 rows; 19 rows, 1024 tiles
+// = 76 rows. The matrices have n[0..nm) rows, each launched `copies` times (expert slots, tokens). A row's sum does
+// not depend on R. (Smaller tiles, whose per-workgroup costs weigh more, keep thr / nb: config 1's 64-thread tiles
+// measured slower balanced.)
+static int tile_rows_balanced(int Rmax, const int *n, int nm, long long copies, int lds) {
+    if (!mv_tune().balance) return Rmax;
+    const int ncu = device_cus(), resident = lds > 0 ? 163840 / lds : 8;
+    int best = Rmax;
+    long long best_load = -1;
+    for (int R = Rmax; R >= 1 && 2 * R >= Rmax; --R) {
+        long long wgs = 0;
+        for (int i = 0; i < nm; ++i) wgs += n[i] > 0 ? (n[i] + R - 1) / R : 0;
+        wgs *= copies;
+        const long long per_cu = (wgs + ncu - 1) / ncu;
+        if (R < Rmax && per_cu > resident) continue;
+        const long long load = per_cu * R;
+        if (best_load < 0 || load < best_load) {
+            best_load = load;
+            best = R;
+        }
+    }
+    return best;
+}
+
 template <int TYPE, int NT, int THR, int NP = NT>
 static hipError_t tile_dense_thr(const MvArgs &a, hipStream_t stream) {
     TileArgs ta = tile_args(a.K / Tu<TYPE>::VALS, THR);
+    if constexpr (THR == 256) {
+        int n[4];
+        for (int i = 0, lo = 0; i < 4; ++i) {
+            n[i] = a.bound[i] - lo;
+            lo = a.bound[i] > lo ? a.bound[i] : lo;
+        }
+        ta.R = tile_rows_balanced(ta.R, n, 4, 1, TileLds<TYPE>(a.K, NP, THR).bytes);
+    }
     int tiles = 0, lo = 0;
     for (int i = 0; i < 4; ++i) {
         const int n = a.bound[i] - lo;
@@ -899,7 +947,9 @@ hipError_t launch_matvec_tile(int type, const MvArgs &a, hipStream_t stream) {
 
 template <int TYPE, int THR>
 static hipError_t tile_id_thr(const MvIdArgs &a, hipStream_t stream) {
-    const TileArgs ta = tile_args(a.K / Tu<TYPE>::VALS, THR);
+    TileArgs ta = tile_args(a.K / Tu<TYPE>::VALS, THR);
+    if (THR == 256 && !a.n_tiles) ta.R = tile_rows_balanced(ta.R, &a.N, 1, (long long)a.n_used * a.nmat * a.T,
+                                                             TileLds<TYPE>(a.K, 1, THR).bytes);
     const unsigned gx = (unsigned)((a.N + ta.R - 1) / ta.R);
     const dim3 grid = a.n_tiles ? dim3(gx, (unsigned)a.tile, (unsigned)a.max_tiles)
                                 : dim3(gx, (unsigned)(a.n_used * a.nmat), (unsigned)a.T);
