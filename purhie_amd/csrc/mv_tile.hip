@@ -474,19 +474,26 @@ struct TileLds {
 
 constexpr int TL_QN = 4, TL_DN = 2, TL_SN = 4;  // activation loads a thread holds across the weight issue
 
-// Stage the activation of NT tokens (global: values q + t K, scales d + t nd, Q8_K 16-value sums
-// bs + t K / 16) into LDS. Each thread's first TL_QN value chunks, TL_DN scales and TL_SN group sums are
-// loaded by issue() (before the weights), anything beyond by commit(). Q4_K's 32-value sums are the two
-// 16-value sums added when written (nothing in issue() waits for a load).
+// Stage the activation of NT tokens (global: values q + t K, scales d + t nd, Q8_K 16-value sums bs + t K / 16)
+// into LDS. Each thread's first TL_QN value chunks, TL_DN scales and TL_SN group sums are loaded by issue() (before
+// the weights), anything beyond by commit(); nothing in issue() waits for a load. The K-quants' group sums: one
+// token (FORM) forms them from the staged values, exact integers equal to the sums in memory, which are then not
+// read (half the bytes a tile loads: config 2's step 13.47 -> 13.24 us); several tokens, whose tiles are bound by
+// their arithmetic rather than their loads, load them (measured 1.5% faster at T = 4). Q6_K's 16-value group is
+// one chunk, Q4_K's 32-value group a chunk and its even / odd neighbour, which thread tid ^ 1 holds; loaded,
+// Q4_K's 32-value sums are the two 16-value sums added when written.
 template <int TYPE, int NT, int THR>
 struct Stager {
     static constexpr bool PAIR = Tu<TYPE>::SUMS == 32;
+    static constexpr bool FORM = Tu<TYPE>::SUMS != 0 && NT == 1;  // sums formed here (else loaded, if any)
+    static constexpr bool LOAD = Tu<TYPE>::SUMS != 0 && !FORM;
     int4 qv[TL_QN];
     float dv[TL_DN];
     int2 sv[TL_SN];
     int nq, ndt, nst;
 
-    __device__ __forceinline__ void issue(const TileLds<TYPE> &L, const int8_t *q, const float *d, const int32_t *bs, int K) {
+    __device__ __forceinline__ void issue(const TileLds<TYPE> &L, const int8_t *q, const float *d, const int32_t *bs,
+                                          int K) {
         nq = NT * K / 16;
         ndt = NT * L.nd;
         nst = NT * L.ns;
@@ -503,7 +510,7 @@ struct Stager {
             const int e = tid + i * THR;
             dv[i] = d[e < ndt ? e : ndt - 1];
         }
-        if (Tu<TYPE>::SUMS) {
+        if constexpr (LOAD) {
 #pragma unroll
             for (int i = 0; i < TL_SN; ++i) {
                 const int e = tid + i * THR;
@@ -515,37 +522,49 @@ struct Stager {
         if (PAIR) return *(const int2 *)(bs + 2 * (long long)e);
         return make_int2(bs[e], 0);
     }
-    __device__ static __forceinline__ void put_q(const TileLds<TYPE> &L, uint8_t *smem, int K, int c, int4 v) {
-        const int per = K / 16, t = c / per, cc = c - t * per;
-        *(int4 *)(smem + t * L.xt + (cc >> 4) * TL_PAD + (cc & 15) * 16) = v;
-    }
     __device__ static __forceinline__ void put_s(const TileLds<TYPE> &L, uint8_t *smem, int e, int2 v) {
         ((int32_t *)(smem + L.off_s))[e] = PAIR ? v.x + v.y : v.x;
+    }
+    // chunk c's 16 values into LDS (c < nq: active) and, with FORM, its group sum. With FORM every lane calls it
+    // (the pair's shuffle); c and c ^ 1 are both below nq or both not (nq is even)
+    __device__ __forceinline__ void put(const TileLds<TYPE> &L, uint8_t *smem, int K, int c, int4 v) const {
+        const bool active = c < nq;
+        if constexpr (FORM) {
+            int s = dot4(v.x, 0x01010101, 0);
+            s = dot4(v.y, 0x01010101, s);
+            s = dot4(v.z, 0x01010101, s);
+            s = dot4(v.w, 0x01010101, s);
+            if (PAIR) s += __shfl_xor(s, 1, 64);
+            if (active && (!PAIR || (c & 1) == 0)) ((int32_t *)(smem + L.off_s))[PAIR ? c >> 1 : c] = s;
+        }
+        if (active) {
+            const int per = K / 16, t = c / per, cc = c - t * per;
+            *(int4 *)(smem + t * L.xt + (cc >> 4) * TL_PAD + (cc & 15) * 16) = v;
+        }
     }
     __device__ __forceinline__ void commit(const TileLds<TYPE> &L, uint8_t *smem, const int8_t *q, const float *d,
                                            const int32_t *bs, int K) {
         const int tid = threadIdx.x;
         float *ld = (float *)(smem + L.off_d);
 #pragma unroll
-        for (int i = 0; i < TL_QN; ++i) {
-            const int c = tid + i * THR;
-            if (c < nq) put_q(L, smem, K, c, qv[i]);
-        }
+        for (int i = 0; i < TL_QN; ++i)
+            if (i * THR < nq) put(L, smem, K, tid + i * THR, qv[i]);  // (uniform)
 #pragma unroll
         for (int i = 0; i < TL_DN; ++i) {
             const int e = tid + i * THR;
             if (e < ndt) ld[e] = dv[i];
         }
-        if (Tu<TYPE>::SUMS) {
+        if constexpr (LOAD) {
 #pragma unroll
             for (int i = 0; i < TL_SN; ++i) {
                 const int e = tid + i * THR;
                 if (e < nst) put_s(L, smem, e, sv[i]);
             }
         }
-        for (int c = tid + TL_QN * THR; c < nq; c += THR) put_q(L, smem, K, c, *(const int4 *)(q + 16 * (long long)c));
+        // the rest (a thread and its tid ^ 1 partner leave the first loop together)
+        for (int c = tid + TL_QN * THR; c < nq; c += THR) put(L, smem, K, c, *(const int4 *)(q + 16 * (long long)c));
         for (int e = tid + TL_DN * THR; e < ndt; e += THR) ld[e] = d[e];
-        if (Tu<TYPE>::SUMS)
+        if constexpr (LOAD)
             for (int e = tid + TL_SN * THR; e < nst; e += THR) put_s(L, smem, e, load_s(bs, e));
         if constexpr (Tu<TYPE>::LUT)
             for (int e = tid; e < 256; e += THR) ((float *)(smem + L.off_lut))[e] = Tu<TYPE>::scale((uint32_t)e);
