@@ -176,7 +176,7 @@ int matvec_lanes(int type, int K, long long rows);
 // (8 .. 64, a power of two, else 0 = chosen per shape), PURHIE_MV_BALANCE=0 keeps the tile kernel's rows a tile at
 // their most (balance 0) instead of fewer where that lightens the most loaded CU
 struct MvTune {
-    int tile, threads, lanes, balance;
+    int tile, threads, lanes, balance, trim;
 };
 const MvTune &mv_tune();
 void mv_tune_set_tile(int on);

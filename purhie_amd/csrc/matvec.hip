@@ -754,9 +754,10 @@ int matvec_lanes(int type, int K, long long rows) {
 
 namespace {
 MvTune tune_from_env() {
-    MvTune t{1, 0, 0, 1};
+    MvTune t{1, 0, 0, 1, 1};
     if (const char *e = getenv("PURHIE_MV_TILE")) t.tile = e[0] == '0' ? 0 : 1;
     if (const char *e = getenv("PURHIE_MV_BALANCE")) t.balance = e[0] == '0' ? 0 : 1;
+    if (const char *e = getenv("PURHIE_MV_TRIM")) t.trim = e[0] == '0' ? 0 : 1;
     if (const char *e = getenv("PURHIE_MV_THREADS")) {
         const int v = atoi(e);
         t.threads = v == 64 || v == 128 || v == 256 ? v : 0;

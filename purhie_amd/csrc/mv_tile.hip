@@ -867,43 +867,78 @@ static int device_cus() {
     return n;
 }
 
-// Rows a 256-thread tile takes: at most 256 / nb, and fewer where that lightens the most loaded CU. Every tile of a
-// launch is resident at once, so the launch lasts about as long as the CU with the most tiles; its rows,
+// Rows a tile takes: at most Rmax, and fewer where that lightens the most loaded CU. Every tile of a launch is
+// meant to be resident at once, so the launch lasts about as long as the CU with the most tiles; its rows,
 // ceil(tiles / CUs) R, are what is minimised, over tile counts that stay resident (LDS: resident tiles a CU <=
 // 160 KiB / lds). Config 2's pair launch: 25 rows a tile, 780 tiles, 4 on some CUs = 100 rows; 19 rows, 1024 tiles
 // = 76 rows. The matrices have n[0..nm) rows, each launched `copies` times (expert slots, tokens). A row's sum does
-// not depend on R. (Smaller tiles, whose per-workgroup costs weigh more, keep thr / nb: config 1's 64-thread tiles
-// measured slower balanced.)
-static int tile_rows_balanced(int Rmax, const int *n, int nm, long long copies, int lds) {
-    if (!mv_tune().balance) return Rmax;
+// not depend on R. *load: that figure for the rows returned, doubled when its tiles cannot all be resident.
+// (Smaller tiles, whose per-workgroup costs weigh more, keep thr / nb: config 1's 64-thread tiles measured slower
+// balanced.)
+static int tile_rows_balanced(int Rmax, const int *n, int nm, long long copies, int lds, long long *load = nullptr) {
     const int ncu = device_cus(), resident = lds > 0 ? 163840 / lds : 8;
-    int best = Rmax;
-    long long best_load = -1;
-    for (int R = Rmax; R >= 1 && 2 * R >= Rmax; --R) {
+    auto load_of = [&](int R, bool &fits) {
         long long wgs = 0;
         for (int i = 0; i < nm; ++i) wgs += n[i] > 0 ? (n[i] + R - 1) / R : 0;
         wgs *= copies;
         const long long per_cu = (wgs + ncu - 1) / ncu;
-        if (R < Rmax && per_cu > resident) continue;
-        const long long load = per_cu * R;
-        if (best_load < 0 || load < best_load) {
-            best_load = load;
-            best = R;
+        fits = per_cu <= resident;
+        return per_cu * R * (fits ? 1 : 2);
+    };
+    bool fits = true;
+    int best = Rmax;
+    long long best_load = load_of(Rmax, fits);
+    if (mv_tune().balance)
+        for (int R = Rmax - 1; R >= 1 && 2 * R >= Rmax; --R) {
+            const long long l = load_of(R, fits);
+            if (fits && l < best_load) {
+                best_load = l;
+                best = R;
+            }
         }
-    }
+    if (load) *load = best_load;
     return best;
+}
+
+// Three-wave tiles: beside the 256-thread tile, a 192-thread one of at most 192 / nb rows (its own balanced
+// count) is considered, and taken when its most loaded CU carries no more rows. A four-wave tile of 190 units
+// has a fourth wave that stages, computes on a repeated unit and joins the barriers for nothing, and takes a
+// fourth weight region of LDS: config 2's pair launch at 4 tokens (48 KiB tiles, 3 resident a CU) had 780 tiles
+// of 25 rows, 1024 tiles of 19 rows at 192 threads (39 KiB, 4 a CU) are all resident at once. Rows and every
+// sum are the same (a row's order depends on K alone); PURHIE_MV_TRIM=0 keeps 256.
+constexpr int TL_TRIM = 192;
+static bool tile_trims(const TileArgs &ta) { return ta.R >= 1 && (ta.R << ta.lg) <= TL_TRIM; }
+
+template <int TYPE, int NT, int THR, int NP>
+static hipError_t tile_dense_launch(const MvArgs &a, const TileArgs &ta, int tiles, hipStream_t stream) {
+    const size_t lds = (size_t)TileLds<TYPE>(a.K, NP, THR).bytes;
+    if (a.cap)
+        hipLaunchKernelGGL((k_mv_tile<TYPE, NT, THR, true, NP>), dim3((unsigned)tiles), dim3(THR), lds, stream, a, ta);
+    else hipLaunchKernelGGL((k_mv_tile<TYPE, NT, THR, false, NP>), dim3((unsigned)tiles), dim3(THR), lds, stream, a, ta);
+    return hipGetLastError();
 }
 
 template <int TYPE, int NT, int THR, int NP = NT>
 static hipError_t tile_dense_thr(const MvArgs &a, hipStream_t stream) {
     TileArgs ta = tile_args(a.K / Tu<TYPE>::VALS, THR);
+    bool trim = false;
     if constexpr (THR == 256) {
         int n[4];
         for (int i = 0, lo = 0; i < 4; ++i) {
             n[i] = a.bound[i] - lo;
             lo = a.bound[i] > lo ? a.bound[i] : lo;
         }
-        ta.R = tile_rows_balanced(ta.R, n, 4, 1, TileLds<TYPE>(a.K, NP, THR).bytes);
+        long long load = 0;
+        ta.R = tile_rows_balanced(ta.R, n, 4, 1, TileLds<TYPE>(a.K, NP, THR).bytes, &load);
+        if (NP == NT && mv_tune().trim) {
+            TileArgs tb = tile_args(ta.nb, TL_TRIM);
+            long long lb = 0;
+            if (tb.R >= 1) tb.R = tile_rows_balanced(tb.R, n, 4, 1, TileLds<TYPE>(a.K, NP, TL_TRIM).bytes, &lb);
+            if (tile_trims(tb) && lb <= load) {
+                ta = tb;
+                trim = true;
+            }
+        }
     }
     int tiles = 0, lo = 0;
     for (int i = 0; i < 4; ++i) {
@@ -912,11 +947,9 @@ static hipError_t tile_dense_thr(const MvArgs &a, hipStream_t stream) {
         ta.tp[i] = tiles;
         lo = a.bound[i] > lo ? a.bound[i] : lo;
     }
-    const size_t lds = (size_t)TileLds<TYPE>(a.K, NP, THR).bytes;
-    if (a.cap)
-        hipLaunchKernelGGL((k_mv_tile<TYPE, NT, THR, true, NP>), dim3((unsigned)tiles), dim3(THR), lds, stream, a, ta);
-    else hipLaunchKernelGGL((k_mv_tile<TYPE, NT, THR, false, NP>), dim3((unsigned)tiles), dim3(THR), lds, stream, a, ta);
-    return hipGetLastError();
+    if constexpr (THR == 256 && NP == NT)
+        if (trim) return tile_dense_launch<TYPE, NT, TL_TRIM, NP>(a, ta, tiles, stream);
+    return tile_dense_launch<TYPE, NT, THR, NP>(a, ta, tiles, stream);
 }
 
 template <int TYPE, int NT>
@@ -964,11 +997,21 @@ hipError_t launch_matvec_tile(int type, const MvArgs &a, hipStream_t stream) {
     return hipErrorNotSupported;
 }
 
+// (expert-indexed launches keep four-wave tiles: three-wave ones measured slower there, config 4's decode token
+// 23.2 -> 23.7 us)
+template <int TYPE, int THR>
+static hipError_t tile_id_launch(const MvIdArgs &a, const TileArgs &ta, hipStream_t stream);
+
 template <int TYPE, int THR>
 static hipError_t tile_id_thr(const MvIdArgs &a, hipStream_t stream) {
     TileArgs ta = tile_args(a.K / Tu<TYPE>::VALS, THR);
     if (THR == 256 && !a.n_tiles) ta.R = tile_rows_balanced(ta.R, &a.N, 1, (long long)a.n_used * a.nmat * a.T,
                                                              TileLds<TYPE>(a.K, 1, THR).bytes);
+    return tile_id_launch<TYPE, THR>(a, ta, stream);
+}
+
+template <int TYPE, int THR>
+static hipError_t tile_id_launch(const MvIdArgs &a, const TileArgs &ta, hipStream_t stream) {
     const unsigned gx = (unsigned)((a.N + ta.R - 1) / ta.R);
     const dim3 grid = a.n_tiles ? dim3(gx, (unsigned)a.tile, (unsigned)a.max_tiles)
                                 : dim3(gx, (unsigned)(a.n_used * a.nmat), (unsigned)a.T);
