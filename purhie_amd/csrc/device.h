@@ -126,9 +126,41 @@ __device__ __forceinline__ void k4_scale_min(const uint32_t s[3], int j, int &sc
     }
 }
 
-// butterfly sum over groups of L lanes (L a power of two <= 64), result in every lane of the group
+// Cross-lane reductions without an LDS round trip (a ds_bpermute per step costs ~100 cycles of latency). Within
+// each 16-lane row, DPP joins lane pairs (quad_perm 1,0,3,2), quad halves (2,3,0,1), quads (row_half_mirror: lane
+// i <- 7 - i) and half rows (row_mirror: i <- 15 - i); once the groups below are whole, every lane of a group holds
+// the same value, so each step joins a group with its neighbour. Rows meet through scalar reads of lanes 0, 16, 32,
+// 48. One order for a given L (a power of two <= 64), the result in every lane of the group; all lanes active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+constexpr int DPP_PAIR = 0xb1, DPP_QHALF = 0x4e, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+
 __device__ __forceinline__ float group_sum(float v, int L) {
-    for (int off = L >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
+    if (L >= 2) v += dpp_f<DPP_PAIR>(v);
+    if (L >= 4) v += dpp_f<DPP_QHALF>(v);
+    if (L >= 8) v += dpp_f<DPP_HALF_MIRROR>(v);
+    if (L >= 16) v += dpp_f<DPP_MIRROR>(v);
+    if (L >= 32) {
+        const float a = readlane_f(v, 0) + readlane_f(v, 16), b = readlane_f(v, 32) + readlane_f(v, 48);
+        v = L == 64 ? a + b : (threadIdx.x & 32) ? b : a;
+    }
+    return v;
+}
+
+__device__ __forceinline__ float group_max(float v, int L) {
+    if (L >= 2) v = fmaxf(v, dpp_f<DPP_PAIR>(v));
+    if (L >= 4) v = fmaxf(v, dpp_f<DPP_QHALF>(v));
+    if (L >= 8) v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    if (L >= 16) v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
+    if (L >= 32) {
+        const float a = fmaxf(readlane_f(v, 0), readlane_f(v, 16)), b = fmaxf(readlane_f(v, 32), readlane_f(v, 48));
+        v = L == 64 ? fmaxf(a, b) : (threadIdx.x & 32) ? b : a;
+    }
     return v;
 }
 

@@ -592,9 +592,7 @@ struct SwStager {
                                         float b) {
         float v = 0.0f;
         if (active) v = a / (1.0f + expf(-a)) * b;
-        float am = fabsf(v);
-#pragma unroll
-        for (int off = 16; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+        const float am = group_max(fabsf(v), 32);
         const float id0 = am != 0.0f ? 127.0f / am : 0.0f;
         if (active) {
             smem[(i >> 8) * TL_PAD + (i & 255)] = (uint8_t)(int8_t)(int)rintf(v * id0);
