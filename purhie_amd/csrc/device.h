@@ -152,6 +152,24 @@ __device__ __forceinline__ float group_sum(float v, int L) {
     return v;
 }
 
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+
+__device__ __forceinline__ int group_isum(int v, int L) {
+    if (L >= 2) v += dpp_i<DPP_PAIR>(v);
+    if (L >= 4) v += dpp_i<DPP_QHALF>(v);
+    if (L >= 8) v += dpp_i<DPP_HALF_MIRROR>(v);
+    if (L >= 16) v += dpp_i<DPP_MIRROR>(v);
+    if (L >= 32) {
+        const int a = __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16),
+                  b = __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
+        v = L == 64 ? a + b : (threadIdx.x & 32) ? b : a;
+    }
+    return v;
+}
+
 __device__ __forceinline__ float group_max(float v, int L) {
     if (L >= 2) v = fmaxf(v, dpp_f<DPP_PAIR>(v));
     if (L >= 4) v = fmaxf(v, dpp_f<DPP_QHALF>(v));

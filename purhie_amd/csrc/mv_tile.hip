@@ -534,7 +534,7 @@ struct Stager {
             s = dot4(v.y, 0x01010101, s);
             s = dot4(v.z, 0x01010101, s);
             s = dot4(v.w, 0x01010101, s);
-            if (PAIR) s += __shfl_xor(s, 1, 64);
+            if (PAIR) s += dpp_i<DPP_PAIR>(s);
             if (active && (!PAIR || (c & 1) == 0)) ((int32_t *)(smem + L.off_s))[PAIR ? c >> 1 : c] = s;
         }
         if (active) {

@@ -8,7 +8,7 @@
 //         s0 = fp16((am / 127) * sum q) kept as float bits (the Q8_1 block sum);
 //   Q8_K: per 256 values v = the signed value of largest |x| (lowest index on ties), iscale = -127 / v,
 //         q = min(127, rint(iscale * x)), d = 1 / iscale (0 for an all-zero block), sums of every 16 q.
-// A 32-value Q8_0 block is half a wave: the xor reductions use offsets 16..1, which stay inside it.
+// A 32-value Q8_0 block is half a wave: its reductions stay inside it.
 #pragma once
 
 #include "device.h"
@@ -29,14 +29,10 @@ __device__ __forceinline__ void q8_quantize_value(float v, bool active, int b, Q
     const float a = fabsf(v);
 
     // Q8_0 over the 32 values of this half-wave
-    float am = a;
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+    const float am = group_max(a, 32);
     const float id0 = am != 0.0f ? 127.0f / am : 0.0f;
     const int q0 = active ? (int)rintf(v * id0) : 0;
-    int s0 = q0;
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) s0 += __shfl_xor(s0, off, 64);
+    const int s0 = group_isum(q0, 32);
     if (active) {
         o.q0[i] = (int8_t)q0;
         if ((lane & 31) == 0) {
@@ -55,17 +51,31 @@ __device__ __forceinline__ void q8_quantize_value(float v, bool active, int b, Q
     if (!o.qK) return;  // (uniform)
 
     // Q8_K over the 256 values: largest |x|, the lowest index on ties
+    // (largest |x| with the lowest index is a total order: any order of the pairwise steps picks the same value;
+    // the steps are group_sum's, DPP within rows and scalar reads across them)
     float ba = a, bv = v;
     int bi = t;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float oa = __shfl_xor(ba, off, 64), ov = __shfl_xor(bv, off, 64);
-        const int oi = __shfl_xor(bi, off, 64);
+    auto take = [&](float oa, float ov, int oi) {
         if (oa > ba || (oa == ba && oi < bi)) {
             ba = oa;
             bi = oi;
             bv = ov;
         }
+    };
+    take(dpp_f<DPP_PAIR>(ba), dpp_f<DPP_PAIR>(bv), dpp_i<DPP_PAIR>(bi));
+    take(dpp_f<DPP_QHALF>(ba), dpp_f<DPP_QHALF>(bv), dpp_i<DPP_QHALF>(bi));
+    take(dpp_f<DPP_HALF_MIRROR>(ba), dpp_f<DPP_HALF_MIRROR>(bv), dpp_i<DPP_HALF_MIRROR>(bi));
+    take(dpp_f<DPP_MIRROR>(ba), dpp_f<DPP_MIRROR>(bv), dpp_i<DPP_MIRROR>(bi));
+    {
+        const float ra[4] = {readlane_f(ba, 0), readlane_f(ba, 16), readlane_f(ba, 32), readlane_f(ba, 48)};
+        const float rv[4] = {readlane_f(bv, 0), readlane_f(bv, 16), readlane_f(bv, 32), readlane_f(bv, 48)};
+        const int ri[4] = {__builtin_amdgcn_readlane(bi, 0), __builtin_amdgcn_readlane(bi, 16),
+                           __builtin_amdgcn_readlane(bi, 32), __builtin_amdgcn_readlane(bi, 48)};
+        ba = ra[0];
+        bv = rv[0];
+        bi = ri[0];
+#pragma unroll
+        for (int k = 1; k < 4; ++k) take(ra[k], rv[k], ri[k]);
     }
     if (lane == 0) {
         sh.a[w] = ba;
@@ -88,9 +98,7 @@ __device__ __forceinline__ void q8_quantize_value(float v, bool active, int b, Q
         iscale = -127.0f / fv;
         q = min(127, (int)rintf(iscale * v));
     }
-    int s16 = q;
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) s16 += __shfl_xor(s16, off, 64);
+    const int s16 = group_isum(q, 16);
     if (active) {
         o.qK[i] = (int8_t)q;
         if (t == 0) o.dK[b] = fa != 0.0f ? 1.0f / iscale : 0.0f;
