@@ -482,13 +482,17 @@ constexpr int TL_QN = 4, TL_DN = 2, TL_SN = 4;  // activation loads a thread hol
 // their arithmetic rather than their loads, load them (measured 1.5% faster at T = 4). Q6_K's 16-value group is
 // one chunk, Q4_K's 32-value group a chunk and its even / odd neighbour, which thread tid ^ 1 holds; loaded,
 // Q4_K's 32-value sums are the two 16-value sums added when written.
-template <int TYPE, int NT, int THR>
+template <int TYPE, int NT, int THR, bool SMALL = false>
 struct Stager {
+    // SMALL (the host's choice when every value chunk and scale has a thread of its own): one load of each a
+    // thread, where the general form issues TL_QN and TL_DN clamped loads whatever K needs (config 2's pair launch:
+    // 1024 value requests for 160 chunks)
+    static constexpr int QN = SMALL ? 1 : TL_QN, DN = SMALL ? 1 : TL_DN;
     static constexpr bool PAIR = Tu<TYPE>::SUMS == 32;
     static constexpr bool FORM = Tu<TYPE>::SUMS != 0 && NT == 1;  // sums formed here (else loaded, if any)
     static constexpr bool LOAD = Tu<TYPE>::SUMS != 0 && !FORM;
-    int4 qv[TL_QN];
-    float dv[TL_DN];
+    int4 qv[QN];
+    float dv[DN];
     int2 sv[TL_SN];
     int nq, ndt, nst;
 
@@ -501,12 +505,12 @@ struct Stager {
         // (unconditional loads, clamped to the last element: with a load skipped on some path the compiler
         // can no longer count the loads in flight and waits for all of them, the weights included)
 #pragma unroll
-        for (int i = 0; i < TL_QN; ++i) {
+        for (int i = 0; i < QN; ++i) {
             const int c = tid + i * THR;
             qv[i] = *(const int4 *)(q + 16 * (long long)(c < nq ? c : nq - 1));
         }
 #pragma unroll
-        for (int i = 0; i < TL_DN; ++i) {
+        for (int i = 0; i < DN; ++i) {
             const int e = tid + i * THR;
             dv[i] = d[e < ndt ? e : ndt - 1];
         }
@@ -547,10 +551,10 @@ struct Stager {
         const int tid = threadIdx.x;
         float *ld = (float *)(smem + L.off_d);
 #pragma unroll
-        for (int i = 0; i < TL_QN; ++i)
+        for (int i = 0; i < QN; ++i)
             if (i * THR < nq) put(L, smem, K, tid + i * THR, qv[i]);  // (uniform)
 #pragma unroll
-        for (int i = 0; i < TL_DN; ++i) {
+        for (int i = 0; i < DN; ++i) {
             const int e = tid + i * THR;
             if (e < ndt) ld[e] = dv[i];
         }
@@ -562,8 +566,8 @@ struct Stager {
             }
         }
         // the rest (a thread and its tid ^ 1 partner leave the first loop together)
-        for (int c = tid + TL_QN * THR; c < nq; c += THR) put(L, smem, K, c, *(const int4 *)(q + 16 * (long long)c));
-        for (int e = tid + TL_DN * THR; e < ndt; e += THR) ld[e] = d[e];
+        for (int c = tid + QN * THR; c < nq; c += THR) put(L, smem, K, c, *(const int4 *)(q + 16 * (long long)c));
+        for (int e = tid + DN * THR; e < ndt; e += THR) ld[e] = d[e];
         if constexpr (LOAD)
             for (int e = tid + TL_SN * THR; e < nst; e += THR) put_s(L, smem, e, load_s(bs, e));
         if constexpr (Tu<TYPE>::LUT)
@@ -622,7 +626,7 @@ struct SwStager {
 // cap_ts further on; r counted as row0 is). NP < NT (tokens whose activation does not fit the tile's LDS at once):
 // the activation is staged NP tokens at a time into the same LDS while each lane keeps its unit's weights in
 // registers, so the weights are still read once; every token's arithmetic is the single-token one.
-template <int TYPE, int NT, int THR, class Rows, bool SW = false, bool CAP = false, int NP = NT>
+template <int TYPE, int NT, int THR, class Rows, bool SW = false, bool CAP = false, int NP = NT, bool SMALL = false>
 __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int row0, int nr, int K, int nb, int lg,
                                           const int8_t *q, const float *d, const int32_t *bs,
                                           const float *sg = nullptr, const float *su = nullptr,
@@ -633,7 +637,7 @@ __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int r
     static_assert(NT % NP == 0 && (!SW || NP == NT), "staging passes of NP tokens");
     const TL L(K, NP, THR);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    Stager<TYPE, NP, THR> st;
+    Stager<TYPE, NP, THR, SMALL> st;
     SwStager<TYPE, THR> sws;
     if constexpr (SW) sws.issue(sg, su, K);
     else st.issue(L, q, d, bs, K);
@@ -749,7 +753,7 @@ static TileArgs tile_args(int nb, int thr) {
     return ta;
 }
 
-template <int TYPE, int NT, int THR, bool CAP = false, int NP = NT>
+template <int TYPE, int NT, int THR, bool CAP = false, int NP = NT, bool SMALL = false>
 __global__ void __launch_bounds__(THR) k_mv_tile(MvArgs a, TileArgs ta) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const DenseRows rows{a};
@@ -759,7 +763,7 @@ __global__ void __launch_bounds__(THR) k_mv_tile(MvArgs a, TileArgs ta) {
     const int row0 = rows.base(m) + (bx - first) * ta.R;
     const int end = DenseRows::pick(m, a.bound[0], a.bound[1], a.bound[2], a.bound[3]);
     const int nr = end - row0 < ta.R ? end - row0 : ta.R;
-    tile_body<TYPE, NT, THR, DenseRows, false, CAP, NP>(smem, rows, row0, nr, a.K, ta.nb, ta.lg, a.q, a.d, a.bs,
+    tile_body<TYPE, NT, THR, DenseRows, false, CAP, NP, SMALL>(smem, rows, row0, nr, a.K, ta.nb, ta.lg, a.q, a.d, a.bs,
                                                         nullptr, nullptr, a.cap,
                                                         (long long)a.Nt * (a.K / cap_group(TYPE)));
 }
@@ -910,6 +914,16 @@ static bool tile_trims(const TileArgs &ta) { return ta.R >= 1 && (ta.R << ta.lg)
 template <int TYPE, int NT, int THR, int NP>
 static hipError_t tile_dense_launch(const MvArgs &a, const TileArgs &ta, int tiles, hipStream_t stream) {
     const size_t lds = (size_t)TileLds<TYPE>(a.K, NP, THR).bytes;
+    if constexpr (NT == 1) {
+        if (a.K / 16 <= THR && a.K / Tu<TYPE>::ACT <= THR) {  // a thread for every value chunk and scale
+            if (a.cap)
+                hipLaunchKernelGGL((k_mv_tile<TYPE, 1, THR, true, 1, true>), dim3((unsigned)tiles), dim3(THR), lds,
+                                   stream, a, ta);
+            else hipLaunchKernelGGL((k_mv_tile<TYPE, 1, THR, false, 1, true>), dim3((unsigned)tiles), dim3(THR), lds,
+                                    stream, a, ta);
+            return hipGetLastError();
+        }
+    }
     if (a.cap)
         hipLaunchKernelGGL((k_mv_tile<TYPE, NT, THR, true, NP>), dim3((unsigned)tiles), dim3(THR), lds, stream, a, ta);
     else hipLaunchKernelGGL((k_mv_tile<TYPE, NT, THR, false, NP>), dim3((unsigned)tiles), dim3(THR), lds, stream, a, ta);
