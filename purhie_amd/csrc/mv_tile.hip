@@ -626,20 +626,25 @@ struct SwStager {
 // cap_ts further on; r counted as row0 is). NP < NT (tokens whose activation does not fit the tile's LDS at once):
 // the activation is staged NP tokens at a time into the same LDS while each lane keeps its unit's weights in
 // registers, so the weights are still read once; every token's arithmetic is the single-token one.
-template <int TYPE, int NT, int THR, class Rows, bool SW = false, bool CAP = false, int NP = NT, bool SMALL = false>
+// PRE: the caller has issued the stager's loads (*pre) already (the routed expert launch, before routing).
+template <int TYPE, int NT, int THR, class Rows, bool SW = false, bool CAP = false, int NP = NT, bool SMALL = false,
+          bool PRE = false>
 __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int row0, int nr, int K, int nb, int lg,
                                           const int8_t *q, const float *d, const int32_t *bs,
                                           const float *sg = nullptr, const float *su = nullptr,
-                                          int32_t *cap = nullptr, long long cap_ts = 0) {
+                                          int32_t *cap = nullptr, long long cap_ts = 0,
+                                          const Stager<TYPE, NP, THR, SMALL> *pre = nullptr) {
     using P = Tu<TYPE>;
     using TL = TileLds<TYPE>;
     static_assert(!SW || (NT == 1 && P::ACT == 32 && P::SUMS == 0), "SwiGLU staging: one token, Q8_0 activation");
     static_assert(NT % NP == 0 && (!SW || NP == NT), "staging passes of NP tokens");
+    static_assert(!PRE || !SW, "a pre-issued stager stages q / d / bs");
     const TL L(K, NP, THR);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     Stager<TYPE, NP, THR, SMALL> st;
     SwStager<TYPE, THR> sws;
-    if constexpr (SW) sws.issue(sg, su, K);
+    if constexpr (PRE) st = *pre;
+    else if constexpr (SW) sws.issue(sg, su, K);
     else st.issue(L, q, d, bs, K);
 
     // this wave's units [64 wave, 64 wave + wu) of the tile: bytes [g, g + wu BYTES), loaded as the 16-byte
@@ -770,15 +775,24 @@ __global__ void __launch_bounds__(THR) k_mv_tile(MvArgs a, TileArgs ta) {
 
 // MoE: grid (tiles, n_used * nmat, T); slot j of token t uses expert ids[t * n_used + j] (-1: Wx). Tiles mode:
 // grid (tiles, tile, max_tiles) over moe_group's expert tiles, one entry per block.
-template <int TYPE, int THR, bool SW = false, bool CAP = false, bool ROUTE = false>
+// SMALL: the stager's one-load form (a thread for every value chunk and scale). ROUTE: the activation's loads are
+// issued before the routing (its rows do not depend on the experts), so their latency runs beside it.
+template <int TYPE, int THR, bool SW = false, bool CAP = false, bool ROUTE = false, bool SMALL = false>
 __global__ void __launch_bounds__(THR) k_mv_tile_id(MvIdArgs a, TileArgs ta) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     IdEntry en;
+    Stager<TYPE, 1, THR, SMALL> pre;
     if constexpr (ROUTE) {  // the token's experts from its logits (every workgroup; the first one stores them)
         static_assert(THR == 256, "the router's reductions take 256 threads");
+        static_assert(!SW, "the routed launch is the gate / up pair");
         __shared__ RouterLds<1> rs;
         const int t = blockIdx.z, slot = (int)blockIdx.y % a.n_used;
         const bool first = blockIdx.x == 0 && blockIdx.y == 0;
+        {
+            const long long ir = a.x_per_slot ? (long long)t * a.n_used + slot : t;
+            pre.issue(TileLds<TYPE>(a.K, 1, THR), a.q + ir * a.K, a.d + ir * (a.K / Tu<TYPE>::ACT),
+                      a.bs ? a.bs + ir * (a.K / 16) : nullptr, a.K);
+        }
         route_token(a.route_logits + (long long)t * a.route_ne, nullptr, nullptr,
                     first ? a.route_ids + (long long)t * a.n_used : nullptr,
                     first ? a.route_wts + (long long)t * a.n_used : nullptr, nullptr, a.route_ne, a.n_used, 0, a.n_used,
@@ -803,9 +817,9 @@ __global__ void __launch_bounds__(THR) k_mv_tile_id(MvIdArgs a, TileArgs ta) {
         tile_body<TYPE, 1, THR, IdRows, true, CAP>(smem, rows, row0, nr, K, ta.nb, ta.lg, nullptr, nullptr, nullptr,
                                                    a.sw_g + in_row * K, a.sw_u + in_row * K, cap, 0);
     else
-        tile_body<TYPE, 1, THR, IdRows, false, CAP>(smem, rows, row0, nr, K, ta.nb, ta.lg, a.q + in_row * K,
-                                                    a.d + in_row * (K / Tu<TYPE>::ACT),
-                                                    a.bs ? a.bs + in_row * (K / 16) : nullptr, nullptr, nullptr, cap, 0);
+        tile_body<TYPE, 1, THR, IdRows, false, CAP, 1, SMALL, ROUTE>(
+            smem, rows, row0, nr, K, ta.nb, ta.lg, a.q + in_row * K, a.d + in_row * (K / Tu<TYPE>::ACT),
+            a.bs ? a.bs + in_row * (K / 16) : nullptr, nullptr, nullptr, cap, 0, &pre);
 }
 
 // ---------------------------------------------------------------- host side
@@ -1037,13 +1051,24 @@ static hipError_t tile_id_launch(const MvIdArgs &a, const TileArgs &ta, hipStrea
     } else if (a.sw_g) {
         return hipErrorInvalidDeviceFunction;
     }
+    const bool small = a.K / 16 <= THR && a.K / Tu<TYPE>::ACT <= THR;  // a thread for every value chunk and scale
     if (a.route_logits) {
         if constexpr (THR == 256) {
             if (a.cap || a.n_tiles) return hipErrorNotSupported;
-            hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, false, false, true>), grid, dim3(THR), lds, stream, a, ta);
+            if (small)
+                hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, false, false, true, true>), grid, dim3(THR), lds, stream, a,
+                                   ta);
+            else hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, false, false, true>), grid, dim3(THR), lds, stream, a, ta);
             return hipGetLastError();
         }
         return hipErrorNotSupported;
+    }
+    if (small) {
+        if (a.cap)
+            hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, false, true, false, true>), grid, dim3(THR), lds, stream, a, ta);
+        else hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, false, false, false, true>), grid, dim3(THR), lds, stream, a,
+                                ta);
+        return hipGetLastError();
     }
     if (a.cap) hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, false, true>), grid, dim3(THR), lds, stream, a, ta);
     else hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR>), grid, dim3(THR), lds, stream, a, ta);
