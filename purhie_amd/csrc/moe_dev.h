@@ -55,7 +55,7 @@ __device__ __forceinline__ unsigned long long route_key(float p, int e) {
 // bits). Each wave keeps its own copy of the keys in LDS (in order within the wave: no barrier) and counts, for
 // both its experts, the keys ahead of them among experts [32 w, 32 w + 32); the four counts meet behind one
 // barrier. Two barriers in all where the general form takes seven, and wave reductions by DPP: the expert pair
-// launch with the routing inside (config 4's decode token) 10.2 -> 9.2 us, the router kernel 4.1 -> 3.0 us. Results
+// launch with the routing inside (config 4's decode token) 10.2 -> 8.8 us, the router kernel 4.1 -> 2.5 us. Results
 // as route_token's.
 template <int PER>
 __device__ __forceinline__ void route_token_128(const float *__restrict__ l, const float *__restrict__ x,
@@ -75,22 +75,18 @@ __device__ __forceinline__ void route_token_128(const float *__restrict__ l, con
     const float inv = 1.0f / sum;
     const float p0 = e0 * inv, p1 = e1 * inv;
     const unsigned long long k0 = route_key(p0, lane), k1 = route_key(p1, lane + 64);
+    // (a missing expert's key is 0, below every real key, so it never counts ahead: the 32 comparisons of a wave
+    // need no bound and unroll, their 16 LDS reads in flight together)
     unsigned long long *wk = s.wkey[wave];
-    wk[lane] = k0;
-    wk[lane + 64] = k1;
+    wk[lane] = h0 ? k0 : 0ull;
+    wk[lane + 64] = h1 ? k1 : 0ull;
     __builtin_amdgcn_wave_barrier();
     int r0 = 0, r1 = 0;
-    const int j0 = 32 * wave, j1 = j0 + 32 < n_expert ? j0 + 32 : n_expert;
-    int j = j0;
-    for (; j + 2 <= j1; j += 2) {  // (uniform)
-        const ulonglong2 u = *(const ulonglong2 *)(wk + j);
+#pragma unroll
+    for (int j = 0; j < 32; j += 2) {
+        const ulonglong2 u = *(const ulonglong2 *)(wk + 32 * wave + j);
         r0 += (u.x > k0) + (u.y > k0);
         r1 += (u.x > k1) + (u.y > k1);
-    }
-    if (j < j1) {
-        const unsigned long long u = wk[j];
-        r0 += u > k0;
-        r1 += u > k1;
     }
     s.part[wave][lane] = r0;
     s.part[wave][lane + 64] = r1;
