@@ -105,10 +105,19 @@ __device__ __forceinline__ void route_token_128(const float *__restrict__ l, con
         if (tid == 0) *sg = 1.0f / (1.0f + expf(-dsum));
     }
     __syncthreads();
-    float ws = 0.0f;  // the sum in slot order, as the reference's loop (every thread the same)
-    for (int r = 0; r < n_used; ++r) ws += s.selw[r];
-    ws = fmaxf(ws, 6.103515625e-5f);
-    if (wts && tid < n_used) wts[tid] = s.selw[tid] / ws;
+    if (wts) {  // (uniform) the sum in slot order, as the reference's loop (every thread the same), 8 reads at once
+        float ws = 0.0f;
+        for (int r0 = 0; r0 < n_used; r0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = s.selw[r0 + i < n_used ? r0 + i : 0];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (r0 + i < n_used) ws += v[i];
+        }
+        ws = fmaxf(ws, 6.103515625e-5f);
+        if (tid < n_used) wts[tid] = s.selw[tid] / ws;
+    }
 }
 
 // One token's routing by a 256-thread workgroup (every thread calls it; it has barriers): softmax of the n_expert
