@@ -173,8 +173,12 @@ hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qm
     else
         PQ_TRY(qmatvec_launch_batch_h(w->type_router, w->router, w->rb_router, xn, L.xh, L.xh ? (size_t)T * E * 2 : 0,
                                       L.logits, NE, E, T, stream));
-    PQ_TRY(gpu_moe_router(L.logits, xn, sh ? w->shexp_gate : nullptr, L.ids, L.wts, sh && w->shexp_gate ? L.sg : nullptr,
-                          NE, NU, E, T, stream, L.ns));
+    // a few tokens without a shared expert: the routing runs inside the expert gate / up launch
+    // (qmatvec_launch_q8_id_pair_routed: gpu_moe_router's ids and weights bit for bit, one launch fewer)
+    const bool routed = !L.grouped && !L.slot && !sh;
+    if (!routed)
+        PQ_TRY(gpu_moe_router(L.logits, xn, sh ? w->shexp_gate : nullptr, L.ids, L.wts,
+                              sh && w->shexp_gate ? L.sg : nullptr, NE, NU, E, T, stream, L.ns));
     const float *sg = sh && w->shexp_gate ? L.sg : nullptr;
 
     // the expert down matvec reads SwiGLU(g, u) quantized in its own kernel where the type allows (the same bits
@@ -215,6 +219,9 @@ hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qm
                                                    L.g, L.u, FE, E, L.max_tiles, L.tile, L.ntiles, L.te, L.ts, L.tn,
                                                    L.tok, L.pair, stream));
         }
+    } else if (routed) {
+        PQ_TRY(qmatvec_launch_q8_id_pair_routed(w->type_gate_up, w->gate_exps, w->up_exps, w->rb_gate_up, L.logits, NE,
+                                                L.ids, L.wts, NU, q8_xn, L.g, L.u, FE, E, T, stream));
     } else {
         PQ_TRY(qmatvec_launch_q8_id_pair(w->type_gate_up, w->gate_exps, w->up_exps, w->rb_gate_up, L.ids, NU, 0, q8_xn,
                                          L.g, L.u, FE, E, T, stream));
