@@ -542,8 +542,16 @@ struct Stager {
             if (active && (!PAIR || (c & 1) == 0)) ((int32_t *)(smem + L.off_s))[PAIR ? c >> 1 : c] = s;
         }
         if (active) {
-            const int per = K / 16, t = c / per, cc = c - t * per;
-            *(int4 *)(smem + t * L.xt + (cc >> 4) * TL_PAD + (cc & 15) * 16) = v;
+            // chunk c is chunk cc = c - t K / 16 of token t. One token, or K a multiple of 256: the tokens' padded
+            // blocks are contiguous (t xt = t (K / 256) TL_PAD), so the place follows from c alone, with no division
+            int off;
+            if (NT == 1 || K % 256 == 0) {
+                off = (c >> 4) * TL_PAD + (c & 15) * 16;
+            } else {
+                const int per = K / 16, t = c / per, cc = c - t * per;
+                off = t * L.xt + (cc >> 4) * TL_PAD + (cc & 15) * 16;
+            }
+            *(int4 *)(smem + off) = v;
         }
     }
     __device__ __forceinline__ void commit(const TileLds<TYPE> &L, uint8_t *smem, const int8_t *q, const float *d,
