@@ -203,6 +203,16 @@ struct DenseRows {
         const long long ys = pick(m, a.ystride[0], a.ystride[1], a.ystride[2], a.ystride[3]);
         y[(long long)t * ys + (row - base(m))] = v * pick(m, a.osc[0], a.osc[1], a.osc[2], a.osc[3]);
     }
+    // the row's value for each of NT tokens (its matrix, output and scale picked once)
+    template <int NT>
+    __device__ void store_all(int row, const float (&v)[NT]) const {
+        const int m = mat(row);
+        float *y = pick(m, a.y[0], a.y[1], a.y[2], a.y[3]) + (row - base(m));
+        const long long ys = pick(m, a.ystride[0], a.ystride[1], a.ystride[2], a.ystride[3]);
+        const float sc = pick(m, a.osc[0], a.osc[1], a.osc[2], a.osc[3]);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) y[t * ys] = v[t] * sc;
+    }
 };
 
 // Capture of the integer dots (the test hook of capture mode): put(t, g, v) adds the dot v of scale group g (of
@@ -226,6 +236,11 @@ struct IdRows {
     float sc;
     __device__ const uint8_t *w(int row) const { return W + (long long)row * rb; }
     __device__ void store(int row, int, float v) const { y[row] = v * sc; }
+    template <int NT>
+    __device__ void store_all(int row, const float (&v)[NT]) const {
+        static_assert(NT == 1, "one token a slot");
+        y[row] = v[0] * sc;
+    }
 };
 
 // The entry a block of an expert-indexed launch computes. ids mode: grid.y = slot + n_used * matrix, grid.z =

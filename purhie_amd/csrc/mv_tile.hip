@@ -732,18 +732,21 @@ __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int r
     __syncthreads();
     // row r's sum: G = 2^lg threads per row each add every G-th partial, then a butterfly over the G
     // (a fixed order, set by K alone)
+    // (every token in one pass over the partials, each token's sum in the same order)
     const int G = 1 << lg, r = tid >> lg, i = tid & (G - 1);
     const int rr = r < nr ? r : 0;
+    float sum[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        float s = 0.0f;
-        for (int kk = i; kk < nb; kk += G) {
-            const int uu = rr * nb + kk;
-            s += ((const float *)(smem + L.off_w + (uu >> 6) * TL::REGION))[t * 64 + (uu & 63)];
-        }
-        s = group_sum(s, G);
-        if (i == 0 && r < nr) rows.store(row0 + r, t, s);
+    for (int t = 0; t < NT; ++t) sum[t] = 0.0f;
+    for (int kk = i; kk < nb; kk += G) {
+        const int uu = rr * nb + kk;
+        const float *pp = (const float *)(smem + L.off_w + (uu >> 6) * TL::REGION) + (uu & 63);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) sum[t] += pp[t * 64];
     }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) sum[t] = group_sum(sum[t], G);
+    if (i == 0 && r < nr) rows.template store_all<NT>(row0 + r, sum);
 }
 
 // ---------------------------------------------------------------- kernels
