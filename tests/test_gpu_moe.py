@@ -28,7 +28,8 @@ def host(t):
     return t.cpu().numpy()
 
 
-@pytest.mark.parametrize("T,E,n_used", [(1, 128, 8), (512, 128, 8), (7, 256, 8), (3, 1024, 64), (5, 16, 4)])
+@pytest.mark.parametrize("T,E,n_used", [(1, 128, 8), (512, 128, 8), (7, 256, 8), (3, 1024, 64), (5, 16, 4),
+                                        (4, 64, 8), (6, 65, 8), (3, 100, 6), (4, 127, 16), (3, 129, 8)])
 def test_router(M, oracle, T, E, n_used):
     import torch
     logits = synth.gaussian(900 + T + E, T * E).reshape(T, E)
@@ -191,7 +192,7 @@ def test_add_rmsnorm_bad_arguments(M):
 @pytest.mark.parametrize("kpath", ["tile", "wave"])
 @pytest.mark.parametrize("t,T,E,n_used,N,K", [(100, 1, 128, 8, 768, 2048), (12, 1, 128, 8, 768, 2048),
                                               (100, 3, 256, 8, 512, 1024), (40, 2, 64, 4, 256, 1024),
-                                              (100, 1, 300, 8, 256, 1024)])
+                                              (100, 1, 300, 8, 256, 1024), (100, 2, 100, 6, 256, 1024)])
 def test_routed_pair_same_bits(M, oracle, kpath, t, T, E, n_used, N, K):
     """qmatvec_launch_q8_id_pair_routed (routing inside the gate / up pair launch) gives gpu_moe_router's ids and
     weights and qmatvec_launch_q8_id_pair's outputs bit for bit: on the tile kernel (n_expert <= 256) and through
