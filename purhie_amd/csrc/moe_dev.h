@@ -107,13 +107,13 @@ __device__ __forceinline__ void route_token_128(const float *__restrict__ l, con
     __syncthreads();
     if (wts) {  // (uniform) the sum in slot order, as the reference's loop (every thread the same), 8 reads at once
         float ws = 0.0f;
-        for (int r0 = 0; r0 < n_used; r0 += 8) {
+        for (int b = 0; b < n_used; b += 8) {
             float v[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = s.selw[r0 + i < n_used ? r0 + i : 0];
+            for (int i = 0; i < 8; ++i) v[i] = s.selw[b + i < n_used ? b + i : 0];
 #pragma unroll
             for (int i = 0; i < 8; ++i)
-                if (r0 + i < n_used) ws += v[i];
+                if (b + i < n_used) ws += v[i];
         }
         ws = fmaxf(ws, 6.103515625e-5f);
         if (tid < n_used) wts[tid] = s.selw[tid] / ws;
