@@ -201,6 +201,49 @@ def test_slot_form_same_bits_as_plain_sequence(M, Q, oracle, t_gu, t_d, E, FE):
     assert np.array_equal(got.view(np.uint32), host(out).view(np.uint32))
 
 
+@pytest.mark.parametrize("T,t_gu,t_d,E,FE,NE,NU", [
+    (1, 100, 100, 512, 256, 16, 4),
+    (3, 101, 8, 512, 256, 16, 4),
+    (7, 100, 100, 1024, 768, 32, 8),   # 13 row tiles of 85 in the down launch
+    (1, 100, 100, 2048, 768, 12, 8),   # config 4's widths (hidden 2048, FFN 768, top-8)
+    (2, 12, 14, 512, 512, 16, 4),      # a Q8_K down matvec: SwiGLU in its own launch
+])
+def test_routed_form_same_bits_as_plain_sequence(M, Q, oracle, T, t_gu, t_d, E, FE, NE, NU):
+    """a few tokens, no shared expert: the routing inside the gate / up launch and, for a Q8_0-activation down
+    type, SwiGLU inside the down launch give the plain sequence's bits (router, gate / up pair, SwiGLU with its
+    quantization, down, combine). Two calls on one workspace: the second starts from what the first left."""
+    import torch
+    lay = Layer(M, Q, oracle, 600 + T, E=E, FE=FE, NE=NE, NU=NU, t_gu=t_gu, t_d=t_d, shexp=False)
+    x = acts(70 + T, T, E)
+    q = Q.Q8(((T * E + 255) // 256) * 256)
+    xd = dev(x)
+    Q.quantize(xd.reshape(-1), T * E, q)
+    ws = torch.empty(M.workspace_bytes(lay.w, T), dtype=torch.uint8, device="cuda")
+    outs = []
+    for _ in range(2):
+        out = torch.full((T, E), float("nan"), dtype=torch.float32, device="cuda")
+        M.ffn(lay.w, xd, q, T, out, ws)
+        outs.append(host(out))
+    L, ML = Q.lib(), M.lib()
+    logits = dev(lay.logits(Q, x))
+    ids = torch.zeros((T, NU), dtype=torch.int32, device="cuda")
+    wts = torch.zeros((T, NU), dtype=torch.float32, device="cuda")
+    assert ML.gpu_moe_router(p(logits), None, None, p(ids), p(wts), None, NE, NU, E, T, None, 0) == 0
+    g = torch.zeros((T * NU, FE), device="cuda")
+    u = torch.zeros((T * NU, FE), device="cuda")
+    Q.launch_q8_id_x(t_gu, lay.keep[0], lay.keep[1], None, None, ids, NU, 0, q, g, u, FE, E, T)
+    act = torch.zeros(T * NU * FE, device="cuda")
+    qx = Q.Q8(((T * NU * FE + 255) // 256) * 256)
+    assert ML.gpu_swiglu(p(g), p(u), p(act), T * NU * FE, qx.ref, None) == 0
+    dn = torch.zeros((T * NU, E), device="cuda")
+    Q.launch_q8_id_x(t_d, lay.keep[2], None, None, None, ids, NU, 1, qx, dn, None, E, FE, T)
+    want = torch.zeros((T, E), device="cuda")
+    assert ML.gpu_moe_combine(p(dn), p(wts), None, None, p(want), NU, E, T, None) == 0
+    want = host(want)
+    for got in outs:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("case", [
     dict(T=1),                                                     # slot form
     dict(T=5),                                                     # per-token matvecs
