@@ -37,16 +37,48 @@ def gaussian(seed, n, mean=0.0, sigma=1.0):
     return (mean + sigma * z[:n]).astype(np.float32)
 
 
+def outlier_positions(seed, size, frac=0.001):
+    """round(frac * size) seeded distinct positions in [0, size), ascending"""
+    k = int(round(frac * size))
+    u = uniform(seed, 4 * k + 16)
+    return np.unique((u * size).astype(np.int64).clip(0, size - 1))[:k]
+
+
 def with_outliers(x, seed, frac=0.001, factor=20.0):
     """x with round(frac * size) entries at seeded distinct positions multiplied by factor"""
     x = np.array(x, dtype=np.float32, copy=True)
     flat = x.reshape(-1)
-    k = int(round(frac * flat.size))
-    u = uniform(seed, 4 * k + 16)
-    pos = np.unique((u * flat.size).astype(np.int64).clip(0, flat.size - 1))[:k]
-    flat[pos] *= np.float32(factor)
+    flat[outlier_positions(seed, flat.size, frac)] *= np.float32(factor)
     return x
 
 
 def seeds(cfg):
     return dict(w=0x5EED0000 + cfg, x=0x5EED1000 + cfg, router=0x5EED2000 + cfg, outlier=0x5EED3000 + cfg)
+
+
+def _i64(v):
+    """a uint64 constant as the int64 of the same bits"""
+    v = int(v)
+    return v - (1 << 64) if v >= (1 << 63) else v
+
+
+def gaussian_torch(torch, seed, n, mean=0.0, sigma=1.0, start=0, device="cuda"):
+    """values start .. start + n - 1 (start even) of gaussian(seed, ...), made by torch on `device` (the benchmark's
+    weights and activations, without a host round trip): the same splitmix64 outputs and uniforms bit for bit
+    (int64 products wrap as the uint64 ones do; right shifts are masked to logical shifts), Box-Muller in float64
+    with the device's log / sqrt / cos / sin, then float32. The float32 values equal gaussian()'s unless a device
+    libm result differs from the host's by an ulp right at a float32 rounding boundary (a few in a billion)."""
+    assert start % 2 == 0, "Box-Muller pairs start at even positions"
+    m = (n + 1) // 2
+    z = torch.arange(start + 1, start + 2 * m + 1, dtype=torch.int64, device=device) * _i64(_GOLDEN) + _i64(seed)
+    z = (z ^ ((z >> 30) & ((1 << 34) - 1))) * _i64(_M1)
+    z = (z ^ ((z >> 27) & ((1 << 37) - 1))) * _i64(_M2)
+    z = z ^ ((z >> 31) & ((1 << 33) - 1))
+    u = (((z >> 11) & ((1 << 53) - 1)).to(torch.float64) + 1.0) * (1.0 / 9007199254740992.0)
+    del z
+    r = torch.sqrt(-2.0 * torch.log(u[0::2]))
+    th = 2.0 * np.pi * u[1::2]
+    out = torch.empty(2 * m, dtype=torch.float64, device=device)
+    out[0::2] = r * torch.cos(th)
+    out[1::2] = r * torch.sin(th)
+    return (mean + sigma * out[:n]).to(torch.float32)

@@ -55,9 +55,7 @@ def host(t):
 def encoded(Q, t, N, K, seed, sd=0.02):
     """N x K ~N(0, sd) weights encoded as type t on the GPU: (device bytes, host bytes)"""
     import torch
-    g = torch.Generator(device="cuda")
-    g.manual_seed(seed)
-    src = torch.randn((N, K), generator=g, device="cuda", dtype=torch.float32) * sd
+    src = synth.gaussian_torch(torch, seed, N * K, 0.0, sd).reshape(N, K)  # synth.gaussian(seed, N K, 0, sd)
     out = torch.empty((N, Q.row_size(t, K)), dtype=torch.uint8, device="cuda")
     step = max(1, (64 << 20) // (4 * K))
     for r0 in range(0, N, step):

@@ -34,16 +34,15 @@ def p(t):
 
 
 def encoded(Q, t, N, K, seed):
-    """N x K ~N(0, 0.02) weights from a seeded device generator, encoded on the device (bit-identical to the
-    oracle's encoder, tests/test_gpu_encode.py)"""
+    """N x K ~N(0, 0.02) weights, synth.gaussian(seed, N K, 0, 0.02) made on the device, encoded on the device
+    (bit-identical to the oracle's encoder, tests/test_gpu_encode.py)"""
     import torch
-    g = torch.Generator(device="cuda")
-    g.manual_seed(seed)
     out = torch.empty((N, Q.row_size(t, K)), dtype=torch.uint8, device="cuda")
     step = max(1, (64 << 20) // K)
     for r0 in range(0, N, step):
         n = min(step, N - r0)
-        Q.encode_device(t, torch.randn((n, K), generator=g, device="cuda") * 0.02, out[r0:r0 + n], n, K)
+        w = synth.gaussian_torch(torch, seed, n * K, 0.0, 0.02, start=r0 * K).reshape(n, K)
+        Q.encode_device(t, w, out[r0:r0 + n], n, K)
     return out
 
 

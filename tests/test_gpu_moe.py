@@ -202,12 +202,11 @@ def test_routed_pair_same_bits(M, oracle, kpath, t, T, E, n_used, N, K):
     from purhie_amd import qmatvec as Q
     prev = Q.decode_path(1 if kpath == "tile" else 0)
     try:
-        g = torch.Generator(device="cuda")
-        g.manual_seed(E * 31 + K)
         W = torch.empty((E * N, Q.row_size(t, K)), dtype=torch.uint8, device="cuda")
         W2 = torch.empty_like(W)
-        for w in (W, W2):
-            Q.encode_device(t, torch.randn((E * N, K), generator=g, device="cuda") * 0.02, w, E * N, K)
+        for i, w in enumerate((W, W2)):
+            src = synth.gaussian_torch(torch, E * 31 + K + i, E * N * K, 0.0, 0.02).reshape(E * N, K)
+            Q.encode_device(t, src, w, E * N, K)
         logits = synth.gaussian(950 + E, T * E).reshape(T, E)
         if T >= 2:
             logits[1, 3] = logits[1, 7] = logits[1].max() + 0.5  # equal leaders

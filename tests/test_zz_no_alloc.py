@@ -35,9 +35,7 @@ def dev(a):
 
 def encoded(Q, t, N, K, seed):
     import torch
-    g = torch.Generator(device="cuda")
-    g.manual_seed(seed)
-    src = torch.randn((N, K), generator=g, device="cuda", dtype=torch.float32) * 0.02
+    src = synth.gaussian_torch(torch, seed, N * K, 0.0, 0.02).reshape(N, K)
     out = torch.empty((N, Q.row_size(t, K)), dtype=torch.uint8, device="cuda")
     Q.encode_device(t, src, out, N, K)
     return out
