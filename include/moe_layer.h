@@ -75,6 +75,21 @@ hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qm
 hipError_t purhie_moe_ffn_noalloc(const purhie_moe_weights *w, const float *xn, const qmatvec_q8 *q8_xn, int T,
                                   float *out, hipStream_t stream);
 
+/* No counterpart in the reference: a test hook for the layer's stage-by-stage parity tests. Where purhie_moe_ffn(w,
+ * T) puts its intermediate results in the caller's workspace, as byte offsets from ws (-1: not in this form):
+ * the routed ids [T][ns] (ns = n_expert_used, or + 1 with the shared expert as slot n_expert_used), their weights
+ * [T][n_expert_used] and the shared expert's gate [T]; the experts' gate and up outputs [T * ns][n_ff_exp] (written
+ * where gu_written is 1; the grouped ROCmFP4 / FAST / NVFP4 form folds SwiGLU into its gate / up GEMM instead and
+ * writes the quantized activation only); the quantized SwiGLU activation [T * ns][n_ff_exp] (a qmatvec_q8 of qx_k
+ * values, qmatvec_q8_bind layout; written where act_written is 1); the down outputs [T * ns][n_embd] (row t * ns +
+ * slot); the shared expert's output [T][n_embd] and its quantized activation (a qmatvec_q8 of qs_k values) outside
+ * the slot form. Returns 0, or -1 when the layer cannot run (purhie_moe_workspace_bytes answers 0). */
+typedef struct {
+    long long ids, wts, sg, g, u, qx, down, shout, qs;
+    int ns, qx_k, qs_k, slot, grouped, gu_written, act_written;
+} purhie_moe_regions;
+int purhie_moe_debug_regions(const purhie_moe_weights *w, int T, purhie_moe_regions *r);
+
 #ifdef __cplusplus
 }
 #endif

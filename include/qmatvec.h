@@ -261,6 +261,14 @@ hipError_t qmatvec_debug_capture(int32_t *out, size_t n_ints);
 int qmatvec_debug_capture_unit(int type, int gemm);
 int qmatvec_debug_decode_path(int mode);
 
+/* No counterpart in the reference: a measured alternative, not used by any launch above. The ROCmFP4 prefill GEMM
+ * (dense, prefill semantics of qmatvec_launch_q8_batch: y [T][ldy] = W x for the Q8_0 activation q) on gfx950's
+ * f8f6f4 matrix core, exact: the codebook levels and the activation's two 4-bit planes as E4M3 operands, every
+ * 16-value group's integer dot from its own pair of instructions, and the reference's float epilogue per group.
+ * K % 64 == 0; hipErrorInvalidValue otherwise. The benchmark times it beside the split GEMM. */
+hipError_t qmatvec_debug_gemm_f8f6f4(const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int ldy, int N,
+                                     int K, int T, hipStream_t stream);
+
 /* No counterpart in the reference: a test hook, an independent scalar kernel. The integer dot of every weight
  * scale group (Q8_0 / FAST / MXFP4 / Q4_K / Q5_K / IQ4_XS: 32 values, ROCmFP4 / NVFP4 / Q6_K: 16) of every row
  * against the quantized activation, computed by the same device decoders as the matvec kernels: out[N][K / group].

@@ -35,7 +35,14 @@ constexpr int SP_ROWS = 256;         // weight rows per workgroup, dense prompts
 constexpr int SP_ROWS_SMALL = 128;   // the same for MoE expert tiles and short prompts (twice the workgroups)
 constexpr int SP_T = 128;            // tokens per workgroup, dense
 constexpr int SP_T_SMALL = 64;       // MoE expert tiles (a few dozen entries on average) and prompts of <= 64 tokens
-constexpr int SP_ROW = 40;           // halves per LDS row: 32 values + 16 bytes of padding (conflict-free reads)
+
+// LDS place (bytes) of 16-byte chunk ch (0..3, values 8 ch .. 8 ch + 7) of a stage's row r (32 fp16 values a row):
+// chunk ch of the 16 rows of group r / 16 lie side by side, so a fragment read (lane: row 16 i + lane % 16, chunk
+// lane / 16) touches 1 KiB as one contiguous read does, with no bank conflict; 80-byte padded rows took two LDS
+// passes per fragment read (a probe kernel under rocprofv3, SQ_LDS_BANK_CONFLICT per instruction). The weight
+// stores (a thread a row) are conflict-free too; the token stores of TPR threads a row keep the conflicts the
+// padded rows had.
+__device__ __forceinline__ int sp_at(int r, int ch) { return ((r >> 4) << 10) + (ch << 8) + ((r & 15) << 4); }
 constexpr int SP_GROUP = 4;          // token tiles advancing together over the row tiles (XCD order)
 constexpr int SP_PD = 2;             // prefetch distance (stages), dense 128-token tiles
 constexpr int SP_PD_SMALL = 4;       // the same, dense 64-token tiles
@@ -100,10 +107,11 @@ struct SpW {
         for (int k = 0; k < 5; ++k) r.w[k] = ld32(al + 4 * k);
     }
     // byte i of the codes holds values i (low nibble, scale e0) and i + 16 (high, scale e1). Part p of P decodes
-    // code words 4 p / P .. (word k: values 4k .. 4k + 3 and 16 + 4k .. 16 + 4k + 3) into dst, the block's 32
-    // values in order.
+    // code words 4 p / P .. (word k: values 4k .. 4k + 3 and 16 + 4k .. 16 + 4k + 3) into LDS row `row` of sw, the
+    // block's 32 values in order.
     template <int P>
-    __device__ static void decode(const Raw &r, _Float16 *dst, int p) {
+    __device__ static void decode(const Raw &r, _Float16 *sw, int row, int p) {
+        uint8_t *base = (uint8_t *)sw;
         const uint32_t sc = r.w[4] >> (8 * r.off);  // the scale bytes at block offset 16 (and 17)
         const h2 e0 = h2of(ue4m3_half(sc));
         const h2 e1 = TYPE == TY_FP4 ? h2of(ue4m3_half(sc >> 8)) : e0;
@@ -114,8 +122,8 @@ struct SpW {
 #pragma unroll
             for (int j = 0; j < 2; ++j)
                 fp4_word<TOP>(align_bytes(r.w[k0 + j + 1], r.w[k0 + j], r.off), e0, e1, lo[j], hi[j]);
-            *(uint4 *)(dst + 4 * k0) = make_uint4(lo[0][0], lo[0][1], lo[1][0], lo[1][1]);
-            *(uint4 *)(dst + 16 + 4 * k0) = make_uint4(hi[0][0], hi[0][1], hi[1][0], hi[1][1]);
+            *(uint4 *)(base + sp_at(row, k0 >> 1)) = make_uint4(lo[0][0], lo[0][1], lo[1][0], lo[1][1]);
+            *(uint4 *)(base + sp_at(row, 2 + (k0 >> 1))) = make_uint4(hi[0][0], hi[0][1], hi[1][0], hi[1][1]);
         }
     }
 };
@@ -139,7 +147,8 @@ struct SpW<TY_NVFP4> {
     // sub-block q (code words 2q, 2q + 1; word k: values 4k' .. 4k' + 3 low nibbles, 8 + 4k' .. high, k' = k & 1)
     // with its own scale; part p of P decodes sub-blocks 2 p / P ..
     template <int P>
-    __device__ static void decode(const Raw &r, _Float16 *dst, int p) {
+    __device__ static void decode(const Raw &r, _Float16 *sw, int row, int p) {
+        uint8_t *base = (uint8_t *)sw;
 #pragma unroll
         for (int k = 0; k < 4 / P; k += 2) {
             const int k0 = 4 / P * p + k, q = k0 >> 1;
@@ -147,8 +156,8 @@ struct SpW<TY_NVFP4> {
             uint32_t lo[2][2], hi[2][2];
 #pragma unroll
             for (int j = 0; j < 2; ++j) fp4_word<TOP>(r.v[k0 + j], e, e, lo[j], hi[j]);
-            *(uint4 *)(dst + 16 * q) = make_uint4(lo[0][0], lo[0][1], lo[1][0], lo[1][1]);
-            *(uint4 *)(dst + 16 * q + 8) = make_uint4(hi[0][0], hi[0][1], hi[1][0], hi[1][1]);
+            *(uint4 *)(base + sp_at(row, 2 * q)) = make_uint4(lo[0][0], lo[0][1], lo[1][0], lo[1][1]);
+            *(uint4 *)(base + sp_at(row, 2 * q + 1)) = make_uint4(hi[0][0], hi[0][1], hi[1][0], hi[1][1]);
         }
     }
 };
@@ -276,20 +285,30 @@ __device__ __forceinline__ void swiglu_epilogue(const GemmArgs &a, const f4 (&ac
     }
 }
 
+// capture mode: four ints at cap[i] (dropped past cap_n)
+__device__ __forceinline__ void cap_put4(const GemmArgs &a, long long i, uint4 v) {
+    if (i >= 0 && i + 4 <= a.cap_n) *(uint4 *)(a.cap + i) = v;
+}
+
 // PD: the prefetch distance in stages (2 or 4): stage s's global loads are issued PD stages before its LDS store,
 // into one of PD register sets. SWP (MoE, the gate / up pair): the workgroup's rows are rows n0 .. n0 + ROWS / 2 - 1
 // of W (gate, waves 0 and 1) and the same rows of W2 (up, waves 2 and 3), and the epilogue writes
-// SwiGLU(gate, up) = g / (1 + exp(-g)) u quantized to Q8_0 (hq, hd, hs) instead of the two outputs.
-template <int TYPE, int TT, int ROWS, bool MOE, int PD, bool SWP = false>
+// SwiGLU(gate, up) = g / (1 + exp(-g)) u quantized to Q8_0 (hq, hd, hs) instead of the two outputs. CAP (capture
+// mode, a test hook): the same kernel, which also stores the operands it hands the matrix core (each staged weight
+// block, each token's hi and lo fragments and its power of two) at gemm_split_capture_layout.
+template <int TYPE, int TT, int ROWS, bool MOE, int PD, bool SWP = false, bool CAP = false>
 __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_split(GemmArgs a) {
     static_assert(PD == 2 || PD == 4, "prefetch distance");
     static_assert(!SWP || (MOE && ROWS == 256 && TT == 64), "the SwiGLU pair: MoE tiles of 256 rows x 64 tokens");
+    static_assert(!(SWP && CAP), "no capture of the SwiGLU pair");
     using S = SpW<TYPE>;
     using G = SpGeo<TT, ROWS>;
     constexpr int PW = G::PW;
-    constexpr int ROW = SP_ROW, VN = G::VN, TPR = G::TPR, NW = VN / 4;
-    __shared__ __attribute__((aligned(16))) _Float16 sW0[ROWS * ROW], sW1[ROWS * ROW];
-    __shared__ __attribute__((aligned(16))) _Float16 sX0[TT * ROW], sX1[TT * ROW];
+    constexpr int VN = G::VN, TPR = G::TPR, NW = VN / 4;
+    // (the SwiGLU epilogue reuses sW0 / sW1 as [32][129] floats each)
+    constexpr int WH = SWP ? (ROWS * 32 > 2 * 32 * 129 ? ROWS * 32 : 2 * 32 * 129) : ROWS * 32;
+    __shared__ __attribute__((aligned(16))) _Float16 sW0[WH], sW1[WH];
+    __shared__ __attribute__((aligned(16))) _Float16 sX0[TT * 32], sX1[TT * 32];
     __shared__ uint16_t sD0[TT], sD1[TT];  // ds of (token, the stage's block), fp16 bits
     __shared__ float sT[TT];               // 2^-s per token
 
@@ -322,10 +341,13 @@ __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_spl
     const int K = a.K, nb = K / 32;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-    // staging roles. Weights: row n0 + tid / PW, part tid % PW of its block (rows past the end repeat the last;
-    // their outputs are not stored). Tokens: row xr = tid / TPR, values x0 .. x0 + VN - 1 of each block.
-    const int wr = n0 + (SWP ? (tid / PW) % (ROWS / 2) : tid / PW), wp = tid % PW;
-    const uint8_t *wrow = (SWP && tid / PW >= ROWS / 2 ? a.W2 : a.W) +
+    // staging roles. Weights: LDS row lr = tid / PW (global row n0 + lr; SWP: rows 0 .. ROWS / 2 - 1 of W, then
+    // of W2), part tid % PW of its block (rows past the end repeat the last; their outputs are not stored).
+    // Tokens: row xr = tid / TPR, values x0 .. x0 + VN - 1 of each block. (Rows by tid % ROWS and tid % TT instead,
+    // with conflict-free token stores, made the compiler wait for every load in flight each stage: 832 -> 1228 us.)
+    const int lr = tid / PW, wp = tid % PW;
+    const int wr = n0 + (SWP ? lr % (ROWS / 2) : lr);
+    const uint8_t *wrow = (SWP && lr >= ROWS / 2 ? a.W2 : a.W) +
                           ((long long)e * a.N + (wr < a.N ? wr : a.N - 1)) * a.row_bytes;
     const int xr = tid / TPR, xp = tid % TPR, x0 = VN * xp;
     const long long xrow = trow(xr);
@@ -364,19 +386,25 @@ __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_spl
         sh = sh > 100 ? 100 : sh < -100 ? -100 : sh;
         up = ldexpf(1.0f, sh);
         if (xp == 0) sT[xr] = ldexpf(1.0f, -sh);
+        if constexpr (CAP) {  // (row tile 0: every row tile forms the same)
+            const bool live = MOE ? xr < tn : tbase + xr < a.T;
+            if (xp == 0 && n0 == 0 && live)
+                a.cap[gemm_split_capture_layout(K, a.cap_xr).s_off + xrow] = sh;
+        }
     }
 
     auto commit = [&](auto cc, const Pre &p) {
         constexpr int c = decltype(cc)::value;
         _Float16 *sw = pick2<c>(sW0, sW1), *sx = pick2<c>(sX0, sX1);
         uint16_t *sd = pick2<c>(sD0, sD1);
-        S::template decode<PW>(p.raw, sw + (tid / PW) * ROW, wp);
+        S::template decode<PW>(p.raw, sw, lr, wp);
         uint32_t o[VN / 2];
 #pragma unroll
         for (int k = 0; k < NW; ++k) i8_to_h2(p.q.w[k], o + 2 * k);
-        uint4 *dst = (uint4 *)(sx + xr * ROW + x0);
 #pragma unroll
-        for (int k = 0; k < VN / 8; ++k) dst[k] = make_uint4(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
+        for (int k = 0; k < VN / 8; ++k)
+            *(uint4 *)((uint8_t *)sx + sp_at(xr, x0 / 8 + k)) = make_uint4(o[4 * k], o[4 * k + 1], o[4 * k + 2],
+                                                                           o[4 * k + 3]);
         sd[xr] = __builtin_bit_cast(uint16_t, (_Float16)(p.d * up));  // (the row's TPR threads: one value)
     };
 
@@ -388,20 +416,30 @@ __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_spl
 #pragma unroll
         for (int j = 0; j < CT; ++j) acc[i][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // the stage's MFMAs: each token tile's hi and lo fragments, then its RT hi and RT lo products
-    auto compute = [&](auto cc) {
+    // the stage's MFMAs: each token tile's hi and lo fragments, then its RT hi and RT lo products (stage index st:
+    // the capture's)
+    auto compute = [&](auto cc, int st) {
         constexpr int c = decltype(cc)::value;
         const _Float16 *sw = pick2<c>(sW0, sW1), *sx = pick2<c>(sX0, sX1);
         const uint16_t *sd = pick2<c>(sD0, sD1);
+        if constexpr (CAP) {  // the weight row this thread staged (dense: token tile 0 only; expert tiles: each)
+            if (wp == 0 && wr < a.N && (MOE || tbase == 0)) {
+                const long long o = gemm_split_capture_layout(K, a.cap_xr).w_off +
+                                    (((long long)e * a.N + wr) * nb + st) * 16;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) cap_put4(a, o + 4 * q, *(const uint4 *)((const uint8_t *)sw + sp_at(lr, q)));
+            }
+        }
         {
             const int kk = 8 * (lane >> 4);
             h8 fa[RT];
 #pragma unroll
-            for (int i = 0; i < RT; ++i) fa[i] = *(const h8 *)(sw + (wr0 + 16 * i + (lane & 15)) * ROW + kk);
+            for (int i = 0; i < RT; ++i)
+                fa[i] = *(const h8 *)((const uint8_t *)sw + sp_at(wr0 + 16 * i + (lane & 15), lane >> 4));
 #pragma unroll
             for (int j = 0; j < CT; ++j) {
                 const int tr = wc0 + 16 * j + (lane & 15);
-                const uint4 x = *(const uint4 *)(sx + tr * ROW + kk);
+                const uint4 x = *(const uint4 *)((const uint8_t *)sx + sp_at(tr, lane >> 4));
                 const uint32_t ds = sd[tr];
                 const h2 dd = __builtin_bit_cast(h2, ds | (ds << 16));
                 const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
@@ -415,6 +453,14 @@ __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_spl
                 }
                 const h8 fh = __builtin_bit_cast(h8, make_uint4(hv[0], hv[1], hv[2], hv[3]));
                 const h8 fl = __builtin_bit_cast(h8, make_uint4(lv[0], lv[1], lv[2], lv[3]));
+                if constexpr (CAP) {  // the token's fragments (waves 0 and 1 of row tile 0)
+                    if ((wave >> 1) == 0 && n0 == 0 && (MOE ? tr < tn : tbase + tr < a.T)) {
+                        const long long o = (trow(tr) * nb + st) * 16 + kk / 2;
+                        cap_put4(a, o, make_uint4(hv[0], hv[1], hv[2], hv[3]));
+                        cap_put4(a, gemm_split_capture_layout(K, a.cap_xr).lo_off + o,
+                                 make_uint4(lv[0], lv[1], lv[2], lv[3]));
+                    }
+                }
 #pragma unroll
                 for (int i = 0; i < RT; ++i)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fh, acc[i][j], 0, 0, 0);
@@ -437,7 +483,7 @@ __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_spl
         issue(P[u % PD], s0 + u + PD);
         __builtin_amdgcn_sched_barrier(0);  // (measured: the staging ahead of the MFMAs, not mixed in, is faster)
         __builtin_amdgcn_s_setprio(1);      // the MFMA phase ahead of the other workgroup's staging on this SIMD
-        compute(IC<c>{});
+        compute(IC<c>{}, s0 + u);
         __builtin_amdgcn_s_setprio(0);
         __syncthreads();
     };
@@ -493,6 +539,15 @@ template <int TYPE>
 hipError_t launch_t(const GemmArgs &a, dim3 grid, hipStream_t stream) {
     if (a.n_tiles && a.hq)
         hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, SP_ROWS, true, SP_PD_MOE, true>), grid, dim3(256), 0, stream,
+                           a);
+    else if (a.cap && a.n_tiles)
+        hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, SP_ROWS, true, SP_PD_MOE, false, true>), grid, dim3(256), 0,
+                           stream, a);
+    else if (a.cap && a.tt == SP_T_SMALL)
+        hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, SP_ROWS_SMALL, false, SP_PD_SMALL, false, true>), grid,
+                           dim3(256), 0, stream, a);
+    else if (a.cap)
+        hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T, SP_ROWS, false, SP_PD, false, true>), grid, dim3(256), 0, stream,
                            a);
     else if (a.n_tiles)
         hipLaunchKernelGGL((k_gemm_split<TYPE, SP_T_SMALL, SP_ROWS, true, SP_PD_MOE>), grid, dim3(256), 0, stream, a);

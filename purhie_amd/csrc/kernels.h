@@ -118,6 +118,10 @@ struct GemmArgs {
     // capture mode (null: off; the integer-exact GEMMs): the exact integer each epilogue scales, per token (dense:
     // t; tiles: the entry's output row) and weight row: cap[(t * N + row) * (K / U) + unit], U = gemm_cap_unit(type)
     int32_t *cap;
+    // the split GEMM's capture (cap set): its operands instead of integer sums, in cap_n ints (writes past them are
+    // dropped) for activations of cap_xr rows; layout at gemm_split_capture_layout
+    long long cap_n;
+    int cap_xr;
 };
 
 // a MoE GEMM workgroup's row-tile column (blockIdx.x), with a switched to the pair's second matrix when the column
@@ -148,6 +152,21 @@ int gemm_split_token_tile(bool moe, int T);
 // the MoE gate / up pair with SwiGLU (GemmArgs hq set): rows of each matrix per workgroup, grid (N / this, tiles)
 int gemm_split_swiglu_rows();
 hipError_t launch_gemm_split(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);
+// the exact ROCmFP4 GEMM on the f8f6f4 matrix core (gemm_f8.hip; a measured alternative, test hook only): dense,
+// Q8_0 activation (xq = q0, dx = d0), K a multiple of 64
+hipError_t launch_gemm_f8_exact(const GemmArgs &a, hipStream_t stream);
+// The split GEMM's capture (GemmArgs cap set), in int32 units, nb = K / 32, XR = cap_xr activation rows: for
+// activation row x and stage (32-value block) s, the fp16 hi plane at cap[(x * nb + s) * 16 ..] (32 halves in K
+// order), the lo plane at lo_off + the same, the row's power of two s_x (the GEMM scales X by 2^s_x) at
+// cap[s_off + x]; for weight row w (dense: the row; expert tiles: e * N + row), the 32 fp16 values it staged for
+// block s at cap[w_off + (w * nb + s) * 16 ..]
+struct SplitCapLayout {
+    long long lo_off, s_off, w_off;
+};
+__host__ __device__ inline SplitCapLayout gemm_split_capture_layout(int K, int XR) {
+    const long long plane = (long long)XR * (K / 32) * 16;
+    return SplitCapLayout{plane, 2 * plane, 2 * plane + (XR + 3) / 4 * 4};
+}
 
 // Float activations over F32 / F16 / BF16 weights (type ids 0, 1, 30): the decode matvec for T tokens (round:
 // the activations rounded to the 16-bit weight type), the F16 / BF16 MFMA GEMM on activations rounded to 16 bits

@@ -264,4 +264,19 @@ hipError_t purhie_moe_ffn_noalloc(const purhie_moe_weights *w, const float *xn, 
     return purhie_moe_ffn(w, xn, q8_xn, T, out, ws, PURHIE_MOE_SCRATCH_BYTES, stream);
 }
 
+int purhie_moe_debug_regions(const purhie_moe_weights *w, int T, purhie_moe_regions *r) {
+    if (!r || !valid(w, T)) return -1;
+    char *const base = (char *)(uintptr_t)256;  // (any aligned base: the offsets are relative to it)
+    const Layout L = layout(w, T, base);
+    auto off = [&](const void *p) { return p ? (long long)((const char *)p - base) : -1LL; };
+    const bool sh = has_shexp(w);
+    const bool swiglu_gemm = L.grouped && !qt_vec_dot_q8k(w->type_down) &&
+                             qmatvec_q8_id_batch_swiglu_supported(w->type_gate_up, w->n_ff_exp, w->n_embd);
+    const bool fused = !L.grouped && qmatvec_q8_id_swiglu_supported(w->type_down, w->n_ff_exp);
+    *r = purhie_moe_regions{off(L.ids), off(L.wts), sh && w->shexp_gate ? off(L.sg) : -1, off(L.g), off(L.u),
+                            off(L.qx), off(L.down), off(L.shout), off(L.qs), L.ns, L.qx_k, L.qs_k, L.slot ? 1 : 0,
+                            L.grouped ? 1 : 0, swiglu_gemm ? 0 : 1, fused ? 0 : 1};
+    return 0;
+}
+
 }  // extern "C"

@@ -93,6 +93,14 @@ bool mfma_on() {
 // expert tiles in the decode order: the tile the engine's grouping may use there (the reference's QMV_MM_TB)
 constexpr int ID_DECODE_TILE = 16;
 
+// capture mode over the split GEMM: its operands into g_cap (gemm_split_capture_layout, for the rows q holds)
+void split_capture(GemmArgs &a, const qmatvec_q8 *q, int K) {
+    if (!g_cap) return;
+    a.cap = g_cap;
+    a.cap_n = (long long)g_cap_n;
+    a.cap_xr = q->max_k / K;
+}
+
 // The GEMM's arguments for the activation q, read where it is: Q8_K (qK, dK, bsK) for the K-quants, Q8_0 (q0, d0)
 // for the others
 GemmArgs gemm_args(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N, int K) {
@@ -124,6 +132,7 @@ hipError_t gemm_dense(int type, const void *W, size_t row_bytes, const qmatvec_q
     if (gemm_split(type)) {
         const int BT = gemm_split_token_tile(false, T), RN = gemm_split_rows(false, T);
         a.tt = BT;
+        split_capture(a, q, K);
         return launch_gemm_split(type, a, dim3((unsigned)((T + BT - 1) / BT), (unsigned)((N + RN - 1) / RN)), stream);
     }
     if (const hipError_t e = cap_for((long long)T * N * (K / gemm_cap_unit(type)), a.cap); e != hipSuccess) return e;
@@ -540,7 +549,10 @@ static hipError_t id_gemm(int type, const void *W, const void *W2, size_t row_by
         a.rt = rt;
     }
     const dim3 grid((unsigned)(W2 ? 2 * rt : rt), (unsigned)max_tiles);
-    if (split) return launch_gemm_split(type, a, grid, stream);
+    if (split) {
+        if (!W2) split_capture(a, q, K);
+        return launch_gemm_split(type, a, grid, stream);
+    }
     a.cap = W2 ? nullptr : g_cap;  // (tiles mode: rows from out_rows; the caller sizes the buffer)
     return launch_gemm_i8kq(type, a, grid, stream);
 }
@@ -639,6 +651,18 @@ hipError_t qmatvec_launch_q8_id_batch_swiglu(int type, const void *W, const void
     a.hd = h->d0;
     a.hs = h->s0;
     return launch_gemm_split(type, a, dim3((unsigned)(N / gemm_split_swiglu_rows()), (unsigned)max_tiles), stream);
+}
+
+hipError_t qmatvec_debug_gemm_f8f6f4(const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int ldy, int N,
+                                     int K, int T, hipStream_t stream) {
+    if (!W || !q || !y || N <= 0 || T <= 0 || K <= 0 || K % 64 != 0 || ldy < N ||
+        row_bytes != qt_row_size(TY_FP4, K) || ((uintptr_t)W & 3) != 0 || (long long)T * K > q->max_k)
+        return hipErrorInvalidValue;
+    GemmArgs a = gemm_args(TY_FP4, W, row_bytes, q, y, N, K);
+    a.ldy = ldy;
+    a.T = T;
+    a.osc = dense_scale(W);
+    return launch_gemm_f8_exact(a, stream);
 }
 
 hipError_t qmatvec_debug_capture(int32_t *out, size_t n_ints) {

@@ -30,6 +30,8 @@ def lib():
         }.items():
             f = getattr(L, name)
             f.restype, f.argtypes = i32, args
+        L.purhie_moe_debug_regions.restype = i32
+        L.purhie_moe_debug_regions.argtypes = [C.POINTER(MoeWeights), i32, C.POINTER(MoeRegions)]
         L.purhie_moe_workspace_bytes.restype = C.c_size_t
         L.purhie_moe_workspace_bytes.argtypes = [C.POINTER(MoeWeights), i32]
         _sigs_done = True
@@ -48,6 +50,20 @@ class MoeWeights(C.Structure):
                 ("gate_shexp", C.c_void_p), ("up_shexp", C.c_void_p), ("down_shexp", C.c_void_p),
                 ("rb_shexp_gate_up", C.c_size_t), ("rb_shexp_down", C.c_size_t),
                 ("shexp_gate", C.c_void_p)]
+
+
+class MoeRegions(C.Structure):
+    """purhie_moe_regions (include/moe_layer.h): byte offsets of the layer's intermediate results in its workspace"""
+    _fields_ = [(n, C.c_longlong) for n in ("ids", "wts", "sg", "g", "u", "qx", "down", "shout", "qs")] + \
+               [(n, C.c_int) for n in ("ns", "qx_k", "qs_k", "slot", "grouped", "gu_written", "act_written")]
+
+
+def regions(w, T):
+    """purhie_moe_debug_regions: where purhie_moe_ffn(w, T) leaves its intermediate results"""
+    r = MoeRegions()
+    if lib().purhie_moe_debug_regions(C.byref(w), T, C.byref(r)) != 0:
+        raise ValueError("the layer cannot run with these weights")
+    return r
 
 
 def _p(t):

@@ -86,6 +86,7 @@ def lib():
             "qmatvec_launch_q8_id_batch_pair": (i32, [i32, vp, vp, sz, pq8, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp,
                                                       vp, vp, vp]),
             "qmatvec_debug_block_dots": (i32, [i32, vp, sz, pq8, vp, i32, i32, vp]),
+            "qmatvec_debug_gemm_f8f6f4": (i32, [vp, sz, pq8, vp, i32, i32, i32, i32, vp]),
             "qmatvec_debug_capture": (i32, [vp, sz]),
             "qmatvec_debug_capture_unit": (i32, [i32, i32]),
             "qmatvec_debug_decode_path": (i32, [i32]),
@@ -249,6 +250,12 @@ def decode_path(mode=None):
     """the decode kernels in use: 1 = tile kernels where they take the shape, 0 = per-wave kernels only; sets
     `mode` when given and returns the previous one"""
     return lib().qmatvec_debug_decode_path(-1 if mode is None else mode)
+
+
+def gemm_f8f6f4(W, q, y, N, K, T, stream=None):
+    """qmatvec_debug_gemm_f8f6f4: the exact ROCmFP4 GEMM on the f8f6f4 matrix core, y [T][N]"""
+    _check("qmatvec_debug_gemm_f8f6f4",
+           lib().qmatvec_debug_gemm_f8f6f4(_p(W), row_size(100, K), q.ref, _p(y), N, N, K, T, stream))
 
 
 def block_dots(t, W, q, out, N, K, stream=None):

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from purhie_amd import synth
-from tests import parity
+from tests import moe_stages, parity
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -109,7 +109,7 @@ class Mixed:
         w.type_router, w.router, w.rb_router = 8, self.router_d.data_ptr(), Q.row_size(8, E)
         self.w = w
 
-    def run(self, M, Q, x):
+    def run(self, M, Q, x, keep_ws=False):
         import torch
         T = x.shape[0]
         xd = dev(x)
@@ -118,7 +118,7 @@ class Mixed:
         ws = torch.empty(M.workspace_bytes(self.w, T), dtype=torch.uint8, device="cuda")
         out = torch.full((T, E), float("nan"), dtype=torch.float32, device="cuda")
         M.ffn(self.w, xd, q, T, out, ws)
-        return host(out)
+        return (host(out), host(ws)) if keep_ws else host(out)
 
     def logits(self, Q, x):
         """the router logits as the layer computes them (the same launch, a Q8_0 matvec / GEMM)"""
@@ -158,8 +158,12 @@ def mixed(M, Q):
 
 def test_config4_mixed_prompt(M, Q, oracle, mixed):
     x = synth.gaussian(0xC4100, T_PROMPT * E).reshape(T_PROMPT, E)
-    got = mixed.run(M, Q, x)
+    got, ws = mixed.run(M, Q, x, keep_ws=True)
     assert np.isfinite(got).all()
+    # the call's own stages on its own inputs: routing and combine of every token bit for bit, the down
+    # projections of the sampled tokens within 1e-5 sum |w x|
+    moe_stages.check(M, oracle, mixed.w, x, mixed.logits(Q, x), got, ws, mixed.down, 14, NU, rows=SAMPLE)
+    del ws
     xs = x[list(SAMPLE)]
     # prefill mode (qmatvec_set_prefill): every batch takes the GEMMs, as the 2427-token call does, so a token's
     # router logits and expert outputs do not depend on the batch
@@ -178,6 +182,7 @@ def test_config4_mixed_prompt(M, Q, oracle, mixed):
 
 def test_config4_mixed_one_token(M, Q, oracle, mixed):
     x = synth.gaussian(0xC4200, E).reshape(1, E)
-    got = mixed.run(M, Q, x)
+    got, ws = mixed.run(M, Q, x, keep_ws=True)
+    moe_stages.check(M, oracle, mixed.w, x, mixed.logits(Q, x), got, ws, mixed.down, 14, NU)
     want = mixed.oracle(oracle, x, mixed.logits(Q, x))
     close(got, want, "config 4 mixed, one token")

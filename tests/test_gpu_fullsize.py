@@ -11,6 +11,8 @@ import pytest
 
 from purhie_amd import synth
 
+from tests import moe_stages
+
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
 
@@ -105,6 +107,9 @@ def test_config4_moe_full_size(Q, oracle, T):
     assert Q.lib().qmatvec_launch_batch(0, p(router), 4 * H, p(xd), p(lg), NE, H, T, None) == 0
     logits = host(lg)
     Wg, Wu, Wdn = host(gate), host(up), host(down)
+    # the call's own stages on its own inputs (routing and combine bit for bit, the sampled tokens' down projections
+    # within 1e-5 sum |w x|); then the whole layer against the oracle's composition as a reading
+    moe_stages.check(M, oracle, w, x, logits, got, host(ws), Wdn, t, NU, rows=sorted({0, T // 3, T - 1}))
     for i in sorted({0, T // 3, T - 1}):
         ids, wts = oracle.moe_router(logits[i:i + 1], NU)
         a = oracle.quantize_act(x[i], False)

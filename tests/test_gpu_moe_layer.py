@@ -12,6 +12,8 @@ import pytest
 
 from purhie_amd import synth
 
+from tests import moe_stages
+
 pytestmark = pytest.mark.gpu
 
 KQ = (12, 13, 14, 23)
@@ -109,7 +111,7 @@ class Layer:
             Q.launch_q8_batch(self.router_t, self.keep[3], q, y, self.NE, self.NE, self.E, T)
         return host(y)
 
-    def run(self, M, Q, x):
+    def run(self, M, Q, x, keep_ws=False):
         import torch
         T = x.shape[0]
         q = Q.Q8(((T * self.E + 255) // 256) * 256)
@@ -120,7 +122,11 @@ class Layer:
         ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
         out = torch.full((T, self.E), float("nan"), dtype=torch.float32, device="cuda")
         M.ffn(self.w, xd, q, T, out, ws)
-        return host(out)
+        return (host(out), host(ws)) if keep_ws else host(out)
+
+    def check_stages(self, M, oracle, x, logits, out, ws):
+        moe_stages.check(M, oracle, self.w, x, logits, out, ws, self.down, self.t_d, self.NU,
+                         self.sdown if self.shexp else None, self.t_sd, self.FS)
 
     def oracle(self, oracle, x, logits):
         T, E, FE, NU = x.shape[0], self.E, self.FE, self.NU
@@ -259,8 +265,12 @@ def test_matches_oracle(M, Q, oracle, case):
     T = case.pop("T")
     lay = Layer(M, Q, oracle, 300 + T, **case)
     x = acts(40 + T, T, lay.E)
-    got = lay.run(M, Q, x)
-    want, _ = lay.oracle(oracle, x, lay.logits(Q, x))
+    got, ws = lay.run(M, Q, x, keep_ws=True)
+    logits = lay.logits(Q, x)
+    lay.check_stages(M, oracle, x, logits, got, ws)
+    # the whole layer against the oracle's own composition: a reading (a re-quantized SwiGLU value can move by a
+    # step where the fp32 sums differ in order, so this bound is looser than the stages')
+    want, _ = lay.oracle(oracle, x, logits)
     close(got, want)
 
 

@@ -21,7 +21,7 @@ from purhie_amd import synth
 T, E, NU, H, F = 512, 128, 8, 2048, 768
 N_ENT = T * NU
 TILE = 64                    # qmatvec_id_batch_tile for the split GEMM's MoE tiles
-ROWS, TT, ROW = 256, 64, 40  # split GEMM MoE tile: weight rows, token entries, LDS halves per row
+ROWS, TT = 256, 64           # split GEMM MoE tile: weight rows, token entries
 PD = 4                       # MoE prefetch distance: stages past the end reload the last one
 BB = 18                      # ROCmFP4 block bytes
 LOGIT_SEED = 0x5EED2104      # bench.py's prefill router logits
@@ -29,6 +29,11 @@ LOGIT_SEED = 0x5EED2104      # bench.py's prefill router logits
 
 def row_size(K):
     return K // 32 * BB
+
+
+def sp_at(r, ch):
+    """gemm_split.hip's LDS place (bytes) of 16-byte chunk ch of a stage's row r"""
+    return ((r >> 4) << 10) + (ch << 8) + ((r & 15) << 4)
 
 
 def q8_sections(max_k):
@@ -114,6 +119,10 @@ def split_gemm_replay(routing, N, K, swp, w_bytes, x_rows, y_or_h):
     VN, TPR = TT // 8, 32 // (TT // 8)
     xr, xp = tid // TPR, tid % TPR
     x0 = VN * xp
+    lr = tid // (256 // ROWS)
+    # LDS bytes of sW0 / sW1 (the SwiGLU epilogue's [32][129] floats share them) and of sX0 / sX1
+    sw_bytes = 2 * (max(ROWS * 32, 2 * 32 * 129) if swp else ROWS * 32)
+    sx_bytes = TT * 64
     stages = np.arange(nb + PD)  # the loop's issues: stages 0 .. nb - 1 + PD, clamped to nb - 1
     s_cl = np.minimum(stages, nb - 1)
     for k in range(nt):
@@ -121,7 +130,7 @@ def split_gemm_replay(routing, N, K, swp, w_bytes, x_rows, y_or_h):
         inside("in_rows / out_rows", (st + np.arange(n)) * 4, 4, N_ENT * 4)
         for bx in range(gx):
             n0 = bx * (ROWS // 2) if swp else bx * ROWS
-            wr = n0 + (tid % (ROWS // 2) if swp else tid)
+            wr = n0 + (lr % (ROWS // 2) if swp else lr)
             wrow = (e * N + np.minimum(wr, N - 1)) * rb  # byte offset in W (or W2: the same size)
             b = wrow[:, None] + s_cl[None, :] * BB
             al = b - (b & 3)  # allocation bases are 256-aligned: the offset's low bits are the address's
@@ -132,24 +141,24 @@ def split_gemm_replay(routing, N, K, swp, w_bytes, x_rows, y_or_h):
             inside("xq = q0", (xrow * K + x0)[:, None] + 32 * s_cl[None, :], 8, sec["q0"])
             inside("dx = d0 (stages)", ((xrow * nb)[:, None] + s_cl[None, :]) * 4, 4, sec["d0"])
             inside("dx = d0 (the prologue's max)", (xrow * nb + nb - 1) * 4, 4, sec["d0"])
-            # LDS: the weight row tid / PW (PW = 1), its 32 halves; the token row xr, values x0 .. x0 + VN - 1
-            inside("sW (LDS)", tid * ROW * 2, 64, ROWS * ROW * 2)
-            inside("sX (LDS)", (xr * ROW + x0) * 2, VN * 2, TT * ROW * 2)
-            # fragments: rows wr0 + 16 i + lane % 16, halves 8 (lane / 16) .. + 7
+            # LDS: the weight row lr's four 16-byte chunks; the token row xr's chunks x0 / 8 ..
+            inside("sW (LDS)", np.array([sp_at(lr, ch) for ch in range(4)]), 16, sw_bytes)
+            inside("sX (LDS)", np.array([sp_at(xr, x0 // 8 + k) for k in range(VN // 8)]), 16, sx_bytes)
+            # fragments: rows wr0 + 16 i + lane % 16, chunk lane / 16
             RT, CT = ROWS // 32, TT // 32
             wr0, wc0 = (wave >> 1) * RT * 16, (wave & 1) * CT * 16
             i = np.arange(RT)[None, :]
-            inside("sW fragments (LDS)", ((wr0[:, None] + 16 * i + (lane[:, None] & 15)) * ROW +
-                                          8 * (lane[:, None] >> 4)) * 2, 16, ROWS * ROW * 2)
+            inside("sW fragments (LDS)", sp_at(wr0[:, None] + 16 * i + (lane[:, None] & 15), lane[:, None] >> 4),
+                   16, sw_bytes)
             jj = np.arange(CT)[None, :]
             tr = wc0[:, None] + 16 * jj + (lane[:, None] & 15)
-            inside("sX fragments (LDS)", (tr * ROW + 8 * (lane[:, None] >> 4)) * 2, 16, TT * ROW * 2)
+            inside("sX fragments (LDS)", sp_at(tr, lane[:, None] >> 4), 16, sx_bytes)
             if swp:
                 # up waves (2, 3) write u into their buffer of sW0 / sW1: [token][129] floats
                 tl = 16 * np.arange(CT)[:, None] + (lane[None, :] & 15)
                 u_idx = (tl[:, :, None] * 129 + 16 * np.arange(RT)[None, None, :] +
                          4 * (lane[None, :, None] >> 4))[..., None] + np.arange(4)
-                inside("sU (LDS, in sW)", u_idx * 4, 4, ROWS * ROW * 2)
+                inside("sU (LDS, in sW)", u_idx * 4, 4, sw_bytes)
                 # gate waves (0, 1): quantized SwiGLU rows out_rows[tt] for tt < n
                 for w_ in (0, 1):
                     tt = 16 * CT * (w_ & 1) + tl
