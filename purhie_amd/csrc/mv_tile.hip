@@ -1065,7 +1065,9 @@ static hipError_t tile_id_launch(const MvIdArgs &a, const TileArgs &ta, hipStrea
     const bool small = a.K / 16 <= THR && a.K / Tu<TYPE>::ACT <= THR;  // a thread for every value chunk and scale
     if (a.route_logits) {
         if constexpr (THR == 256) {
-            if (a.cap || a.n_tiles) return hipErrorNotSupported;
+            // (the routed kernel's static router LDS comes on top of the tile's: past 64 KiB in all, the caller
+            // falls back to the router and the pair as two launches)
+            if (a.cap || a.n_tiles || lds + sizeof(RouterLds<1>) > 65536) return hipErrorNotSupported;
             if (small)
                 hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, false, false, true, true>), grid, dim3(THR), lds, stream, a,
                                    ta);
