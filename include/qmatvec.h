@@ -37,17 +37,20 @@ void qmatvec_free(void);
 int qmatvec_set_out_scale(const void *owner, const void *W, size_t bytes, const float *s, int n);
 void qmatvec_drop_out_scales(const void *owner);
 
-/* replaces src/qmatvec.h:29: 1 if a float-activation matvec exists for the type: F32, F16 and BF16 (the
- * quantized types' path is the int8 one below) */
+/* replaces src/qmatvec.h:29: 1 if a float-activation matvec exists for the type: F32, F16, BF16, and the quantized
+ * types Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS, MXFP4, NVFP4, ROCmFP4 and ROCmFP4_FAST (fp32 activations against the
+ * exactly decoded weights; the int8 path below is the fast one) */
 int qmatvec_supported(int type);
 
-/* Float activations over F32 / F16 / BF16 weights (replace src/qmatvec.h:33-75). F16 / BF16 weights multiply the
- * activations rounded to the weight type (nearest even), so every product is exact; F32 and _bf16f multiply
- * the fp32 activations as they are. Same arguments, checks and error codes as the reference's.
+/* Float activations (replace src/qmatvec.h:33-75). F16 / BF16 weights multiply the activations rounded to the
+ * weight type (nearest even), so every product is exact; F32, _bf16f and the quantized types multiply the fp32
+ * activations as they are. Same arguments, checks and error codes as the reference's.
  *   qmatvec_launch_bf16f    BF16 weights (row_bytes = 2 K), fp32 activations not rounded, T rows
- *   qmatvec_launch          one row of x; type F32 / F16 / BF16, row_bytes = qt_row_size(type, K)
+ *   qmatvec_launch          one row of x; a type qmatvec_supported takes, row_bytes = qt_row_size(type, K), K a
+ *                           whole number of blocks; a registered output scale multiplies the quantized types' rows
  *   qmatvec_launch_batch    T rows; F16 / BF16 batches qmatvec_half_supported takes go to the MFMA GEMM (which
- *                           rounds x while staging it: nothing allocated), the rest to the decode kernel
+ *                           rounds x while staging it: nothing allocated), the rest to the decode kernels (a
+ *                           token's row the same bits as qmatvec_launch gives it)
  *   qmatvec_launch_batch_h  the same with the caller's scratch xh (16-byte aligned, xh_bytes >= 2 T K) for the copy
  *   qmatvec_half_supported  F16 / BF16, GEMMs on, T >= 32 (any T in prefill mode), N >= 64, K % 8 == 0,
  *                           row_bytes >= 2 K and a multiple of 16, W 16-byte aligned
@@ -66,10 +69,9 @@ hipError_t qmatvec_round_half(int type, const float *x, uint16_t *xh, long long 
 hipError_t qmatvec_launch_batch_hx(int type, const void *W, size_t row_bytes, const uint16_t *xh, float *y, int N,
                                    int K, int T, hipStream_t stream);
 
-/* The low-rank, split-Q8_0 and float MoE entries of the reference (src/qmatvec.h:68-75,145-147,179-199) are
- * outside this path. They are exported so that the engine links unchanged; their *_supported queries return 0
- * and the launches return hipErrorInvalidDeviceFunction, as the reference's do for a kernel its code object
- * lacks. */
+/* The low-rank and split-Q8_0 entries of the reference (src/qmatvec.h:68-75,145-147) are outside this path. They
+ * are exported so that the engine links unchanged; their *_supported queries return 0 and the launches return
+ * hipErrorInvalidDeviceFunction, as the reference's do for a kernel its code object lacks. */
 int qmatvec_q8_0s_source_supported(int type, int K);
 hipError_t qmatvec_quantize_rows_q8_0(int type, const void *W, size_t row_bytes, int N, int K, int8_t *qs, uint16_t *d,
                                       hipStream_t stream);
@@ -223,13 +225,20 @@ hipError_t qmatvec_launch_q8_id_batch_swiglu(int type, const void *W, const void
                                              const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
                                              const int32_t *out_rows, hipStream_t stream);
 
-/* outside this path (as qmatvec_launch above): the split-Q8_0 LM head, the low-rank and the float MoE entries
- * (src/qmatvec.h:74-75,145-147,179-180,195-199): *_supported 0, hipErrorInvalidDeviceFunction */
+/* outside this path (as qmatvec_quantize_rows_q8_0 above): the split-Q8_0 LM head and the low-rank entry
+ * (src/qmatvec.h:74-75,145-147): *_supported 0, hipErrorInvalidDeviceFunction */
 hipError_t qmatvec_launch_q8_0s(const int8_t *qs, const uint16_t *d, const qmatvec_q8 *q, float *y, int N, int K,
                                 hipStream_t stream);
 int qmatvec_q8_lr_supported(int type, int K);
 hipError_t qmatvec_launch_q8_lr(int type, const void *W, size_t row_bytes, const float *lo, int n, int K, float scale,
                                 float *y, int N, hipStream_t stream);
+
+/* Float-activation MoE entries (replace src/qmatvec.h:179-180,195-199), for the types qmatvec_supported takes.
+ * qmatvec_launch_id: token t, slot j < n_used: expert e = ids[t n_used + j] (rows e N .. e N + N - 1 of W) times
+ * input row t (x_per_slot 0) or t n_used + j into output row t n_used + j; an id below 0 writes nothing.
+ * qmatvec_launch_id_batch_f: the same over the grouping's expert tiles of up to `tile` <= 16 entries (in_rows:
+ * input rows, out_rows: output rows); each entry gets the bits qmatvec_launch_id gives it, and a quantized type's
+ * entry the bits qmatvec_launch gives that expert's rows. Registered output scales (per stacked expert) apply. */
 hipError_t qmatvec_launch_id(int type, const void *W, size_t row_bytes, const int32_t *ids, int n_used, int x_per_slot,
                              const float *x, float *y, int N, int K, int T, hipStream_t stream);
 int qmatvec_id_batch_f_supported(int type);

@@ -178,6 +178,19 @@ hipError_t launch_gemm_float(int type, const uint8_t *W, long long rb, const uin
 hipError_t launch_gemm_float_x(int type, const uint8_t *W, long long rb, const float *x, float *y, int N, int K,
                                int T, hipStream_t stream);
 hipError_t launch_round_half(int type, const float *x, uint16_t *xh, long long n, hipStream_t stream);
+// fp32 activations over quantized weights (fquant.hip; with_float: F32 / F16 / BF16 too, for the expert-indexed
+// forms): T dense tokens; expert-indexed (ids [T][n_used]); expert tiles of up to fq_tile() entries. s: the output
+// scale, es: per-expert scales (null: s)
+bool fq_type(int type, bool with_float);
+int fq_tile();
+hipError_t launch_fq_dense(int type, const uint8_t *W, long long rb, const float *x, float *y, int N, int K, int T,
+                           float s, hipStream_t stream);
+hipError_t launch_fq_id(int type, const uint8_t *W, long long rb, const int32_t *ids, int n_used, int x_per_slot,
+                        const float *x, float *y, int N, int K, int T, const float *es, float s, hipStream_t stream);
+hipError_t launch_fq_tiles(int type, const uint8_t *W, long long rb, const float *x, float *y, int N, int K,
+                           int max_tiles, const int32_t *n_tiles, const int32_t *tile_e, const int32_t *tile_start,
+                           const int32_t *tile_n, const int32_t *in_rows, const int32_t *out_rows, const float *es,
+                           float s, hipStream_t stream);
 // the int8-MFMA GEMM (gemm_i8.hip: Q4_K, Q5_K, Q6_K, IQ4_XS with the Q8_K activation, xq = qK, dx = dK, xsum =
 // bsK; Q8_0, MXFP4 with the Q8_0 one, xq = q0, dx = d0): dense grid (tokens / gemm_i8kq_token_tile(false), rows /
 // gemm_i8kq_rows()), MoE grid (rows / gemm_i8kq_rows(), tiles) with tiles of up to gemm_i8kq_token_tile(true) entries

@@ -155,25 +155,34 @@ int qmatvec_init(const char *co_path) {
 
 void qmatvec_free(void) { g_inited = 0; }
 
-// ---- float activations over F32 / F16 / BF16 weights (src/qmatvec.cpp:255-366). The quantized types have no
-// float-activation kernel here (their path is the int8 one): qmatvec_supported answers 0 for them and their
-// float launches return hipErrorInvalidDeviceFunction, the reference's answer for a missing kernel.
+// ---- float activations (src/qmatvec.cpp:255-366, 601-671): F32 / F16 / BF16 weights through fmat.hip (decode
+// matvec, MFMA GEMM), the quantized types (Q8_0, K-quants, IQ4_XS, the FP4 family) through fquant.hip's kernel (fp32
+// activations against the exactly decoded weights), expert-indexed forms of both through fquant.hip. Other types
+// return hipErrorInvalidDeviceFunction, the reference's answer for a missing kernel.
 namespace {
 bool float_type(int t) { return t == QT_F32 || t == QT_F16 || t == QT_BF16; }
 bool half_type(int t) { return t == QT_F16 || t == QT_BF16; }
 bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
+// the reference's shape checks: K a whole number of blocks, row_bytes the type's row size
+bool float_shape_ok(int type, size_t row_bytes, int K) {
+    const qt_traits *tr = qt_get_traits(type);
+    return tr && K > 0 && K % tr->blck_size == 0 && row_bytes == qt_row_size(type, K);
+}
+
 // the decode kernel over T tokens, after the reference's argument checks
 hipError_t float_rows(int type, bool round, const void *W, size_t row_bytes, const float *x, float *y, int N, int K,
                       int T, hipStream_t stream) {
-    if (!float_type(type)) return hipErrorInvalidDeviceFunction;
-    if (!W || !x || !y || N < 0 || K <= 0 || T < 1 || row_bytes != qt_row_size(type, K)) return hipErrorInvalidValue;
+    if (!float_type(type) && !fq_type(type, false)) return hipErrorInvalidDeviceFunction;
+    if (!W || !x || !y || N < 0 || T < 1 || !float_shape_ok(type, row_bytes, K)) return hipErrorInvalidValue;
     if (N == 0) return hipSuccess;
+    if (!float_type(type))
+        return launch_fq_dense(type, (const uint8_t *)W, (long long)row_bytes, x, y, N, K, T, dense_scale(W), stream);
     return launch_mv_float(type, round, (const uint8_t *)W, (long long)row_bytes, x, y, N, K, T, stream);
 }
 }  // namespace
 
-int qmatvec_supported(int type) { return float_type(type) ? 1 : 0; }
+int qmatvec_supported(int type) { return float_type(type) || fq_type(type, false) ? 1 : 0; }
 
 hipError_t qmatvec_launch_bf16f(const void *W, size_t row_bytes, const float *x, float *y, int N, int K, int T,
                                 hipStream_t stream) {
@@ -235,15 +244,40 @@ int qmatvec_q8_lr_supported(int, int) { return 0; }
 hipError_t qmatvec_launch_q8_lr(int, const void *, size_t, const float *, int, int, float, float *, int, hipStream_t) {
     return hipErrorInvalidDeviceFunction;
 }
-hipError_t qmatvec_launch_id(int, const void *, size_t, const int32_t *, int, int, const float *, float *, int, int, int,
-                             hipStream_t) {
-    return hipErrorInvalidDeviceFunction;
+// Float expert-indexed matvecs: for token t and slot j, expert e = ids[t n_used + j] (rows e N .. e N + N - 1 of W)
+// times input row t (x_per_slot 0) or t n_used + j into output row t n_used + j; an id below 0 writes nothing.
+hipError_t qmatvec_launch_id(int type, const void *W, size_t row_bytes, const int32_t *ids, int n_used, int x_per_slot,
+                             const float *x, float *y, int N, int K, int T, hipStream_t stream) {
+    if (!fq_type(type, true)) return hipErrorInvalidDeviceFunction;
+    if (T <= 0 || n_used <= 0 || !float_shape_ok(type, row_bytes, K)) return hipErrorInvalidValue;
+    if (!W || !ids || !x || !y || N < 0) return hipErrorInvalidValue;
+    if (N == 0) return hipSuccess;
+    const float *es;
+    float s;
+    expert_scale(W, es, s);
+    return launch_fq_id(type, (const uint8_t *)W, (long long)row_bytes, ids, n_used, x_per_slot, x, y, N, K, T, es, s,
+                        stream);
 }
-int qmatvec_id_batch_f_supported(int) { return 0; }
-hipError_t qmatvec_launch_id_batch_f(int, const void *, size_t, const float *, float *, int, int, int, int,
-                                     const int32_t *, const int32_t *, const int32_t *, const int32_t *, const int32_t *,
-                                     const int32_t *, hipStream_t) {
-    return hipErrorInvalidDeviceFunction;
+
+int qmatvec_id_batch_f_supported(int type) { return fq_type(type, true) ? 1 : 0; }
+
+// The same over expert tiles (the grouping's tiles of up to `tile` <= 16 entries): each entry gets the bits
+// qmatvec_launch_id gives it
+hipError_t qmatvec_launch_id_batch_f(int type, const void *W, size_t row_bytes, const float *x, float *y, int N, int K,
+                                     int max_tiles, int tile, const int32_t *n_tiles, const int32_t *tile_e,
+                                     const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
+                                     const int32_t *out_rows, hipStream_t stream) {
+    if (!qmatvec_id_batch_f_supported(type)) return hipErrorInvalidDeviceFunction;
+    if (max_tiles <= 0 || tile <= 0 || tile > fq_tile() || !float_shape_ok(type, row_bytes, K))
+        return hipErrorInvalidValue;
+    if (!W || !x || !y || !n_tiles || !tile_e || !tile_start || !tile_n || !in_rows || !out_rows || N < 0)
+        return hipErrorInvalidValue;
+    if (N == 0) return hipSuccess;
+    const float *es;
+    float s;
+    expert_scale(W, es, s);
+    return launch_fq_tiles(type, (const uint8_t *)W, (long long)row_bytes, x, y, N, K, max_tiles, n_tiles, tile_e,
+                           tile_start, tile_n, in_rows, out_rows, es, s, stream);
 }
 
 void qmatvec_set_prefill(int on) { g_prefill = on && !getenv("QMATVEC_PREFILL_SPLIT_VARIANT"); }

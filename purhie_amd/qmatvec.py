@@ -97,6 +97,9 @@ def lib():
             "qmatvec_q8_id_swiglu_supported": (i32, [i32, i32]),
             "qmatvec_launch_q8_id_swiglu": (i32, [i32, vp, vp, sz, vp, i32, vp, vp, vp, i32, i32, i32, vp]),
             "qmatvec_launch": (i32, [i32, vp, sz, vp, vp, i32, i32, vp]),
+            "qmatvec_launch_id": (i32, [i32, vp, sz, vp, i32, i32, vp, vp, i32, i32, i32, vp]),
+            "qmatvec_id_batch_f_supported": (i32, [i32]),
+            "qmatvec_launch_id_batch_f": (i32, [i32, vp, sz, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp]),
             "qmatvec_launch_bf16f": (i32, [vp, sz, vp, vp, i32, i32, i32, vp]),
             "qmatvec_launch_batch": (i32, [i32, vp, sz, vp, vp, i32, i32, i32, vp]),
             "qmatvec_launch_batch_h": (i32, [i32, vp, sz, vp, vp, sz, vp, i32, i32, i32, vp]),

@@ -195,8 +195,8 @@ def test_float_error_codes(Q):
     W = torch.zeros(1 << 16, dtype=torch.uint8, device="cuda")
     x = torch.zeros(4096, dtype=torch.float32, device="cuda")
     y = torch.zeros(4096, dtype=torch.float32, device="cuda")
-    assert [L.qmatvec_supported(t) for t in (0, 1, 30, 8, 12, 100)] == [1, 1, 1, 0, 0, 0]
-    assert L.qmatvec_launch(8, p(W), 34 * 2, p(x), p(y), 4, 64, None) == 98     # no float kernel for Q8_0
+    assert [L.qmatvec_supported(t) for t in (0, 1, 30, 8, 12, 100, 2)] == [1, 1, 1, 1, 1, 1, 0]
+    assert L.qmatvec_launch(2, p(W), 18 * 2, p(x), p(y), 4, 64, None) == 98     # no float kernel for Q4_0
     assert L.qmatvec_launch(1, p(W), 2 * 64 + 2, p(x), p(y), 4, 64, None) == 1  # row bytes != 2 K
     assert L.qmatvec_launch_bf16f(p(W), 2 * 64, p(x), p(y), 4, 64, 0, None) == 1  # T < 1
     assert L.qmatvec_half_supported(1, p(W), 2 * 1024, 64, 1024, 31) == 0  # under 32 tokens outside prefill
