@@ -69,9 +69,10 @@ hipError_t qmatvec_round_half(int type, const float *x, uint16_t *xh, long long 
 hipError_t qmatvec_launch_batch_hx(int type, const void *W, size_t row_bytes, const uint16_t *xh, float *y, int N,
                                    int K, int T, hipStream_t stream);
 
-/* The low-rank and split-Q8_0 entries of the reference (src/qmatvec.h:68-75,145-147) are outside this path. They
- * are exported so that the engine links unchanged; their *_supported queries return 0 and the launches return
- * hipErrorInvalidDeviceFunction, as the reference's do for a kernel its code object lacks. */
+/* The split-Q8_0 copy of a float matrix, for the opt-in Q8_0 LM head (replace src/qmatvec.h:68-75): ggml's Q8_0
+ * quantization per 32 values (d = amax / 127 stored as fp16, q = roundf(x / d) with the fp32 d) into values qs [N][K]
+ * (16-byte aligned) and scales d [N][K / 32]; F32 / F16 / BF16 rows, K % 256 == 0. qmatvec_launch_q8_0s: y = qs x
+ * with x given by the Q8_0 part of q, as ggml's Q8_0 x Q8_0 dot (K % 256 == 0, K <= q->max_k). */
 int qmatvec_q8_0s_source_supported(int type, int K);
 hipError_t qmatvec_quantize_rows_q8_0(int type, const void *W, size_t row_bytes, int N, int K, int8_t *qs, uint16_t *d,
                                       hipStream_t stream);
@@ -225,10 +226,11 @@ hipError_t qmatvec_launch_q8_id_batch_swiglu(int type, const void *W, const void
                                              const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
                                              const int32_t *out_rows, hipStream_t stream);
 
-/* outside this path (as qmatvec_quantize_rows_q8_0 above): the split-Q8_0 LM head and the low-rank entry
- * (src/qmatvec.h:74-75,145-147): *_supported 0, hipErrorInvalidDeviceFunction */
 hipError_t qmatvec_launch_q8_0s(const int8_t *qs, const uint16_t *d, const qmatvec_q8 *q, float *y, int N, int K,
                                 hipStream_t stream);
+/* replace src/qmatvec.h:145-147: one token, y = W x with x = SiLU(lo * scale) for lo [n], zero-padded to K and
+ * quantized to Q8_0 inside the kernel: the bits gpu_swiglu(lo * scale, 1, .., q8) followed by qmatvec_launch_q8
+ * give (no output scale). ROCmFP4_FAST, K % 128 == 0, K <= 1024, n <= K, W and row_bytes 4-byte aligned. */
 int qmatvec_q8_lr_supported(int type, int K);
 hipError_t qmatvec_launch_q8_lr(int type, const void *W, size_t row_bytes, const float *lo, int n, int K, float scale,
                                 float *y, int N, hipStream_t stream);

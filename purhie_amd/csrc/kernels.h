@@ -38,8 +38,17 @@ struct MvArgs {
     int Nt, K, L, T;
     int32_t *cap;        // capture mode (null: off): every scale group's integer dot is added into
                          // cap[(t * Nt + row) * (K / G) + group] (G = cap_group(type)); the buffer starts at zero
+    // set (ROCmFP4_FAST, one token, K <= 1024): the activation is SiLU(lr_lo[i] lr_scale) for i < lr_n, 0 up to K,
+    // quantized to Q8_0 in the kernel (q / d unused)
+    const float *lr_lo;
+    int lr_n;
+    float lr_scale;
 };
 hipError_t launch_matvec(int type, const MvArgs &a, hipStream_t stream);
+// the low-rank input (MvArgs lr_lo set): the tile kernel where it takes the shape, else the per-wave kernel, each
+// with the activation made in the kernel as the launch_matvec of SwiGLU(lo scale, 1)'s quantization would see it
+hipError_t launch_matvec_lr(int type, const MvArgs &a, hipStream_t stream);
+constexpr int LR_MAXK = 1024;
 
 // the values one weight scale covers (the capture's group): 16 for ROCmFP4, NVFP4 and Q6_K, else 32
 constexpr int cap_group(int type) { return type == 100 || type == 40 || type == 14 ? 16 : 32; }
@@ -82,6 +91,7 @@ bool matvec_id_swiglu_supported(int type, int K);
 // the one-unit-per-lane tile kernels (mv_tile.hip); hipErrorNotSupported for a shape or alignment they do
 // not take (launch_matvec / launch_matvec_id then use the per-wave kernels)
 hipError_t launch_matvec_tile(int type, const MvArgs &a, hipStream_t stream);
+hipError_t launch_matvec_tile_lr(int type, const MvArgs &a, hipStream_t stream);
 hipError_t launch_matvec_id_tile(int type, const MvIdArgs &a, hipStream_t stream);
 
 // per-scale-group integer dots (test hook)
@@ -191,6 +201,12 @@ hipError_t launch_fq_tiles(int type, const uint8_t *W, long long rb, const float
                            int max_tiles, const int32_t *n_tiles, const int32_t *tile_e, const int32_t *tile_start,
                            const int32_t *tile_n, const int32_t *in_rows, const int32_t *out_rows, const float *es,
                            float s, hipStream_t stream);
+// the split-Q8_0 copy of an F32 / F16 / BF16 matrix (qs [N][K], fp16 d [N][K / 32]; K % 256 == 0) and its matvec
+// on a Q8_0 activation (q8, d8): lmhead.hip
+hipError_t launch_quant_rows_q8_0(int type, const uint8_t *W, long long rb, int N, int K, int8_t *qs, uint16_t *d,
+                                  hipStream_t stream);
+hipError_t launch_mv_q8_0s(const int8_t *qs, const uint16_t *d, const int8_t *q8, const float *d8, float *y, int N,
+                           int K, hipStream_t stream);
 // the int8-MFMA GEMM (gemm_i8.hip: Q4_K, Q5_K, Q6_K, IQ4_XS with the Q8_K activation, xq = qK, dx = dK, xsum =
 // bsK; Q8_0, MXFP4 with the Q8_0 one, xq = q0, dx = d0): dense grid (tokens / gemm_i8kq_token_tile(false), rows /
 // gemm_i8kq_rows()), MoE grid (rows / gemm_i8kq_rows(), tiles) with tiles of up to gemm_i8kq_token_tile(true) entries

@@ -638,6 +638,40 @@ __global__ void __launch_bounds__(MV_THREADS) k_matvec(MvArgs a) {
     }
 }
 
+// The low-rank input (the reference's matvec_q8_lr, src/matvec_q.hip:2107-2135): every workgroup makes the Q8_0
+// activation of SiLU(lo[i] scale) (i < n, 0 up to K) in LDS with the tile stager's arithmetic (that of gpu_swiglu
+// with u = 1 and of its quantizer), then the rows as k_matvec computes them from it.
+template <int TYPE, int L>
+__global__ void __launch_bounds__(MV_THREADS) k_matvec_lr(MvArgs a) {
+    __shared__ __attribute__((aligned(16))) int8_t xs[LR_MAXK];
+    __shared__ float xd[LR_MAXK / 32];
+    for (int base = 0; base < a.K; base += MV_THREADS) {  // (a half-wave holds a 32-value block, all in or out)
+        const int i = base + (int)threadIdx.x;
+        const bool active = i < a.K;
+        const float g = active && i < a.lr_n ? a.lr_lo[i] * a.lr_scale : 0.0f, u = 1.0f;
+        float v = 0.0f;
+        if (active) v = g / (1.0f + expf(-g)) * u;
+        const float am = group_max(fabsf(v), 32);
+        const float id0 = am != 0.0f ? 127.0f / am : 0.0f;
+        if (active) {
+            xs[i] = (int8_t)(int)rintf(v * id0);
+            if ((threadIdx.x & 31) == 0) xd[i >> 5] = __half2float(__float2half(am / 127.0f));
+        }
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, gl = lane & (L - 1);
+    const int row = (blockIdx.x * (MV_THREADS / 64) + (threadIdx.x >> 6)) * (64 / L) + lane / L;
+    if (row >= a.Nt) return;
+    Act<1> x;
+    x.q[0] = xs;
+    x.d[0] = xd;
+    x.bs[0] = nullptr;
+    float acc[1];
+    row_sum<TYPE, 1, L>(a.W[0] + (long long)row * a.row_bytes, a.K, gl, x, acc, NoCap{});
+    const float v = group_sum(acc[0], L);
+    if (gl == 0) a.y[0][row] = v * a.osc[0];
+}
+
 // ---------------------------------------------------------------- MoE expert-indexed kernel
 // grid (row groups, n_used * nmat, T): slot j of token t uses expert ids[t * n_used + j] (-1: Wx)
 
@@ -827,6 +861,29 @@ hipError_t launch_matvec(int type, const MvArgs &a, hipStream_t stream) {
     case TY_Q6_K: return launch_nt<TY_Q6_K>(a, stream);
     }
     return hipErrorInvalidDeviceFunction;
+}
+
+template <int L>
+static hipError_t launch_lr_l(const MvArgs &a, hipStream_t stream) {
+    const int rows_per_wg = (MV_THREADS / 64) * (64 / L);
+    hipLaunchKernelGGL((k_matvec_lr<TY_FAST, L>), dim3((unsigned)((a.Nt + rows_per_wg - 1) / rows_per_wg)),
+                       dim3(MV_THREADS), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_matvec_lr(int type, const MvArgs &a, hipStream_t stream) {
+    if (type != TY_FAST || a.T != 1 || !a.lr_lo || a.K > LR_MAXK || a.K % 128) return hipErrorInvalidValue;
+    if (tile_enabled()) {
+        const hipError_t e = launch_matvec_tile_lr(type, a, stream);
+        if (e != hipErrorNotSupported) return e;
+    }
+    switch (a.L) {
+    case 8: return launch_lr_l<8>(a, stream);
+    case 16: return launch_lr_l<16>(a, stream);
+    case 32: return launch_lr_l<32>(a, stream);
+    case 64: return launch_lr_l<64>(a, stream);
+    }
+    return hipErrorInvalidValue;
 }
 
 template <int TYPE, int L>

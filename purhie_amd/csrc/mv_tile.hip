@@ -589,15 +589,24 @@ struct Stager {
 // == 0: a half-wave is all in or all out). issue() loads the first SW_R values of each thread before the weights
 // are issued (as the stager's first loads), commit() the rest, then computes and writes.
 constexpr int SW_R = 4;
+// A null u: the low-rank input instead, g[i] lsc for i < ln and 0 up to K, times u = 1 (SiLU(g lsc)).
 template <int TYPE, int THR>
 struct SwStager {
     float gv[SW_R], uv[SW_R];
+    float lsc = 1.0f;
+    int ln = 0;
+    __device__ __forceinline__ float lr_a(const float *g, int i) const { return i < ln ? g[i] * lsc : 0.0f; }
     __device__ __forceinline__ void issue(const float *g, const float *u, int K) {
 #pragma unroll
         for (int j = 0; j < SW_R; ++j) {
             const int i = j * THR + (int)threadIdx.x, c = i < K ? i : K - 1;  // (clamped, unconditional loads)
-            gv[j] = g[c];
-            uv[j] = u[c];
+            if (u) {
+                gv[j] = g[c];
+                uv[j] = u[c];
+            } else {
+                gv[j] = lr_a(g, c);
+                uv[j] = 1.0f;
+            }
         }
     }
     __device__ __forceinline__ void put(const TileLds<TYPE> &L, uint8_t *smem, int i, bool active, float a,
@@ -620,7 +629,8 @@ struct SwStager {
         }
         for (int base = SW_R * THR; base < K; base += THR) {
             const int i = base + (int)threadIdx.x;
-            put(L, smem, i, i < K, i < K ? g[i] : 0.0f, i < K ? u[i] : 0.0f);
+            if (u) put(L, smem, i, i < K, i < K ? g[i] : 0.0f, i < K ? u[i] : 0.0f);
+            else put(L, smem, i, i < K, i < K ? lr_a(g, i) : 0.0f, 1.0f);
         }
         if constexpr (Tu<TYPE>::LUT)
             for (int e = threadIdx.x; e < 256; e += THR)
@@ -641,7 +651,8 @@ __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int r
                                           const int8_t *q, const float *d, const int32_t *bs,
                                           const float *sg = nullptr, const float *su = nullptr,
                                           int32_t *cap = nullptr, long long cap_ts = 0,
-                                          const Stager<TYPE, NP, THR, SMALL> *pre = nullptr) {
+                                          const Stager<TYPE, NP, THR, SMALL> *pre = nullptr, float lr_scale = 1.0f,
+                                          int lr_n = 0) {
     using P = Tu<TYPE>;
     using TL = TileLds<TYPE>;
     static_assert(!SW || (NT == 1 && P::ACT == 32 && P::SUMS == 0), "SwiGLU staging: one token, Q8_0 activation");
@@ -651,6 +662,8 @@ __device__ __forceinline__ void tile_body(uint8_t *smem, const Rows &rows, int r
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     Stager<TYPE, NP, THR, SMALL> st;
     SwStager<TYPE, THR> sws;
+    sws.lsc = lr_scale;
+    sws.ln = lr_n;
     if constexpr (PRE) st = *pre;
     else if constexpr (SW) sws.issue(sg, su, K);
     else st.issue(L, q, d, bs, K);
@@ -769,7 +782,7 @@ static TileArgs tile_args(int nb, int thr) {
     return ta;
 }
 
-template <int TYPE, int NT, int THR, bool CAP = false, int NP = NT, bool SMALL = false>
+template <int TYPE, int NT, int THR, bool CAP = false, int NP = NT, bool SMALL = false, bool LR = false>
 __global__ void __launch_bounds__(THR) k_mv_tile(MvArgs a, TileArgs ta) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const DenseRows rows{a};
@@ -779,9 +792,14 @@ __global__ void __launch_bounds__(THR) k_mv_tile(MvArgs a, TileArgs ta) {
     const int row0 = rows.base(m) + (bx - first) * ta.R;
     const int end = DenseRows::pick(m, a.bound[0], a.bound[1], a.bound[2], a.bound[3]);
     const int nr = end - row0 < ta.R ? end - row0 : ta.R;
-    tile_body<TYPE, NT, THR, DenseRows, false, CAP, NP, SMALL>(smem, rows, row0, nr, a.K, ta.nb, ta.lg, a.q, a.d, a.bs,
-                                                        nullptr, nullptr, a.cap,
-                                                        (long long)a.Nt * (a.K / cap_group(TYPE)));
+    if constexpr (LR)  // (the low-rank input: SiLU(lo scale) quantized in the stager)
+        tile_body<TYPE, 1, THR, DenseRows, true, false, 1, false, false>(smem, rows, row0, nr, a.K, ta.nb, ta.lg,
+                                                                          nullptr, nullptr, nullptr, a.lr_lo, nullptr,
+                                                                          nullptr, 0, nullptr, a.lr_scale, a.lr_n);
+    else
+        tile_body<TYPE, NT, THR, DenseRows, false, CAP, NP, SMALL>(smem, rows, row0, nr, a.K, ta.nb, ta.lg, a.q, a.d,
+                                                            a.bs, nullptr, nullptr, a.cap,
+                                                            (long long)a.Nt * (a.K / cap_group(TYPE)));
 }
 
 // MoE: grid (tiles, n_used * nmat, T); slot j of token t uses expert ids[t * n_used + j] (-1: Wx). Tiles mode:
@@ -939,6 +957,14 @@ static bool tile_trims(const TileArgs &ta) { return ta.R >= 1 && (ta.R << ta.lg)
 template <int TYPE, int NT, int THR, int NP>
 static hipError_t tile_dense_launch(const MvArgs &a, const TileArgs &ta, int tiles, hipStream_t stream) {
     const size_t lds = (size_t)TileLds<TYPE>(a.K, NP, THR).bytes;
+    if constexpr (NT == 1 && TYPE == TY_FAST) {
+        if (a.lr_lo) {
+            hipLaunchKernelGGL((k_mv_tile<TYPE, 1, THR, false, 1, false, true>), dim3((unsigned)tiles), dim3(THR), lds,
+                               stream, a, ta);
+            return hipGetLastError();
+        }
+    }
+    if (a.lr_lo) return hipErrorNotSupported;
     if constexpr (NT == 1) {
         if (a.K / 16 <= THR && a.K / Tu<TYPE>::ACT <= THR) {  // a thread for every value chunk and scale
             if (a.cap)
@@ -1017,6 +1043,11 @@ static hipError_t tile_dense_t(const MvArgs &a, hipStream_t stream) {
     case 4: return tile_dense<TYPE, 4>(a, stream);
     }
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_matvec_tile_lr(int type, const MvArgs &a, hipStream_t stream) {
+    if (type != TY_FAST || a.T != 1 || !a.lr_lo) return hipErrorNotSupported;
+    return tile_dense<TY_FAST, 1>(a, stream);
 }
 
 hipError_t launch_matvec_tile(int type, const MvArgs &a, hipStream_t stream) {

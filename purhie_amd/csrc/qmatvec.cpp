@@ -233,16 +233,54 @@ hipError_t qmatvec_launch_batch_h(int type, const void *W, size_t row_bytes, con
     }
     return float_rows(type, true, W, row_bytes, x, y, N, K, T, stream);
 }
-int qmatvec_q8_0s_source_supported(int, int) { return 0; }
-hipError_t qmatvec_quantize_rows_q8_0(int, const void *, size_t, int, int, int8_t *, uint16_t *, hipStream_t) {
-    return hipErrorInvalidDeviceFunction;
+// The split-Q8_0 copy of a float matrix (the opt-in LM head, src/qmatvec.cpp:369-390): ggml's Q8_0 quantization
+// per 32 values into qs [N][K] (16-byte aligned) and fp16 d [N][K / 32]; y = qs x on the activation's Q8_0 part
+int qmatvec_q8_0s_source_supported(int type, int K) { return K > 0 && K % 256 == 0 && float_type(type) ? 1 : 0; }
+
+hipError_t qmatvec_quantize_rows_q8_0(int type, const void *W, size_t row_bytes, int N, int K, int8_t *qs, uint16_t *d,
+                                      hipStream_t stream) {
+    if (!qmatvec_q8_0s_source_supported(type, K)) return hipErrorInvalidDeviceFunction;
+    if (row_bytes != qt_row_size(type, K) || !al16(qs) || !W || !d || N < 0) return hipErrorInvalidValue;
+    return launch_quant_rows_q8_0(type, (const uint8_t *)W, (long long)row_bytes, N, K, qs, d, stream);
 }
-hipError_t qmatvec_launch_q8_0s(const int8_t *, const uint16_t *, const qmatvec_q8 *, float *, int, int, hipStream_t) {
-    return hipErrorInvalidDeviceFunction;
+
+hipError_t qmatvec_launch_q8_0s(const int8_t *qs, const uint16_t *d, const qmatvec_q8 *q, float *y, int N, int K,
+                                hipStream_t stream) {
+    if (!q || K <= 0 || K % 256 != 0 || K > q->max_k || !al16(qs) || !d || !y || !q->q0 || !q->d0 || N < 0)
+        return hipErrorInvalidValue;
+    return launch_mv_q8_0s(qs, d, q->q0, q->d0, y, N, K, stream);
 }
-int qmatvec_q8_lr_supported(int, int) { return 0; }
-hipError_t qmatvec_launch_q8_lr(int, const void *, size_t, const float *, int, int, float, float *, int, hipStream_t) {
-    return hipErrorInvalidDeviceFunction;
+// One token of the low-rank up projection (src/qmatvec.cpp:467-479): y = W x, x = SiLU(lo scale) zero-padded from
+// n to K values and quantized to Q8_0 inside the kernel, the bits that SwiGLU(lo scale, 1)'s quantization followed by
+// qmatvec_launch_q8 give (no output scale, as the reference's kernel). ROCmFP4_FAST, K % 128 == 0, K <= 1024.
+int qmatvec_q8_lr_supported(int type, int K) {
+    return type == QT_Q4_0_ROCMFP4_FAST && K > 0 && K % 128 == 0 && K <= LR_MAXK ? 1 : 0;
+}
+
+hipError_t qmatvec_launch_q8_lr(int type, const void *W, size_t row_bytes, const float *lo, int n, int K, float scale,
+                                float *y, int N, hipStream_t stream) {
+    if (!qmatvec_q8_lr_supported(type, K)) return hipErrorInvalidDeviceFunction;
+    if (n < 0 || n > K || row_bytes != qt_row_size(type, K) || row_bytes % 4 != 0 || ((uintptr_t)W & 3) != 0 || !W ||
+        !y || (n > 0 && !lo) || N < 0)
+        return hipErrorInvalidValue;
+    if (N == 0) return hipSuccess;
+    MvArgs a{};
+    for (int i = 0; i < 4; ++i) {
+        a.W[i] = (const uint8_t *)W;
+        a.y[i] = y;
+        a.bound[i] = N;
+        a.ystride[i] = N;
+        a.osc[i] = 1.0f;
+    }
+    a.row_bytes = (long long)row_bytes;
+    a.Nt = N;
+    a.K = K;
+    a.T = 1;
+    a.L = matvec_lanes(type, K, N);
+    a.lr_lo = lo ? lo : y;  // (n == 0: never read)
+    a.lr_n = n;
+    a.lr_scale = scale;
+    return launch_matvec_lr(type, a, stream);
 }
 // Float expert-indexed matvecs: for token t and slot j, expert e = ids[t n_used + j] (rows e N .. e N + N - 1 of W)
 // times input row t (x_per_slot 0) or t n_used + j into output row t n_used + j; an id below 0 writes nothing.

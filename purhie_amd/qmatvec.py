@@ -99,6 +99,11 @@ def lib():
             "qmatvec_launch": (i32, [i32, vp, sz, vp, vp, i32, i32, vp]),
             "qmatvec_launch_id": (i32, [i32, vp, sz, vp, i32, i32, vp, vp, i32, i32, i32, vp]),
             "qmatvec_id_batch_f_supported": (i32, [i32]),
+            "qmatvec_q8_0s_source_supported": (i32, [i32, i32]),
+            "qmatvec_quantize_rows_q8_0": (i32, [i32, vp, sz, i32, i32, vp, vp, vp]),
+            "qmatvec_launch_q8_0s": (i32, [vp, vp, pq8, vp, i32, i32, vp]),
+            "qmatvec_q8_lr_supported": (i32, [i32, i32]),
+            "qmatvec_launch_q8_lr": (i32, [i32, vp, sz, vp, i32, i32, C.c_float, vp, i32, vp]),
             "qmatvec_launch_id_batch_f": (i32, [i32, vp, sz, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp]),
             "qmatvec_launch_bf16f": (i32, [vp, sz, vp, vp, i32, i32, i32, vp]),
             "qmatvec_launch_batch": (i32, [i32, vp, sz, vp, vp, i32, i32, i32, vp]),

@@ -140,20 +140,25 @@ def test_library_exports_the_reference_surface():
 
 
 def test_float_path_entries_report_unsupported():
-    """the float-activation entries answer as the reference does for a missing kernel (*_supported 0, launches
-    hipErrorInvalidDeviceFunction, 98, without touching their pointers) for types outside this path (Q4_0, 2), and
-    report support for this path's quantized types"""
+    """the float-activation, split-Q8_0 and low-rank entries answer as the reference does for a missing kernel
+    (*_supported 0, launches hipErrorInvalidDeviceFunction, 98, without touching their pointers) for types and shapes
+    outside this path (Q4_0, 2; the low-rank entry's ROCmFP4_FAST-only K % 128 <= 1024), and report support for the
+    rest"""
     lib = C.CDLL(LIB)
     assert lib.qmatvec_supported(2) == 0
     assert [lib.qmatvec_supported(t) for t in (0, 1, 30, 8, 12, 13, 14, 23, 39, 40, 100, 101)] == [1] * 12
     assert [lib.qmatvec_id_batch_f_supported(t) for t in (0, 1, 30, 8, 12, 100)] == [1] * 6
     assert lib.qmatvec_half_supported(1, None, C.c_size_t(0), 64, 256, 64) == 0
-    assert lib.qmatvec_q8_0s_source_supported(0, 256) == 0
-    assert lib.qmatvec_q8_lr_supported(12, 256) == 0
+    assert [lib.qmatvec_q8_0s_source_supported(t, 256) for t in (0, 1, 30, 8)] == [1, 1, 1, 0]
+    assert lib.qmatvec_q8_0s_source_supported(0, 320) == 0
+    assert [lib.qmatvec_q8_lr_supported(t, 384) for t in (101, 100, 12)] == [1, 0, 0]
+    assert lib.qmatvec_q8_lr_supported(101, 1152) == 0
     assert lib.qmatvec_id_batch_f_supported(2) == 0
     assert lib.qmatvec_launch(2, None, C.c_size_t(0), None, None, 64, 256, None) == 98
     assert lib.qmatvec_launch_batch(2, None, C.c_size_t(0), None, None, 64, 256, 4, None) == 98
     assert lib.qmatvec_launch_id(2, None, C.c_size_t(0), None, 8, 0, None, None, 64, 256, 1, None) == 98
+    assert lib.qmatvec_quantize_rows_q8_0(8, None, C.c_size_t(0), 4, 256, None, None, None) == 98
+    assert lib.qmatvec_launch_q8_lr(100, None, C.c_size_t(0), None, 4, 384, C.c_float(1.0), None, 4, None) == 98
 
 
 def test_fp8_e4m3_decoder(oracle):
