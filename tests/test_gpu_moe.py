@@ -109,14 +109,23 @@ def test_group(M, oracle, T, n_used, E, tile):
     assert np.array_equal(got["tok_rows"], got["pair_rows"] // n_used)
 
 
-@pytest.mark.parametrize("n", [768, 2048, 4096, 96])
+@pytest.mark.parametrize("n", [768, 2048, 4096, 96, 4096 * 256, 4097 * 256 - 160, 100])
 def test_swiglu_fused_quantize(M, oracle, n):
+    """gpu_swiglu with both activation formats against the oracle; n from one block to past 4096 blocks (the
+    wave-per-block kernel, four blocks a wave, with a ragged last block); n = 100 (n % 32 != 0) is the
+    workgroup-per-block kernel's, with its Q8_0 refused"""
     import torch
     from purhie_amd import qmatvec as Q
     g = synth.gaussian(980 + n, n) * 3.0
     u = synth.gaussian(981 + n, n)
     out = torch.zeros(n, dtype=torch.float32, device="cuda")
     q = Q.Q8(((n + 255) // 256) * 256)
+    if n % 32:
+        with pytest.raises(Q.HipError):
+            M.swiglu(dev(g), dev(u), out, n, q)
+        M.swiglu(dev(g), dev(u), out, n)
+        assert np.allclose(host(out), oracle.swiglu(g, u), rtol=1e-6, atol=1e-30)
+        return
     M.swiglu(dev(g), dev(u), out, n, q)
     got = host(out)
     assert np.allclose(got, oracle.swiglu(g, u), rtol=1e-6, atol=1e-30)
@@ -133,6 +142,17 @@ def test_swiglu_fused_quantize(M, oracle, n):
     out2 = torch.zeros(n, dtype=torch.float32, device="cuda")
     M.swiglu(dev(g), dev(u), out2, n)  # without quantization: the same values
     assert np.array_equal(host(out2).view(np.uint32), got.view(np.uint32))
+    # buffers one float off 16-byte alignment go to the workgroup-per-block kernel: the same bits
+    gb, ub = torch.zeros(n + 1, dtype=torch.float32, device="cuda"), torch.zeros(n + 1, dtype=torch.float32, device="cuda")
+    gb[1:] = dev(g)
+    ub[1:] = dev(u)
+    out3 = torch.zeros(n + 1, dtype=torch.float32, device="cuda")
+    q3 = Q.Q8(((n + 255) // 256) * 256)
+    M.swiglu(gb[1:], ub[1:], out3[1:], n, q3)
+    assert np.array_equal(host(out3[1:]).view(np.uint32), got.view(np.uint32))
+    v3 = {k: host(t) for k, t in q3.views(n).items()}
+    for k in v:
+        assert np.array_equal(v3[k].view(np.uint8), v[k].view(np.uint8)), k
 
 
 @pytest.mark.parametrize("n,T", [(2560, 1), (5120, 3), (2048, 16), (1024, 40), (9728, 9)])
