@@ -257,6 +257,10 @@ __global__ void __launch_bounds__(256) k_moe_router(const float *__restrict__ lo
                 n, ids_stride, s);
 }
 
+// Up to CB slots' values of an output are loaded together before the add chain (slots past n_used load slot
+// n_used - 1 again, unused), the rest one after another.
+constexpr int CB = 8;
+
 __global__ void __launch_bounds__(256) k_moe_combine(const float *__restrict__ down, const float *__restrict__ wts,
                                                      const float *__restrict__ shared, const float *__restrict__ sg,
                                                      const int *__restrict__ ids, const float *__restrict__ es,
@@ -265,23 +269,31 @@ __global__ void __launch_bounds__(256) k_moe_combine(const float *__restrict__ d
     const int t = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const float *d = down + (long long)t * n_used * n + i;
+    float dv[CB];
+#pragma unroll
+    for (int j = 0; j < CB; ++j) dv[j] = d[(long long)(j < n_used ? j : n_used - 1) * n];
+    const float s = shared ? shared[(long long)t * n + i] : 0.0f;
+    auto dj = [&](int j) { return j < CB ? dv[j] : d[(long long)j * n]; };
     float acc;
     if (!wts) {  // (uniform) weight 1
-        acc = d[0];
-        for (int j = 1; j < n_used; ++j) acc = acc + d[(long long)j * n];
+        acc = dv[0];
+#pragma unroll
+        for (int j = 1; j < CB; ++j)
+            if (j < n_used) acc = acc + dv[j];
+        for (int j = CB; j < n_used; ++j) acc = acc + d[(long long)j * n];
     } else {
         const float *w = wts + (long long)t * n_used;
         const int *e = ids + (long long)t * n_used;
-        acc = es ? (d[0] * es[e[0]]) * w[0] : w[0] * d[0];
-        for (int j = 1; j < n_used; ++j) {
-            const float dj = d[(long long)j * n];
-            acc = acc + (es ? (dj * es[e[j]]) * w[j] : w[j] * dj);
+        acc = es ? (dv[0] * es[e[0]]) * w[0] : w[0] * dv[0];
+#pragma unroll
+        for (int j = 1; j < CB; ++j)
+            if (j < n_used) acc = acc + (es ? (dv[j] * es[e[j]]) * w[j] : w[j] * dv[j]);
+        for (int j = CB; j < n_used; ++j) {
+            const float v = dj(j);
+            acc = acc + (es ? (v * es[e[j]]) * w[j] : w[j] * v);
         }
     }
-    if (shared) {
-        const float s = shared[(long long)t * n + i];
-        acc = acc + (sg ? s * sg[t] : s);
-    }
+    if (shared) acc = acc + (sg ? s * sg[t] : s);
     out[(long long)t * n + i] = acc;
 }
 
