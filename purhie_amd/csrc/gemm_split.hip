@@ -377,7 +377,16 @@ __global__ void __launch_bounds__(256, ROWS == SP_ROWS_SMALL ? 3 : 2) k_gemm_spl
     {
         const float *drow = a.dx + xrow * nb;
         float m = 0.0f;
-        for (int b = xp; b < nb; b += TPR) m = fmaxf(m, drow[b]);
+        // sixteen loads in flight at a time (a loop of one load each waited for every load before it: the dense
+        // 128-token tiles' 80 scales a thread were 80 memory round trips)
+        constexpr int ML = 16;
+        for (int b0 = xp; b0 < nb; b0 += ML * TPR) {
+            float v[ML];
+#pragma unroll
+            for (int k = 0; k < ML; ++k) v[k] = b0 + k * TPR < nb ? drow[b0 + k * TPR] : 0.0f;
+#pragma unroll
+            for (int k = 0; k < ML; ++k) m = fmaxf(m, v[k]);
+        }
 #pragma unroll
         for (int o = 1; o < TPR; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
         int ex = 0;
