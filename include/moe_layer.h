@@ -6,7 +6,8 @@
  *     as slot n_used (id -1) of the experts' launches (gate / up, SwiGLU, down in 3 launches instead of 6; the
  *     same arithmetic per row, the shared output added last by the combine);
  *   - 8 tokens or more: the (token, slot) entries grouped by expert for the expert-tiled GEMMs, at the largest
- *     tile all three expert matrices take (qmatvec_id_batch_tile);
+ *     tile all three expert matrices take (qmatvec_id_batch_tile), but at most 64 entries where the experts' mean
+ *     entry count m (T n_used / n_expert) is at most 56 or fills fewer 64-entry than 128-entry slots;
  *   - otherwise the expert-indexed matvecs, token by token in the decode order (gate / up as one pair launch,
  *     down with x_per_slot; for a Q8_0-activation down type the SwiGLU and its quantization run inside the down
  *     launch, qmatvec_launch_q8_id_swiglu, with the same bits);

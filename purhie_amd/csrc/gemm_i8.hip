@@ -752,6 +752,13 @@ int gemm_cap_unit(int type) {
 
 int gemm_i8kq_token_tile(bool moe) { return moe ? I8Geo<1, 2>::BT : I8Geo<2, 2>::BT; }
 
+// the largest expert tile: the K-quants' planes cost vector work per tile (each tile builds its expert's planes), so
+// their tiles go up to the dense 128 tokens (the launch takes the 64-token form for tiles of at most 64); Q8_0 and
+// MXFP4 stage their weights as they are and keep 64
+int gemm_i8_moe_tile(int type) {
+    return type == TY_Q8_0 || type == TY_MXFP4 ? I8Geo<1, 2>::BT : I8Geo<2, 2>::BT;
+}
+
 int gemm_i8kq_rows() { return I8_N; }
 
 template <int TYPE, int WI, int WT, bool MOE, bool CAP>
@@ -775,6 +782,9 @@ static hipError_t launch_i8kq_t(const GemmArgs &a, dim3 grid, hipStream_t stream
 
 template <int TYPE>
 static hipError_t launch_i8kq_type(const GemmArgs &a, dim3 grid, hipStream_t stream) {
+    if (a.n_tiles && a.tt > I8Geo<1, 2>::BT)  // expert tiles of up to 128 entries
+        return a.cap ? launch_i8kq_t<TYPE, 2, 2, true, true>(a, grid, stream)
+                     : launch_i8kq_t<TYPE, 2, 2, true, false>(a, grid, stream);
     if (a.n_tiles)
         return a.cap ? launch_i8kq_t<TYPE, 1, 2, true, true>(a, grid, stream)
                      : launch_i8kq_t<TYPE, 1, 2, true, false>(a, grid, stream);

@@ -124,7 +124,8 @@ struct GemmArgs {
     int8_t *hq;
     float *hd;
     int32_t *hs;
-    int tt;                 // split GEMM, dense: tokens per workgroup (gemm_split_token_tile)
+    int tt;                 // split GEMM, dense: tokens per workgroup (gemm_split_token_tile); int8 GEMMs, MoE: the
+                            // caller's tile (at most 64: the 64-token form)
     // capture mode (null: off; the integer-exact GEMMs): the exact integer each epilogue scales, per token (dense:
     // t; tiles: the entry's output row) and weight row: cap[(t * N + row) * (K / U) + unit], U = gemm_cap_unit(type)
     int32_t *cap;
@@ -212,6 +213,7 @@ hipError_t launch_mv_q8_0s(const int8_t *qs, const uint16_t *d, const int8_t *q8
 // gemm_i8kq_rows()), MoE grid (rows / gemm_i8kq_rows(), tiles) with tiles of up to gemm_i8kq_token_tile(true) entries
 bool gemm_i8kq_supported(int type);
 int gemm_i8kq_token_tile(bool moe);
+int gemm_i8_moe_tile(int type);  // the largest expert tile of the int8 GEMMs (GemmArgs::tt: the caller's tile)
 int gemm_i8kq_rows();  // weight rows per workgroup
 hipError_t launch_gemm_i8kq(int type, const GemmArgs &a, dim3 grid, hipStream_t stream);
 

@@ -7,6 +7,7 @@
 #include "../../include/quant_types.h"
 
 #include <algorithm>
+#include <cmath>
 #include <mutex>
 
 // purhie_moe_ffn_noalloc's workspace: one static device array on each GPU the library runs on (the runtime places it
@@ -75,6 +76,13 @@ Layout layout(const purhie_moe_weights *w, int T, char *base) {
     L.ns = L.slot ? NU + 1 : NU;
     if (L.grouped) {
         L.tile = std::min({qmatvec_id_batch_tile(w->type_gate_up, FE, E), qmatvec_id_batch_tile(w->type_down, E, FE)});
+        // 128-entry tiles build each expert's weight planes half as often as 64-entry ones: they win where an
+        // expert's mean entry count m fills as many 128-slots as 64-slots (m in (56, 128], (192, 256], ...: config 5's
+        // 76 entries 1570 -> 1481 us) and lose where they pad more (config 4's mixed-quant 152 entries: 699 -> 751 us)
+        if (L.tile > 64) {
+            const double m = (double)T * NU / NE;
+            if (m <= 56.0 || std::ceil(m / 128.0) * 128.0 > std::ceil(m / 64.0) * 64.0) L.tile = 64;
+        }
         L.max_tiles = gpu_moe_max_tiles(T, NU, NE, L.tile);
     }
     L.qx_k = (int)round256((long long)T * L.ns * FE);

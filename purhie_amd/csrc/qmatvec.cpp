@@ -595,16 +595,17 @@ static bool id_gemm_ok(int type, int N, int K) {
 // entries; the decode-order path takes the reference's 16 (src/qmatvec.cpp:612-615)
 int qmatvec_id_batch_tile(int type, int N, int K) {
     if (!id_gemm_ok(type, N, K)) return ID_DECODE_TILE;
-    return gemm_split(type) ? gemm_split_token_tile(true, 0) : gemm_i8kq_token_tile(true);
+    return gemm_split(type) ? gemm_split_token_tile(true, 0) : gemm_i8_moe_tile(type);
 }
 
 // the expert-tiled GEMM over W (and W2, the pair's second matrix, or null), the activation read in place: input
 // rows are in_rows[] of q
 static hipError_t id_gemm(int type, const void *W, const void *W2, size_t row_bytes, const qmatvec_q8 *q, float *y,
-                          float *y2, int N, int K, int max_tiles, const int32_t *n_tiles, const int32_t *tile_e,
-                          const int32_t *tile_start, const int32_t *tile_n, const int32_t *in_rows,
-                          const int32_t *out_rows, hipStream_t stream) {
+                          float *y2, int N, int K, int max_tiles, int tile, const int32_t *n_tiles,
+                          const int32_t *tile_e, const int32_t *tile_start, const int32_t *tile_n,
+                          const int32_t *in_rows, const int32_t *out_rows, hipStream_t stream) {
     GemmArgs a = gemm_args(type, W, row_bytes, q, y, N, K);
+    a.tt = tile;
     a.n_tiles = n_tiles;
     a.tile_e = tile_e;
     a.tile_start = tile_start;
@@ -663,8 +664,8 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
         a.cap_rows = 0;
         return launch_matvec_id(type, a, stream);
     }
-    return id_gemm(type, W, nullptr, row_bytes, q, y, nullptr, N, K, max_tiles, n_tiles, tile_e, tile_start, tile_n,
-                   in_rows, out_rows, stream);
+    return id_gemm(type, W, nullptr, row_bytes, q, y, nullptr, N, K, max_tiles, tile, n_tiles, tile_e, tile_start,
+                   tile_n, in_rows, out_rows, stream);
 }
 
 // the gate and up projections of the experts over the same tiles in one expert-tiled GEMM launch (no counterpart in
@@ -685,7 +686,7 @@ hipError_t qmatvec_launch_q8_id_batch_pair(int type, const void *W, const void *
                                : qmatvec_launch_q8_id_batch(type, W2, row_bytes, q, y2, N, K, max_tiles, tile, n_tiles,
                                                             tile_e, tile_start, tile_n, in_rows, out_rows, stream);
     }
-    return id_gemm(type, W, W2, row_bytes, q, y, y2, N, K, max_tiles, n_tiles, tile_e, tile_start, tile_n, in_rows,
+    return id_gemm(type, W, W2, row_bytes, q, y, y2, N, K, max_tiles, tile, n_tiles, tile_e, tile_start, tile_n, in_rows,
                    out_rows, stream);
 }
 

@@ -217,6 +217,36 @@ def test_kquant_gemm_isum(Q, oracle, t, N, K, T):
         assert np.array_equal(got[i], oracle.unit_isum(t, W, N, K, a["q"], a["bs"])), f"token {i}"
 
 
+@pytest.mark.parametrize("t,N,K", [(12, 768, 2048), (14, 2048, 768)])
+@pytest.mark.parametrize("tile", [128, 64])
+def test_kquant_expert_gemm_isum(Q, oracle, t, N, K, tile):
+    """the K-quant expert-tiled GEMM's per-super-block integers at both launch forms (128- and 64-entry tiles; the
+    mixed-quant MoE's gate and down shapes), per entry's output row"""
+    import ctypes as C
+    import torch
+    E, n_used, T = 4, 4, 100
+    W = rand_rows(Q, t, E * N, K, 71 + t)
+    ids = (synth.splitmix64(72, T * n_used) % np.uint64(E)).astype(np.int32).reshape(T, n_used)
+    x = acts(73, T, K)
+    q = quantized(Q, x)
+    g = oracle.moe_group(ids, E, tile)
+    p = lambda a: C.c_void_p(a.data_ptr())
+    bufs = [dev(np.array([g["n_tiles"]], np.int32)), dev(g["tile_e"]), dev(g["tile_start"]), dev(g["tile_n"]),
+            dev(g["tok_rows"]), dev(g["pair_rows"])]
+    cap = cap_buf(T * n_used * N * (K // 256))
+    y = torch.zeros((T * n_used, N), device="cuda")
+    with Q.capture(cap):
+        assert Q.lib().qmatvec_launch_q8_id_batch(t, p(dev(W)), Q.row_size(t, K), q.ref, p(y), N, K,
+                                                  g["n_tiles"] + 1, tile, *[p(b) for b in bufs], None) == 0
+    got = host(cap).reshape(T * n_used, N, K // 256)
+    rb = W.shape[1]
+    for tt in range(0, T, 9):
+        a = oracle.quantize_act(x[tt], True)
+        for j in range(n_used):
+            rows = W.reshape(E, N, rb)[ids[tt, j]]
+            assert np.array_equal(got[tt * n_used + j], oracle.unit_isum(t, rows, N, K, a["q"], a["bs"])), (tt, j)
+
+
 def test_capture_units(Q):
     """the group each decode capture holds is the weight scale's; the GEMMs' units: a K-quant super-block, a Q8_0 /
     MXFP4 block, and none for the split GEMM of ROCmFP4 / FAST / NVFP4 (exact fp16 operands chained through K)"""

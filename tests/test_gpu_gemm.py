@@ -121,6 +121,44 @@ def test_moe_tiled_gemm(Q, oracle, t, N, K):
             parity.check(f"expert-tiled GEMM {Q.NAMES[t]}", got[tt * n_used + j], want, mag, ref, TOL)
 
 
+@pytest.mark.parametrize("t,N,K", [(12, 768, 2048), (14, 2048, 768), (13, 256, 1024), (23, 512, 1024)])
+def test_moe_tiled_gemm_kquant_tiles(Q, oracle, t, N, K):
+    """the K-quant expert GEMM's 128-entry tiles (the launch's 128-token form, experts of ~150 entries: a full tile
+    and a partial one each) against 64-entry tiles (the 64-token form) and 16-entry ones: every entry's output bit for
+    bit the same (the same per-super-block integers and epilogue order), and within 1e-5 sum |w x| of the oracle"""
+    import ctypes as C
+    import torch
+    L = Q.lib()
+    assert L.qmatvec_id_batch_tile(t, N, K) == 128
+    E, n_used, T = 4, 4, 150
+    W = oracle.quantize(t, synth.gaussian(90 + t, E * N * K, 0, 0.02).reshape(E * N, K))
+    Wd = dev(W)
+    ids = (synth.splitmix64(91, T * n_used) % np.uint64(E)).astype(np.int32).reshape(T, n_used)
+    x = acts(92, T, K)
+    q = Q.Q8(((T * K + 255) // 256) * 256)
+    Q.quantize(dev(x.reshape(-1)), T * K, q)
+    p = lambda a: C.c_void_p(a.data_ptr())
+    outs = {}
+    for tile in (128, 64, 16):
+        g = oracle.moe_group(ids, E, tile)
+        bufs = [dev(np.array([g["n_tiles"]], np.int32)), dev(g["tile_e"]), dev(g["tile_start"]), dev(g["tile_n"]),
+                dev(g["tok_rows"]), dev(g["pair_rows"])]
+        y = torch.full((T * n_used, N), float("nan"), dtype=torch.float32, device="cuda")
+        assert L.qmatvec_launch_q8_id_batch(t, p(Wd), Q.row_size(t, K), q.ref, p(y), N, K, g["n_tiles"] + 1, tile,
+                                            *[p(b) for b in bufs], None) == 0
+        outs[tile] = host(y)
+    assert np.isfinite(outs[128]).all()
+    for tile in (64, 16):
+        assert np.array_equal(outs[128].view(np.uint32), outs[tile].view(np.uint32)), tile
+    rb = W.shape[1]
+    for tt in range(0, T, 7):
+        a = oracle.quantize_act(x[tt], True)
+        for j in range(n_used):
+            want, ref, mag = oracle.matvec(t, W.reshape(E, N, rb)[ids[tt, j]], N, K, a)
+            parity.check(f"expert-tiled GEMM (128-entry tiles) {Q.NAMES[t]}", outs[128][tt * n_used + j], want, mag,
+                         ref, TOL)
+
+
 @pytest.mark.parametrize("t,N,K", [(100, 768, 2048), (101, 256, 1024), (40, 768, 2048), (8, 512, 1024),
                                    (39, 256, 1024), (12, 768, 2048), (13, 512, 1024), (14, 256, 768),
                                    (23, 512, 1024), (100, 200, 512)])
