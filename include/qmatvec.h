@@ -194,7 +194,9 @@ hipError_t qmatvec_launch_q8_id_swiglu(int type, const void *W, const void *Wx, 
                                        hipStream_t stream);
 
 /* replaces src/qmatvec.h:189-195: MoE prefill over gpu_moe_group's expert tiles (tile k: expert
- * tile_e[k], entries tile_start[k] .. + tile_n[k] - 1 of in_rows / out_rows) */
+ * tile_e[k], entries tile_start[k] .. + tile_n[k] - 1 of in_rows / out_rows). qmatvec_id_batch_tile is the largest
+ * tile a launch takes: 64 for the FP4 family, Q8_0 and MXFP4, 128 for the K-quants (any smaller tile works, with
+ * the same bits). */
 int qmatvec_id_batch_tile(int type, int N, int K);
 int qmatvec_q8_id_batch_supported(int type, int K);
 hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y, int N,
