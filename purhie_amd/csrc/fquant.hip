@@ -212,8 +212,8 @@ struct Grp<TY_IQ4_XS> {  // sub-block g & 7: (d (ls - 32)) level (src/quant_type
         const float dl = hd.half(0) * (float)iq4xs_scale(hd.r[0] >> 16, hd.r[1], g & 7);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            i8x4((uint32_t)iq4nl4(q.r[k] & 0x0f0f0f0fu), dl, w + 4 * k);
-            i8x4((uint32_t)iq4nl4((q.r[k] >> 4) & 0x0f0f0f0fu), dl, w + 16 + 4 * k);
+            i8x4((uint32_t)iq4nl4_lo(q.r[k]), dl, w + 4 * k);
+            i8x4((uint32_t)iq4nl4_hi(q.r[k]), dl, w + 16 + 4 * k);
         }
     }
 };

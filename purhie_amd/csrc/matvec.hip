@@ -442,8 +442,8 @@ struct Mv<TY_IQ4_XS> {
         int lo[4], hi[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            lo[k] = iq4nl4(r.q[k] & 0x0f0f0f0fu);
-            hi[k] = iq4nl4((r.q[k] >> 4) & 0x0f0f0f0fu);
+            lo[k] = iq4nl4_lo(r.q[k]);
+            hi[k] = iq4nl4_hi(r.q[k]);
         }
         const int ls = iq4xs_scale(r.h0 >> 16, r.h1, o.s);
         const float dw = h2f(r.h0 & 0xffffu);

@@ -324,8 +324,8 @@ struct Tu<TY_IQ4_XS> {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const uint32_t q = w[2 + 4 * j + k];
-                lo[k] = iq4nl4(q & 0x0f0f0f0fu);
-                hi[k] = iq4nl4((q >> 4) & 0x0f0f0f0fu);
+                lo[k] = iq4nl4_lo(q);
+                hi[k] = iq4nl4_hi(q);
             }
             const int ls = iq4xs_scale(sh, sl, j);
 #pragma unroll
