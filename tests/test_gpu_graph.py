@@ -1,6 +1,6 @@
-"""The launch paths allocate nothing: config 3's ROCmFP4 prefill GEMM (qmatvec_launch_q8_batch) and a 24-token MoE
-FFN at config 4's sizes (purhie_moe_ffn: ROCmFP4 experts, and the mixed Q4_K gate / up, Q6_K down form) are
-captured into a HIP graph whose nodes are all kernel launches (no memory alloc / free, memset or copy nodes), and
+"""The launch paths allocate nothing: config 3's ROCmFP4 prefill GEMM (qmatvec_launch_q8_batch), a 24-token MoE
+FFN at config 4's sizes (purhie_moe_ffn: ROCmFP4 experts, and the mixed Q4_K gate / up, Q6_K down form), and the
+float-activation, LM-head, low-rank and SwiGLU entries are captured into a HIP graph whose nodes are all kernel launches (no memory alloc / free, memset or copy nodes), and
 every replay of the graph, with eager work and synchronisations between replays, gives the eager call's bits."""
 import ctypes as C
 
@@ -160,3 +160,70 @@ def test_config4_moe_ffn_graph(hip, Q, M, t_gu, t_d):
     assert np.isfinite(want).all() and np.abs(want).max() > 0
     G = Captured(hip, calls)
     replays_match(G, out, want, lambda: M.ffn(w, xd, q, T, out, ws))
+
+
+def test_decode_side_entries_graph(hip, Q, M):
+    """the float-activation matvec and batch over Q4_K (qmatvec_launch, _batch), the expert-indexed float matvec
+    (qmatvec_launch_id), the split-Q8_0 LM head (qmatvec_quantize_rows_q8_0, qmatvec_launch_q8_0s), the low-rank
+    matvec (qmatvec_launch_q8_lr) and gpu_swiglu with its quantizer, in one graph of kernel nodes whose replays give
+    the eager bits"""
+    import torch
+    L = Q.lib()
+    p = lambda t: C.c_void_p(t.data_ptr())
+    N, K, T, E, NU = 1024, 2048, 3, 4, 2
+    Wq = encoded(Q, 12, N, K, 21)
+    We = encoded(Q, 12, E * N, K, 22)
+    Wf = (synth.gaussian_torch(torch, 23, N * K, 0.0, 0.02).reshape(N, K)).to(torch.bfloat16).view(torch.uint8)
+    Wl = encoded(Q, 101, N, 384, 24)
+    x = dev(synth.gaussian(25, T * K).reshape(T, K))
+    ids = dev(np.array([[1, 3], [0, 0], [2, -1]], np.int32))
+    lo = dev(synth.gaussian(26, 320))
+    g = dev(synth.gaussian(27, 8 * 256) * 3.0)
+    u = dev(synth.gaussian(28, 8 * 256))
+    q = Q.Q8(K)
+    Q.quantize(x[0], K, q)
+    qs = torch.empty(N * K, dtype=torch.int8, device="cuda")
+    d = torch.empty(N * K // 32, dtype=torch.int16, device="cuda")
+    qa = Q.Q8(8 * 256)
+    outs = [torch.empty(N, device="cuda"), torch.empty((T, N), device="cuda"), torch.empty((T * NU, N), device="cuda"),
+            torch.empty(N, device="cuda"), torch.empty(N, device="cuda"), torch.empty(8 * 256, device="cuda")]
+    for o in outs:
+        o.fill_(float("nan"))  # (the id -1 slot's row is never written)
+
+    def calls(stream=None):
+        assert L.qmatvec_launch(12, p(Wq), Wq.shape[1], p(x), p(outs[0]), N, K, stream) == 0
+        assert L.qmatvec_launch_batch(12, p(Wq), Wq.shape[1], p(x), p(outs[1]), N, K, T, stream) == 0
+        assert L.qmatvec_launch_id(12, p(We), We.shape[1], p(ids), NU, 0, p(x), p(outs[2]), N, K, T, stream) == 0
+        assert L.qmatvec_quantize_rows_q8_0(30, p(Wf), 2 * K, N, K, p(qs), p(d), stream) == 0
+        assert L.qmatvec_launch_q8_0s(p(qs), p(d), q.ref, p(outs[3]), N, K, stream) == 0
+        assert L.qmatvec_launch_q8_lr(101, p(Wl), Wl.shape[1], p(lo), 320, 384, C.c_float(0.5), p(outs[4]), N,
+                                      stream) == 0
+        M.swiglu(g, u, outs[5], 8 * 256, qa, stream)
+
+    def snapshot():
+        torch.cuda.synchronize()
+        return [o.cpu().numpy().copy() for o in outs] + [qa.mem.cpu().numpy().copy()]
+
+    calls()
+    want = snapshot()
+    assert all(np.isfinite(want[i]).all() for i in (0, 1, 3, 4, 5))
+    assert np.isfinite(np.delete(want[2], 2 * NU + 1, axis=0)).all() and np.isnan(want[2][2 * NU + 1]).all()
+    G = Captured(hip, calls)
+    try:
+        assert G.types and all(t == NODE_KERNEL for t in G.types), f"graph node types {sorted(set(G.types))}"
+        for r in range(3):
+            for o in outs:
+                o.fill_(float("nan"))
+            qa.mem.fill_(0x55)
+            calls()  # the program's own eager work between replays
+            torch.cuda.synchronize()
+            for o in outs:
+                o.fill_(float("nan"))
+            qa.mem.fill_(0x55)
+            torch.cuda.synchronize()
+            G.replay()
+            got = snapshot()
+            for i, (a, b) in enumerate(zip(got, want)):
+                assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"replay {r}, output {i}"
+    finally:
+        G.close()
