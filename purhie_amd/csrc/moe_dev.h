@@ -120,6 +120,86 @@ __device__ __forceinline__ void route_token_128(const float *__restrict__ l, con
     }
 }
 
+// 129 to 256 experts and at most RT_ROUNDS of them used: every wave holds all the logits (experts lane + 64 j, j < 4)
+// and computes the softmax with wave reductions, as the 128-expert form; then n_used rounds of argmax over the
+// experts' 64-bit keys, each a wave-wide maximum by DPP and scalar reads (the keys are distinct, so the maximum is
+// one expert, which its lane then drops). No LDS but the results and no barrier but the last one; the ranks of the
+// general form took each thread 128 LDS reads and 256 64-bit comparisons (config 5's 256-expert router, 2427 tokens:
+// ~28 us). The same selection (descending, equal probabilities: the lower expert) and the weight sum in slot order.
+constexpr int RT_ROUNDS = 16;
+
+// the larger of two keys given as (hi, lo) words
+__device__ __forceinline__ void key_take(uint32_t &bh, uint32_t &bl, uint32_t oh, uint32_t ol) {
+    const bool t = oh > bh || (oh == bh && ol > bl);
+    bh = t ? oh : bh;
+    bl = t ? ol : bl;
+}
+template <int CTRL>
+__device__ __forceinline__ void key_dpp(uint32_t &bh, uint32_t &bl) {
+    key_take(bh, bl, (uint32_t)dpp_i<CTRL>((int)bh), (uint32_t)dpp_i<CTRL>((int)bl));
+}
+
+template <int PER>
+__device__ __forceinline__ void route_token_256(const float *__restrict__ l, const float *__restrict__ x,
+                                                const float *__restrict__ w_sh, int *__restrict__ ids,
+                                                float *__restrict__ wts, float *__restrict__ sg, int n_expert,
+                                                int n_used, int n, int ids_stride, RouterLds<PER> &s) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = lane + 64 * j < n_expert ? l[lane + 64 * j] : -INFINITY;
+    float dsum = 0.0f;
+    if (w_sh) {  // (uniform)
+        for (int i = tid; i < n; i += 256) dsum = fmaf(x[i], w_sh[i], dsum);
+    }
+    const float mx = group_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])), 64);
+    float e[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) e[j] = lane + 64 * j < n_expert ? expf(v[j] - mx) : 0.0f;
+    const float inv = 1.0f / group_sum((e[0] + e[1]) + (e[2] + e[3]), 64);
+    uint32_t kh[4], kl[4];  // a missing expert's key is 0: below every real key
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const bool h = lane + 64 * j < n_expert;
+        const unsigned long long k = route_key(e[j] * inv, lane + 64 * j);
+        kh[j] = h ? (uint32_t)(k >> 32) : 0u;
+        kl[j] = h ? (uint32_t)k : 0u;
+    }
+    float ws = 0.0f;
+    for (int r = 0; r < n_used; ++r) {  // (uniform)
+        uint32_t bh = kh[0], bl = kl[0];
+#pragma unroll
+        for (int j = 1; j < 4; ++j) key_take(bh, bl, kh[j], kl[j]);
+        key_dpp<DPP_PAIR>(bh, bl);
+        key_dpp<DPP_QHALF>(bh, bl);
+        key_dpp<DPP_HALF_MIRROR>(bh, bl);
+        key_dpp<DPP_MIRROR>(bh, bl);
+        uint32_t th = (uint32_t)__builtin_amdgcn_readlane((int)bh, 0), tl = (uint32_t)__builtin_amdgcn_readlane((int)bl, 0);
+#pragma unroll
+        for (int q = 16; q < 64; q += 16)
+            key_take(th, tl, (uint32_t)__builtin_amdgcn_readlane((int)bh, q), (uint32_t)__builtin_amdgcn_readlane((int)bl, q));
+        const int ex = (int)~tl;                    // the winner (uniform)
+        const float p = __uint_as_float(th - 1u);   // its probability (the key's high word is its bits plus one)
+        ws += p;                                    // (slot order, as the reference's loop)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (lane + 64 * j == ex) kh[j] = kl[j] = 0u;  // dropped: the next round takes the next key
+        if (tid == 0) {
+            if (ids) ids[r] = ex;
+            s.selid[r] = ex;
+            s.selw[r] = p;
+        }
+    }
+    if (ids && tid == n_used && ids_stride > n_used) ids[n_used] = -1;  // the shared slot
+    if (w_sh) {  // (uniform) the shared expert's gate
+        dsum = wg_sum(dsum, s.red);
+        if (tid == 0) *sg = 1.0f / (1.0f + expf(-dsum));
+    }
+    __syncthreads();  // (selid / selw for every thread)
+    ws = fmaxf(ws, 6.103515625e-5f);
+    if (wts && tid < n_used) wts[tid] = s.selw[tid] / ws;
+}
+
 // One token's routing by a 256-thread workgroup (every thread calls it; it has barriers): softmax of the n_expert
 // logits l (exp(l - max) / sum), the n_used largest probabilities in descending order (equal values: the lower
 // expert) by each expert's rank among 64-bit (probability, ~index) keys, their weights divided by max(sum, 2^-14),
@@ -133,6 +213,10 @@ __device__ __forceinline__ void route_token(const float *__restrict__ l, const f
                                             int n, int ids_stride, RouterLds<PER> &s) {
     if (n_expert <= 128) {  // (uniform)
         route_token_128(l, x, w_sh, ids, wts, sg, n_expert, n_used, n, ids_stride, s);
+        return;
+    }
+    if (n_expert <= 256 && n_used <= RT_ROUNDS) {  // (uniform)
+        route_token_256(l, x, w_sh, ids, wts, sg, n_expert, n_used, n, ids_stride, s);
         return;
     }
     const int tid = threadIdx.x;

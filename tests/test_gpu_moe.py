@@ -29,7 +29,8 @@ def host(t):
 
 
 @pytest.mark.parametrize("T,E,n_used", [(1, 128, 8), (512, 128, 8), (7, 256, 8), (3, 1024, 64), (5, 16, 4),
-                                        (4, 64, 8), (6, 65, 8), (3, 100, 6), (4, 127, 16), (3, 129, 8)])
+                                        (4, 64, 8), (6, 65, 8), (3, 100, 6), (4, 127, 16), (3, 129, 8),
+                                        (300, 256, 8), (4, 256, 16), (4, 256, 17), (5, 192, 1), (3, 255, 12)])
 def test_router(M, oracle, T, E, n_used):
     import torch
     logits = synth.gaussian(900 + T + E, T * E).reshape(T, E)
@@ -44,9 +45,10 @@ def test_router(M, oracle, T, E, n_used):
     assert np.allclose(host(wts), want_w, rtol=2e-6, atol=1e-8)
 
 
-def test_router_shared_gate_and_stride(M, oracle):
+@pytest.mark.parametrize("E", [128, 256, 200])
+def test_router_shared_gate_and_stride(M, oracle, E):
     import torch
-    T, E, n_used, n = 6, 128, 8, 2048
+    T, n_used, n = 6, 8, 2048
     logits = synth.gaussian(950, T * E).reshape(T, E)
     x = synth.gaussian(951, T * n).reshape(T, n)
     w = synth.gaussian(952, n, 0, 0.02)
