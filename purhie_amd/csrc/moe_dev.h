@@ -30,7 +30,7 @@ __device__ __forceinline__ float wg_max(float v, float *red) {
     return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-// the router's LDS for up to 256 PER experts (wkey, part: the form for at most 128)
+// the router's LDS for up to 256 PER experts (wkey, part: the forms for at most 128 and at most 256)
 template <int PER>
 struct RouterLds {
     unsigned long long key[256 * PER];
@@ -120,31 +120,19 @@ __device__ __forceinline__ void route_token_128(const float *__restrict__ l, con
     }
 }
 
-// 129 to 256 experts and at most RT_ROUNDS of them used: every wave holds all the logits (experts lane + 64 j, j < 4)
-// and computes the softmax with wave reductions, as the 128-expert form; then n_used rounds of argmax over the
-// experts' 64-bit keys, each a wave-wide maximum by DPP and scalar reads (the keys are distinct, so the maximum is
-// one expert, which its lane then drops). No LDS but the results and no barrier but the last one; the ranks of the
-// general form took each thread 128 LDS reads and 256 64-bit comparisons (config 5's 256-expert router, 2427 tokens:
-// ~28 us). The same selection (descending, equal probabilities: the lower expert) and the weight sum in slot order.
-constexpr int RT_ROUNDS = 16;
-
-// the larger of two keys given as (hi, lo) words
-__device__ __forceinline__ void key_take(uint32_t &bh, uint32_t &bl, uint32_t oh, uint32_t ol) {
-    const bool t = oh > bh || (oh == bh && ol > bl);
-    bh = t ? oh : bh;
-    bl = t ? ol : bl;
-}
-template <int CTRL>
-__device__ __forceinline__ void key_dpp(uint32_t &bh, uint32_t &bl) {
-    key_take(bh, bl, (uint32_t)dpp_i<CTRL>((int)bh), (uint32_t)dpp_i<CTRL>((int)bl));
-}
-
+// 129 to 256 experts: the 128-expert form with four experts a lane (lane + 64 j). Every wave computes the softmax
+// with wave reductions and all the keys; wave w writes the keys of its slice, experts 64 w .. 64 w + 63 (its lanes'
+// j = w keys), to its own LDS row and counts, for each of its lanes' four keys, the slice keys ahead of it (32
+// 16-byte reads and 256 comparisons a lane); the four waves' counts (at most 64 each, bytes) meet behind one
+// barrier. The general form's ranks took each thread 128 LDS reads and 256 comparisons against all the keys, behind
+// seven barriers: config 5's decode token (the router inside its expert gate / up launch) 47.0 -> 34.8 us (rounds
+// of a wave-wide argmax instead, one per expert used, measured 36.3). Results as route_token's.
 template <int PER>
 __device__ __forceinline__ void route_token_256(const float *__restrict__ l, const float *__restrict__ x,
                                                 const float *__restrict__ w_sh, int *__restrict__ ids,
                                                 float *__restrict__ wts, float *__restrict__ sg, int n_expert,
                                                 int n_used, int n, int ids_stride, RouterLds<PER> &s) {
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float v[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] = lane + 64 * j < n_expert ? l[lane + 64 * j] : -INFINITY;
@@ -153,41 +141,37 @@ __device__ __forceinline__ void route_token_256(const float *__restrict__ l, con
         for (int i = tid; i < n; i += 256) dsum = fmaf(x[i], w_sh[i], dsum);
     }
     const float mx = group_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])), 64);
-    float e[4];
+    float p[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) e[j] = lane + 64 * j < n_expert ? expf(v[j] - mx) : 0.0f;
-    const float inv = 1.0f / group_sum((e[0] + e[1]) + (e[2] + e[3]), 64);
-    uint32_t kh[4], kl[4];  // a missing expert's key is 0: below every real key
+    for (int j = 0; j < 4; ++j) p[j] = lane + 64 * j < n_expert ? expf(v[j] - mx) : 0.0f;
+    const float inv = 1.0f / group_sum((p[0] + p[1]) + (p[2] + p[3]), 64);
+    unsigned long long k[4];  // (a missing expert's key is 0: below every real key, it never counts ahead)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const bool h = lane + 64 * j < n_expert;
-        const unsigned long long k = route_key(e[j] * inv, lane + 64 * j);
-        kh[j] = h ? (uint32_t)(k >> 32) : 0u;
-        kl[j] = h ? (uint32_t)k : 0u;
+        p[j] *= inv;
+        k[j] = lane + 64 * j < n_expert ? route_key(p[j], lane + 64 * j) : 0ull;
     }
-    float ws = 0.0f;
-    for (int r = 0; r < n_used; ++r) {  // (uniform)
-        uint32_t bh = kh[0], bl = kl[0];
+    auto mine = [&](auto a) { return wave == 0 ? a[0] : wave == 1 ? a[1] : wave == 2 ? a[2] : a[3]; };
+    unsigned long long *wk = s.wkey[wave];
+    wk[lane] = mine(k);
+    __builtin_amdgcn_wave_barrier();
+    int r[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int j = 1; j < 4; ++j) key_take(bh, bl, kh[j], kl[j]);
-        key_dpp<DPP_PAIR>(bh, bl);
-        key_dpp<DPP_QHALF>(bh, bl);
-        key_dpp<DPP_HALF_MIRROR>(bh, bl);
-        key_dpp<DPP_MIRROR>(bh, bl);
-        uint32_t th = (uint32_t)__builtin_amdgcn_readlane((int)bh, 0), tl = (uint32_t)__builtin_amdgcn_readlane((int)bl, 0);
+    for (int j = 0; j < 64; j += 2) {
+        const ulonglong2 u = *(const ulonglong2 *)(wk + j);
 #pragma unroll
-        for (int q = 16; q < 64; q += 16)
-            key_take(th, tl, (uint32_t)__builtin_amdgcn_readlane((int)bh, q), (uint32_t)__builtin_amdgcn_readlane((int)bl, q));
-        const int ex = (int)~tl;                    // the winner (uniform)
-        const float p = __uint_as_float(th - 1u);   // its probability (the key's high word is its bits plus one)
-        ws += p;                                    // (slot order, as the reference's loop)
+        for (int q = 0; q < 4; ++q) r[q] += (u.x > k[q]) + (u.y > k[q]);
+    }
+    uint8_t *part = (uint8_t *)s.part;  // [4][256] bytes within the 128-expert form's ints
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (lane + 64 * j == ex) kh[j] = kl[j] = 0u;  // dropped: the next round takes the next key
-        if (tid == 0) {
-            if (ids) ids[r] = ex;
-            s.selid[r] = ex;
-            s.selw[r] = p;
+    for (int q = 0; q < 4; ++q) part[256 * wave + lane + 64 * q] = (uint8_t)r[q];
+    __syncthreads();
+    if (tid < n_expert) {  // thread tid holds expert tid as its lane's key j = wave
+        const int rk = ((int)part[tid] + (int)part[256 + tid]) + ((int)part[512 + tid] + (int)part[768 + tid]);
+        if (rk < n_used) {
+            if (ids) ids[rk] = tid;
+            s.selid[rk] = tid;
+            s.selw[rk] = mine(p);
         }
     }
     if (ids && tid == n_used && ids_stride > n_used) ids[n_used] = -1;  // the shared slot
@@ -195,9 +179,20 @@ __device__ __forceinline__ void route_token_256(const float *__restrict__ l, con
         dsum = wg_sum(dsum, s.red);
         if (tid == 0) *sg = 1.0f / (1.0f + expf(-dsum));
     }
-    __syncthreads();  // (selid / selw for every thread)
-    ws = fmaxf(ws, 6.103515625e-5f);
-    if (wts && tid < n_used) wts[tid] = s.selw[tid] / ws;
+    __syncthreads();
+    if (wts) {  // (uniform) the sum in slot order, as the reference's loop (every thread the same), 8 reads at once
+        float ws = 0.0f;
+        for (int b = 0; b < n_used; b += 8) {
+            float w8[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w8[i] = s.selw[b + i < n_used ? b + i : 0];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (b + i < n_used) ws += w8[i];
+        }
+        ws = fmaxf(ws, 6.103515625e-5f);
+        if (tid < n_used) wts[tid] = s.selw[tid] / ws;
+    }
 }
 
 // One token's routing by a 256-thread workgroup (every thread calls it; it has barriers): softmax of the n_expert
@@ -215,7 +210,7 @@ __device__ __forceinline__ void route_token(const float *__restrict__ l, const f
         route_token_128(l, x, w_sh, ids, wts, sg, n_expert, n_used, n, ids_stride, s);
         return;
     }
-    if (n_expert <= 256 && n_used <= RT_ROUNDS) {  // (uniform)
+    if (n_expert <= 256) {  // (uniform)
         route_token_256(l, x, w_sh, ids, wts, sg, n_expert, n_used, n, ids_stride, s);
         return;
     }
