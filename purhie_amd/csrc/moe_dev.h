@@ -156,11 +156,16 @@ __device__ __forceinline__ void route_token_256(const float *__restrict__ l, con
     wk[lane] = mine(k);
     __builtin_amdgcn_wave_barrier();
     int r[4] = {0, 0, 0, 0};
+    // (16 keys, 8 reads, at a time: the whole slice's 32 reads in flight took 60 more registers in every kernel
+    // that inlines the router)
+#pragma unroll 1
+    for (int j0 = 0; j0 < 64; j0 += 16) {
 #pragma unroll
-    for (int j = 0; j < 64; j += 2) {
-        const ulonglong2 u = *(const ulonglong2 *)(wk + j);
+        for (int j = j0; j < j0 + 16; j += 2) {
+            const ulonglong2 u = *(const ulonglong2 *)(wk + j);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) r[q] += (u.x > k[q]) + (u.y > k[q]);
+            for (int q = 0; q < 4; ++q) r[q] += (u.x > k[q]) + (u.y > k[q]);
+        }
     }
     uint8_t *part = (uint8_t *)s.part;  // [4][256] bytes within the 128-expert form's ints
 #pragma unroll

@@ -26,6 +26,8 @@
 // from the start and each wave computes as its data arrives. A row's result is a sum of per-unit partials
 // in an order set by K alone: it does not depend on the other matrices of the launch or on how many
 // tokens share it.
+#include <algorithm>
+
 #include "device.h"
 #include "kernels.h"
 #include "moe_dev.h"
@@ -814,7 +816,10 @@ __global__ void __launch_bounds__(THR) k_mv_tile_id(MvIdArgs a, TileArgs ta) {
     if constexpr (ROUTE) {  // the token's experts from its logits (every workgroup; the first one stores them)
         static_assert(THR == 256, "the router's reductions take 256 threads");
         static_assert(!SW, "the routed launch is the gate / up pair");
-        __shared__ RouterLds<1> rs;
+        // the router's LDS is the start of the tile's (activation, then weights), which the tile writes only after
+        // the barrier below: no LDS of its own on top of the tile's (config 5's 1024-tile expert pair: 3 tiles a CU
+        // with it, all 4 without)
+        RouterLds<1> &rs = *reinterpret_cast<RouterLds<1> *>(smem);
         const int t = blockIdx.z, slot = (int)blockIdx.y % a.n_used;
         const bool first = blockIdx.x == 0 && blockIdx.y == 0;
         {
@@ -830,6 +835,7 @@ __global__ void __launch_bounds__(THR) k_mv_tile_id(MvIdArgs a, TileArgs ta) {
         en.e = rs.selid[slot];
         en.out_row = (long long)t * a.n_used + slot;
         en.in_row = a.x_per_slot ? en.out_row : t;
+        __syncthreads();  // (every thread's reads of the router's LDS are done)
     } else if (!id_entry(a, en)) {
         return;  // (uniform: before any barrier)
     }
@@ -1096,13 +1102,14 @@ static hipError_t tile_id_launch(const MvIdArgs &a, const TileArgs &ta, hipStrea
     const bool small = a.K / 16 <= THR && a.K / Tu<TYPE>::ACT <= THR;  // a thread for every value chunk and scale
     if (a.route_logits) {
         if constexpr (THR == 256) {
-            // (the routed kernel's static router LDS comes on top of the tile's: past 64 KiB in all, the caller
-            // falls back to the router and the pair as two launches)
-            if (a.cap || a.n_tiles || lds + sizeof(RouterLds<1>) > 65536) return hipErrorNotSupported;
+            // (the router's LDS lies within the tile's, which is at least its size; past 64 KiB the caller falls back
+            // to the router and the pair as two launches)
+            const size_t lr = std::max(lds, sizeof(RouterLds<1>));
+            if (a.cap || a.n_tiles || lr > 65536) return hipErrorNotSupported;
             if (small)
-                hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, false, false, true, true>), grid, dim3(THR), lds, stream, a,
+                hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, false, false, true, true>), grid, dim3(THR), lr, stream, a,
                                    ta);
-            else hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, false, false, true>), grid, dim3(THR), lds, stream, a, ta);
+            else hipLaunchKernelGGL((k_mv_tile_id<TYPE, THR, false, false, true>), grid, dim3(THR), lr, stream, a, ta);
             return hipGetLastError();
         }
         return hipErrorNotSupported;
