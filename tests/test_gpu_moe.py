@@ -219,7 +219,7 @@ def test_add_rmsnorm_bad_arguments(M):
 def test_routed_pair_same_bits(M, oracle, kpath, t, T, E, n_used, N, K):
     """qmatvec_launch_q8_id_pair_routed (routing inside the gate / up pair launch) gives gpu_moe_router's ids and
     weights and qmatvec_launch_q8_id_pair's outputs bit for bit: on the tile kernel (n_expert <= 256) and through
-    the two launches it falls back to (n_expert 300, the per-wave path, and a K whose tile with the router's LDS
+    the two launches it falls back to (n_expert 300, the per-wave path, and a K whose tile's LDS
     would pass 64 KiB: Q8_0 at K = 24576)"""
     import ctypes as C
     import torch
