@@ -215,12 +215,13 @@ def test_add_rmsnorm_bad_arguments(M):
 @pytest.mark.parametrize("t,T,E,n_used,N,K", [(100, 1, 128, 8, 768, 2048), (12, 1, 128, 8, 768, 2048),
                                               (100, 3, 256, 8, 512, 1024), (40, 2, 64, 4, 256, 1024),
                                               (100, 1, 300, 8, 256, 1024), (100, 2, 100, 6, 256, 1024),
-                                              (8, 1, 16, 4, 64, 16384), (8, 1, 16, 4, 64, 24576)])
+                                              (8, 1, 16, 4, 64, 16384), (8, 1, 16, 4, 64, 24576),
+                                              (8, 1, 16, 4, 64, 32768)])
 def test_routed_pair_same_bits(M, oracle, kpath, t, T, E, n_used, N, K):
     """qmatvec_launch_q8_id_pair_routed (routing inside the gate / up pair launch) gives gpu_moe_router's ids and
     weights and qmatvec_launch_q8_id_pair's outputs bit for bit: on the tile kernel (n_expert <= 256) and through
     the two launches it falls back to (n_expert 300, the per-wave path, and a K whose tile's LDS
-    would pass 64 KiB: Q8_0 at K = 24576)"""
+    would pass 64 KiB: Q8_0 at K = 32768; at K = 24576 the tile and the router's LDS within it take 62.5 KiB)"""
     import ctypes as C
     import torch
     from purhie_amd import qmatvec as Q
