@@ -56,11 +56,8 @@ __global__ void __launch_bounds__(256) k_swiglu(const float *__restrict__ g, con
 }
 
 // The same values and bits with a wave per 256-value block (n % 32 == 0, 16-byte aligned g / u / out, 4-byte
-// aligned q0 / qK): lane l holds values 4l .. 4l + 3 of the block (one 16-byte load of g and of u, one store), a
-// Q8_0 block is 8 lanes and a Q8_K block the wave, so the maxima and sums stay in the wave (no LDS, no barrier).
-// BW blocks a wave, their loads issued before the first is computed. The arithmetic is q8_quantize_value's value
-// for value; maxima and integer sums are exact in any order, and the Q8_K pick (largest |x|, lowest index) is a
-// total order.
+// aligned q0 / qK): lane l holds values 4l .. 4l + 3 of the block (one 16-byte load of g and of u, one store), and
+// q8_quantize4 quantizes them within the wave. BW blocks a wave, their loads issued before the first is computed.
 template <int BW>
 __global__ void __launch_bounds__(256) k_swiglu4(const float4 *__restrict__ g, const float4 *__restrict__ u,
                                                  float4 *__restrict__ out, int n, Q8Ptrs o, int quantize) {
@@ -89,77 +86,7 @@ __global__ void __launch_bounds__(256) k_swiglu4(const float4 *__restrict__ g, c
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[r] = active ? gv[r] / (1.0f + expf(-gv[r])) * uv[r] : 0.0f;
         if (active) out[i4] = make_float4(v[0], v[1], v[2], v[3]);
-        if (!quantize) continue;
-
-        // Q8_0 over 32 values: 8 lanes
-        float a[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) a[r] = fabsf(v[r]);
-        const float am = group_max(fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3])), 8);
-        const float id0 = am != 0.0f ? 127.0f / am : 0.0f;
-        int q[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) q[r] = active ? (int)rintf(v[r] * id0) : 0;
-        const int s0 = group_isum((q[0] + q[1]) + (q[2] + q[3]), 8);
-        const long long i = 4 * i4;
-        auto pack = [](const int *x) {
-            return (uint32_t)(x[0] & 0xff) | (uint32_t)(x[1] & 0xff) << 8 | (uint32_t)(x[2] & 0xff) << 16 |
-                   (uint32_t)(x[3] & 0xff) << 24;
-        };
-        if (active) {
-            *(uint32_t *)(o.q0 + i) = pack(q);
-            if ((lane & 7) == 0) {
-                const float d = am / 127.0f;
-                o.d0[i >> 5] = __half2float(__float2half(d));
-                if (o.s0) {
-                    float p = d * (float)s0;
-                    __asm__ volatile("" : "+v"(p));  // (fp16 of the fp32 product: no fused conversion)
-                    o.s0[i >> 5] = __float_as_int(__half2float(__float2half(p)));
-                }
-            }
-        }
-        if (!o.qK) continue;
-
-        // Q8_K over the wave's 256 values: the lane's own pick (strict: the lowest index), then the wave's
-        float ba = a[0], bv = v[0];
-        int bi = 4 * lane;
-#pragma unroll
-        for (int r = 1; r < 4; ++r)
-            if (a[r] > ba) {
-                ba = a[r];
-                bv = v[r];
-                bi = 4 * lane + r;
-            }
-        auto take = [&](float oa, float ov, int oi) {
-            if (oa > ba || (oa == ba && oi < bi)) {
-                ba = oa;
-                bi = oi;
-                bv = ov;
-            }
-        };
-        take(dpp_f<DPP_PAIR>(ba), dpp_f<DPP_PAIR>(bv), dpp_i<DPP_PAIR>(bi));
-        take(dpp_f<DPP_QHALF>(ba), dpp_f<DPP_QHALF>(bv), dpp_i<DPP_QHALF>(bi));
-        take(dpp_f<DPP_HALF_MIRROR>(ba), dpp_f<DPP_HALF_MIRROR>(bv), dpp_i<DPP_HALF_MIRROR>(bi));
-        take(dpp_f<DPP_MIRROR>(ba), dpp_f<DPP_MIRROR>(bv), dpp_i<DPP_MIRROR>(bi));
-        const float ra[4] = {readlane_f(ba, 0), readlane_f(ba, 16), readlane_f(ba, 32), readlane_f(ba, 48)};
-        const float rv[4] = {readlane_f(bv, 0), readlane_f(bv, 16), readlane_f(bv, 32), readlane_f(bv, 48)};
-        const int ri[4] = {__builtin_amdgcn_readlane(bi, 0), __builtin_amdgcn_readlane(bi, 16),
-                           __builtin_amdgcn_readlane(bi, 32), __builtin_amdgcn_readlane(bi, 48)};
-        ba = ra[0];
-        bv = rv[0];
-        bi = ri[0];
-#pragma unroll
-        for (int r = 1; r < 4; ++r) take(ra[r], rv[r], ri[r]);
-        float iscale = 0.0f;
-        if (ba != 0.0f) iscale = -127.0f / bv;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) q[r] = ba != 0.0f ? min(127, (int)rintf(iscale * v[r])) : 0;
-        const int s16 = group_isum((q[0] + q[1]) + (q[2] + q[3]), 4);
-        if (active) {
-            *(uint32_t *)(o.qK + i) = pack(q);
-            if (lane == 0) o.dK[b] = ba != 0.0f ? 1.0f / iscale : 0.0f;
-            if ((lane & 3) == 0) o.bsK[i >> 4] = s16;
-        }
+        if (quantize) q8_quantize4(v, active, b, 4 * i4, lane, o);
     }
 }
 
