@@ -53,7 +53,7 @@ int qmatvec_supported(int type);
  *                           token's row the same bits as qmatvec_launch gives it)
  *   qmatvec_launch_batch_h  the same with the caller's scratch xh (16-byte aligned, xh_bytes >= 2 T K) for the copy
  *   qmatvec_half_supported  F16 / BF16, GEMMs on, T >= 32 (any T in prefill mode), N >= 64, K % 8 == 0,
- *                           row_bytes >= 2 K and a multiple of 16, W 16-byte aligned
+ *                           K < 2^22, row_bytes >= 2 K, a multiple of 16 and below 2^23, W 16-byte aligned
  *   qmatvec_round_half      x -> xh rounded to the type (n % 8 == 0, both 16-byte aligned)
  *   qmatvec_launch_batch_hx the GEMM on xh (T rows of K values) */
 hipError_t qmatvec_launch_bf16f(const void *W, size_t row_bytes, const float *x, float *y, int N, int K, int T,

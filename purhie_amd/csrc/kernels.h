@@ -179,6 +179,9 @@ __host__ __device__ inline SplitCapLayout gemm_split_capture_layout(int K, int X
     return SplitCapLayout{plane, 2 * plane, 2 * plane + (XR + 3) / 4 * 4};
 }
 
+// CUs of the current device (read once per device; 256 when the query fails)
+int device_cus();
+
 // Float activations over F32 / F16 / BF16 weights (type ids 0, 1, 30): the decode matvec for T tokens (round:
 // the activations rounded to the 16-bit weight type), the F16 / BF16 MFMA GEMM on activations rounded to 16 bits
 // (xh; or x itself, rounded while staging: launch_gemm_float_x), and that rounding (n % 8 == 0)

@@ -906,7 +906,7 @@ static int tile_threads(int nb, long long rows) {
 }
 
 // CUs of the current device (read once per device)
-static int device_cus() {
+int device_cus() {
     static int cus[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;

@@ -197,7 +197,8 @@ hipError_t qmatvec_launch(int type, const void *W, size_t row_bytes, const float
 
 int qmatvec_half_supported(int type, const void *W, size_t row_bytes, int N, int K, int T) {
     return half_type(type) && mfma_on() && (g_prefill || T >= gemm_min_t()) && T >= 1 && N >= 64 && K > 0 &&
-           K % 8 == 0 && row_bytes >= (size_t)K * 2 && row_bytes % 16 == 0 && al16(W);
+           K % 8 == 0 && K < (1 << 22) && row_bytes >= (size_t)K * 2 && row_bytes % 16 == 0 &&
+           row_bytes < ((size_t)1 << 23) && al16(W);
 }
 
 hipError_t qmatvec_round_half(int type, const float *x, uint16_t *xh, long long n, hipStream_t stream) {

@@ -122,6 +122,35 @@ def test_half_gemm(Q, oracle, t, N, K, T):
 
 
 @pytest.mark.parametrize("t", (F16, BF16))
+def test_half_gemm_256_row_tiles(Q, oracle, t):
+    """N = 2200 (a partial last row tile), K = 1000 (a partial last stage), T = 2000: enough workgroups for the
+    256-row tiles on MI355X's 256 CUs. The fp32-x form the same bits as the scratch form, sampled tokens within
+    tolerance of the oracle, and every token's row the same bits as a 40-token launch (128-row tiles) gives it:
+    the row tile does not change the summation order."""
+    import torch
+    L = Q.lib()
+    N, K, T = 2200, 1000, 2000
+    W = weights(t, 60, N, K)
+    Wd = dev(W)
+    rb = W.shape[1]
+    x = acts(61, T, K)
+    assert L.qmatvec_half_supported(t, p(Wd), rb, N, K, T) == 1
+    y1 = torch.full((T, N), float("nan"), dtype=torch.float32, device="cuda")
+    assert L.qmatvec_launch_batch(t, p(Wd), rb, p(dev(x)), p(y1), N, K, T, None) == 0
+    xh = torch.empty(T * K, dtype=torch.uint16, device="cuda")
+    y2 = torch.full((T, N), float("nan"), dtype=torch.float32, device="cuda")
+    assert L.qmatvec_launch_batch_h(t, p(Wd), rb, p(dev(x)), p(xh), T * K * 2, p(y2), N, K, T, None) == 0
+    g1, g2 = host(y1), host(y2)
+    assert np.array_equal(g1.view(np.uint32), g2.view(np.uint32))
+    sel = np.arange(0, T, 21)
+    check(oracle, t, W, N, K, x[sel], g1[sel])
+    for a, b in ((0, 40), (1000, 1040), (1960, 2000)):
+        part = torch.full((b - a, N), float("nan"), dtype=torch.float32, device="cuda")
+        assert L.qmatvec_launch_batch(t, p(Wd), rb, p(dev(x[a:b])), p(part), N, K, b - a, None) == 0
+        assert np.array_equal(host(part).view(np.uint32), g1[a:b].view(np.uint32)), (a, b)
+
+
+@pytest.mark.parametrize("t", (F16, BF16))
 def test_round_half_special_values(Q, oracle, t):
     import torch
     L = Q.lib()
