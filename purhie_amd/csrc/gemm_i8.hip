@@ -456,17 +456,23 @@ __global__ void __launch_bounds__(I8_THREADS, 2) k_gemm_i8kq(GemmArgs a) {
 
     // stages st = 4 s + c; step c issues stage st + 2 (into set st & 1, whose stage st went to LDS in the previous
     // step), computes stage st (and the super-block's epilogue after its last stage), and commits stage st + 1 (set
-    // (st + 1) & 1) before the barrier
+    // (st + 1) & 1) before the barrier. UNC (Q6_K, IQ4_XS): past the last super-block the issues load its stages
+    // again and the last step commits one of them into buffers nothing reads afterwards, so the loop body has no
+    // branch and the waits count the loads exactly, and the loads are kept ahead of the MFMAs (sched_barrier):
+    // Q6_K 9728 x 2560 / 2560 x 9728 x 2427 218 / 230 -> 210 / 205 us, IQ4_XS 204 -> 200 us. Q4_K and Q5_K keep the
+    // branches (the same form measured 197 -> 204 and 216 -> 222 us on 9728 x 2560). One box, interleaved.
+    constexpr bool UNC = TYPE == TY_Q6_K || TYPE == TY_IQ4_XS;
     auto step = [&](auto cc, int s) {
         constexpr int c = decltype(cc)::value;
         Pre &pi = pick2<c & 1>(P0, P1);
         Pre &pc = pick2<(c + 1) & 1>(P0, P1);
         if constexpr (c < 2) issue(IC<c + 2>{}, pi, s);
-        else if (s + 1 < nsb) issue(IC<c - 2>{}, pi, s + 1);
+        else if (UNC || s + 1 < nsb) issue(IC<c - 2>{}, pi, s + 1 < nsb ? s + 1 : nsb - 1);
+        if constexpr (UNC) __builtin_amdgcn_sched_barrier(0);
         compute(cc);
         if constexpr (c == 3) epilogue(s);
         if constexpr (c < 3) commit(IC<c + 1>{}, pc, s);
-        else if (s + 1 < nsb) commit(IC<0>{}, pc, s + 1);
+        else if (UNC || s + 1 < nsb) commit(IC<0>{}, pc, s + 1);
         __syncthreads();
     };
 
@@ -621,9 +627,10 @@ __global__ void __launch_bounds__(I8_THREADS, 2) k_gemm_i8blk(GemmArgs a) {
     const int8_t *xsrc[XR];
 #pragma unroll
     for (int i = 0; i < XR; ++i) xsrc[i] = a.xq + trow((tid >> 2) + 64 * i) * K + 16 * (tid & 3);
-    // token scales: thread t < 2 BT stages block t / BT of the stage for token t % BT
+    // token scales: thread t < 2 BT stages block t / BT of the stage for token t % BT (the other threads load the
+    // same value as thread t % (2 BT) and store nothing: no branch around the load)
     const bool don = tid < 2 * BT;
-    const float *dsrc = a.dx + trow(tid % BT) * nb + (tid / BT);
+    const float *dsrc = a.dx + trow(tid % BT) * nb + ((tid % (2 * BT)) / BT);
 
     struct Pre {
         typename S::Raw raw;
@@ -635,7 +642,7 @@ __global__ void __launch_bounds__(I8_THREADS, 2) k_gemm_i8blk(GemmArgs a) {
         S::load(wrow, 2 * st, p.raw);
 #pragma unroll
         for (int i = 0; i < XR; ++i) p.xv[i] = *(const uint4 *)(xsrc[i] + 64 * st);
-        if (don) p.dv = dsrc[2 * st];
+        p.dv = dsrc[2 * st];
     };
     auto commit = [&](auto cc, const Pre &p) {
         constexpr int buf = decltype(cc)::value;
@@ -694,19 +701,22 @@ __global__ void __launch_bounds__(I8_THREADS, 2) k_gemm_i8blk(GemmArgs a) {
         }
     };
 
-    // stage st: issue st + 2 (set st & 1), compute st, commit st + 1 (set (st + 1) & 1), barrier
+    // stage st: issue st + 2 (set st & 1), compute st, commit st + 1 (set (st + 1) & 1), barrier. A stage past the
+    // end loads the last one again, committed into the idle buffer and never read: a step has no branch around its
+    // loads, so the waits count them exactly. (The odd last step stays inside the loop: peeled after it, the
+    // compiler's schedule held 256 registers and spilled.)
     auto step = [&](auto cc, int st) {
         constexpr int c = decltype(cc)::value;
         Pre &pi = pick2<c>(P0, P1);
         Pre &pc = pick2<1 - c>(P0, P1);
-        if (st + 2 < nst) issue(pi, st + 2);
+        issue(pi, st + 2 < nst ? st + 2 : nst - 1);
         compute(cc, st);
-        if (st + 1 < nst) commit(IC<1 - c>{}, pc);
+        commit(IC<1 - c>{}, pc);
         __syncthreads();
     };
 
     issue(P0, 0);
-    if (nst > 1) issue(P1, 1);
+    issue(P1, nst > 1 ? 1 : 0);
     commit(IC<0>{}, P0);
     __syncthreads();
     for (int st = 0; st < nst; st += 2) {
