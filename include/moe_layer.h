@@ -69,7 +69,7 @@ hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qm
  * The workspace is a static device array of PURHIE_MOE_SCRATCH_BYTES on each GPU, held from the library's load
  * until the process ends; its address is looked up once per device, on the first call with that device current.
  * Returns hipErrorInvalidValue when purhie_moe_workspace_bytes(w, T) exceeds PURHIE_MOE_SCRATCH_BYTES (at n_embd
- * 2048, 128 experts of n_ff_exp 768, top 8, no shared expert: above 215 tokens) or for any argument
+ * 2048, 128 experts of n_ff_exp 768, top 8, no shared expert: above 256 tokens) or for any argument
  * purhie_moe_ffn rejects. Every call on one GPU shares that GPU's array and leaves its contents behind (each call
  * writes every region before reading it): calls that overlap on one GPU (other streams, other threads) race.
  * Nothing is allocated. */

@@ -25,7 +25,8 @@ hipError_t gpu_add_rmsnorm(const float *x_in, const float *add, float *x_out, co
 
 /* replaces src/gpu_ops.h:29 (kernel src/gpu_ops.hip:103-113): out = SiLU(g) * u = g / (1 + exp(-g)) * u for
  * n values, quantized into q8 in the same launch when q8 is not NULL (n % 32 == 0, n <= q8->max_k; the Q8_K
- * side is complete only for whole 256-value blocks). */
+ * side is complete only for whole 256-value blocks). With q8 set, out may be NULL: only the quantized form is
+ * written (no counterpart in the reference, whose out is always written). */
 hipError_t gpu_swiglu(const float *g, const float *u, float *out, int n, const qmatvec_q8 *q8, hipStream_t stream);
 
 /* replaces src/gpu_ops.h:36-37 (kernels src/gpu_ops.hip:149-241): for T tokens, logits [T][n_expert] ->

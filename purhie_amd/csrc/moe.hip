@@ -46,7 +46,7 @@ __global__ void __launch_bounds__(256) k_swiglu(const float *__restrict__ g, con
         float v = 0.0f;
         if (active) {
             v = a / (1.0f + expf(-a)) * ub;
-            out[i] = v;
+            if (out) out[i] = v;  // (uniform: null when only the quantized form is wanted)
         }
         if (quantize) {  // (uniform)
             if (k) __syncthreads();  // the previous block's reads of sh are done
@@ -85,7 +85,7 @@ __global__ void __launch_bounds__(256) k_swiglu4(const float4 *__restrict__ g, c
         float v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[r] = active ? gv[r] / (1.0f + expf(-gv[r])) * uv[r] : 0.0f;
-        if (active) out[i4] = make_float4(v[0], v[1], v[2], v[3]);
+        if (active && out) out[i4] = make_float4(v[0], v[1], v[2], v[3]);  // (out null: only the quantized form)
         if (quantize) q8_quantize4(v, active, b, 4 * i4, lane, o);
     }
 }
@@ -306,7 +306,7 @@ using namespace pq;
 extern "C" {
 
 hipError_t gpu_swiglu(const float *g, const float *u, float *out, int n, const qmatvec_q8 *q8, hipStream_t stream) {
-    if (!g || !u || !out || n < 0) return hipErrorInvalidValue;
+    if (!g || !u || (!out && !q8) || n < 0) return hipErrorInvalidValue;
     if (n == 0) return hipSuccess;
     Q8Ptrs o{};
     if (q8) {

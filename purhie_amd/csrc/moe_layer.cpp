@@ -33,7 +33,7 @@ long long round256(long long n) { return (n + 255) / 256 * 256; }
 
 // the workspace regions, each 256-byte aligned
 struct Layout {
-    float *logits = nullptr, *wts = nullptr, *sg = nullptr, *g = nullptr, *u = nullptr, *act = nullptr;
+    float *logits = nullptr, *wts = nullptr, *sg = nullptr, *g = nullptr, *u = nullptr;
     float *down = nullptr, *ffg = nullptr, *ffu = nullptr, *sact = nullptr, *shout = nullptr;
     int32_t *ids = nullptr, *tok = nullptr, *pair = nullptr, *ntiles = nullptr, *te = nullptr, *ts = nullptr,
             *tn = nullptr;
@@ -100,7 +100,6 @@ Layout layout(const purhie_moe_weights *w, int T, char *base) {
     L.sg = (float *)take((size_t)T * 4);
     L.g = (float *)take((size_t)T * L.ns * FE * 4);
     L.u = (float *)take((size_t)T * L.ns * FE * 4);
-    L.act = (float *)take((size_t)T * L.ns * FE * 4);
     L.down = (float *)take((size_t)T * L.ns * E * 4);
     L.qx = take(qmatvec_q8_bytes(L.qx_k));
     if (L.grouped) {
@@ -205,7 +204,7 @@ hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qm
                                       w->rb_gate_up, L.ids, L.ns, 0, q8_xn, L.g, L.u, FE, E, 1, stream));
         if (fuse) PQ_TRY(fused(w->down_shexp, L.down, L.ns, 1));
         if (!fuse) {
-            PQ_TRY(gpu_swiglu(L.g, L.u, L.act, L.ns * FE, &qx, stream));
+            PQ_TRY(gpu_swiglu(L.g, L.u, nullptr, L.ns * FE, &qx, stream));  // (the quantized form only)
             PQ_TRY(qmatvec_launch_q8_id_x(w->type_down, w->down_exps, nullptr, w->down_shexp, nullptr, w->rb_down,
                                           L.ids, L.ns, 1, &qx, L.down, nullptr, E, FE, 1, stream));
         }
@@ -243,7 +242,7 @@ hipError_t purhie_moe_ffn(const purhie_moe_weights *w, const float *xn, const qm
     }
     if (fuse) PQ_TRY(fused(nullptr, L.down, NU, T));
     if (!fuse) {
-        if (!swiglu_done) PQ_TRY(gpu_swiglu(L.g, L.u, L.act, T * NU * FE, &qx, stream));
+        if (!swiglu_done) PQ_TRY(gpu_swiglu(L.g, L.u, nullptr, T * NU * FE, &qx, stream));
         if (L.grouped)
             PQ_TRY(qmatvec_launch_q8_id_batch(w->type_down, w->down_exps, w->rb_down, &qx, L.down, E, FE, L.max_tiles,
                                               L.tile, L.ntiles, L.te, L.ts, L.tn, L.pair, L.pair, stream));

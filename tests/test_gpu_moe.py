@@ -125,6 +125,8 @@ def test_swiglu_fused_quantize(M, oracle, n):
     if n % 32:
         with pytest.raises(Q.HipError):
             M.swiglu(dev(g), dev(u), out, n, q)
+        with pytest.raises(Q.HipError):  # out NULL needs q8
+            M.swiglu(dev(g), dev(u), None, n)
         M.swiglu(dev(g), dev(u), out, n)
         assert np.allclose(host(out), oracle.swiglu(g, u), rtol=1e-6, atol=1e-30)
         return
@@ -155,6 +157,13 @@ def test_swiglu_fused_quantize(M, oracle, n):
     v3 = {k: host(t) for k, t in q3.views(n).items()}
     for k in v:
         assert np.array_equal(v3[k].view(np.uint8), v[k].view(np.uint8)), k
+    # out NULL with q8 (the MoE layer's call): only the quantized form, the same bits, from both kernels
+    for gg, uu in ((dev(g), dev(u)), (gb[1:], ub[1:])):
+        q4 = Q.Q8(((n + 255) // 256) * 256)
+        M.swiglu(gg, uu, None, n, q4)
+        v4 = {k: host(t) for k, t in q4.views(n).items()}
+        for k in v:
+            assert np.array_equal(v4[k].view(np.uint8), v[k].view(np.uint8)), k
 
 
 @pytest.mark.parametrize("n,T", [(2560, 1), (5120, 3), (2048, 16), (1024, 40), (9728, 9)])

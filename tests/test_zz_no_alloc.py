@@ -78,7 +78,7 @@ def test_noalloc_matches_workspace_form(M, Q, t_gu, t_d):
 def test_noalloc_refuses_beyond_the_array(M, Q):
     import torch
     w, keep = layer(M, Q, 100, 100, 41)
-    T = 216  # the first token count whose workspace exceeds 32 MiB at these sizes
+    T = 257  # the first token count whose workspace exceeds 32 MiB at these sizes
     assert M.workspace_bytes(w, T) > M.SCRATCH_BYTES >= M.workspace_bytes(w, T - 1)
     xd = torch.zeros((T, E), dtype=torch.float32, device="cuda")
     q = Q.Q8(((T * E + 255) // 256) * 256)
