@@ -87,19 +87,34 @@ __device__ __forceinline__ float load1(const uint8_t *wr, int k) {
     else return val16<TYPE>(((const uint16_t *)wr)[k]);
 }
 
-// rows row0 .. row0 + FMV_RW - 1 (those below N) of wave w = blockIdx.x * FMV_WAVES + threadIdx.x / 64
+// rows row0 .. row0 + FMV_RW - 1 (those below N) of wave w = blockIdx.x * FMV_WAVES + threadIdx.x / 64.
+// stage (vec only): the workgroup's nt tokens, as the products see them (act), go to LDS first, so the 4 waves read
+// them there instead of each loading them from global memory (the activation was as many bytes as a row's weights:
+// the loads, not the arithmetic, bound the kernel). The weight chunks a lane has in flight are loaded whether or not
+// they are past the row's end (a past chunk reloads the last one and adds nothing): the loads have no branch around
+// them, so the waits count them exactly. Every lane adds its chunks in the same order in every form: the same bits.
 template <int TYPE, bool ROUND>
 __global__ void __launch_bounds__(64 * FMV_WAVES) k_mv_float(const uint8_t *__restrict__ W, long long rb,
                                                                const float *__restrict__ x, float *__restrict__ y,
-                                                               int N, int K, int T, int vec) {
+                                                               int N, int K, int T, int vec, int stage) {
     constexpr int EB = TYPE == QT_F32_ ? 4 : 2;
+    extern __shared__ __attribute__((aligned(16))) float sx[];
     const int lane = threadIdx.x & 63;
     const int row0 = (blockIdx.x * FMV_WAVES + (threadIdx.x >> 6)) * FMV_RW;
+    const int t0 = blockIdx.y * FMV_NT, nt = min(FMV_NT, T - t0);
+    const float *xt = x + (long long)t0 * K;
+    if (stage) {  // (uniform; every wave of the workgroup, before any returns)
+        const int n4 = nt * K / 4;
+        for (int j = threadIdx.x; j < n4; j += 64 * FMV_WAVES) {
+            const float4 v = ((const float4 *)xt)[j];
+            ((float4 *)sx)[j] = make_float4(act<TYPE, ROUND>(v.x), act<TYPE, ROUND>(v.y), act<TYPE, ROUND>(v.z),
+                                            act<TYPE, ROUND>(v.w));
+        }
+        __syncthreads();
+    }
     if (row0 >= N) return;
     const int nr = min(FMV_RW, N - row0);
-    const int t0 = blockIdx.y * FMV_NT, nt = min(FMV_NT, T - t0);
     const uint8_t *wr = W + (long long)row0 * rb;
-    const float *xt = x + (long long)t0 * K;
     float acc[FMV_RW][FMV_NT];
 #pragma unroll
     for (int r = 0; r < FMV_RW; ++r)
@@ -108,29 +123,40 @@ __global__ void __launch_bounds__(64 * FMV_WAVES) k_mv_float(const uint8_t *__re
     if (vec) {  // 16-byte aligned rows and activations, K % 8 == 0 (uniform)
         const int n8 = K / 8;
         // FMV_U chunks of each row in flight per lane: their weight loads are all issued before the arithmetic
-        for (int i0 = lane; i0 < n8; i0 += 64 * FMV_U) {
+        for (int c0 = 0; c0 < n8; c0 += 64 * FMV_U) {
             float w[FMV_RW][FMV_U][8];
 #pragma unroll
             for (int r = 0; r < FMV_RW; ++r)
 #pragma unroll
-                for (int u = 0; u < FMV_U; ++u)
-                    if (r < nr && i0 + 64 * u < n8) load8<TYPE>(wr + r * rb + (long long)EB * 8 * (i0 + 64 * u), w[r][u]);
+                for (int u = 0; u < FMV_U; ++u) {
+                    const int i = c0 + lane + 64 * u;
+                    load8<TYPE>(wr + (r < nr ? r : 0) * rb + (long long)EB * 8 * (i < n8 ? i : n8 - 1), w[r][u]);
+                }
 #pragma unroll
             for (int u = 0; u < FMV_U; ++u) {
-                const int i = i0 + 64 * u;
+                const int i = c0 + lane + 64 * u;
                 if (i >= n8) break;
 #pragma unroll
                 for (int t = 0; t < FMV_NT; ++t)
                     if (t < nt) {
-                        const float4 *xv = (const float4 *)(xt + (long long)t * K) + 2 * i;
-                        const float4 a = xv[0], b = xv[1];
-                        const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                        float xs[8];
+                        if (stage) {
+                            const float4 a = ((const float4 *)(sx + t * K))[2 * i], b = ((const float4 *)(sx + t * K))[2 * i + 1];
+                            xs[0] = a.x; xs[1] = a.y; xs[2] = a.z; xs[3] = a.w; xs[4] = b.x; xs[5] = b.y; xs[6] = b.z; xs[7] = b.w;
+                        } else {
+                            const float4 *xv = (const float4 *)(xt + (long long)t * K) + 2 * i;
+                            const float4 a = xv[0], b = xv[1];
+                            xs[0] = act<TYPE, ROUND>(a.x); xs[1] = act<TYPE, ROUND>(a.y);
+                            xs[2] = act<TYPE, ROUND>(a.z); xs[3] = act<TYPE, ROUND>(a.w);
+                            xs[4] = act<TYPE, ROUND>(b.x); xs[5] = act<TYPE, ROUND>(b.y);
+                            xs[6] = act<TYPE, ROUND>(b.z); xs[7] = act<TYPE, ROUND>(b.w);
+                        }
 #pragma unroll
                         for (int r = 0; r < FMV_RW; ++r)
                             if (r < nr) {
                                 float s = acc[r][t];
 #pragma unroll
-                                for (int k = 0; k < 8; ++k) s = __builtin_fmaf(w[r][u][k], act<TYPE, ROUND>(xs[k]), s);
+                                for (int k = 0; k < 8; ++k) s = __builtin_fmaf(w[r][u][k], xs[k], s);
                                 acc[r][t] = s;
                             }
                     }
@@ -391,7 +417,14 @@ hipError_t mv_float_t(const uint8_t *W, long long rb, const float *x, float *y, 
     const int vec = ((((uintptr_t)W | (uintptr_t)rb | (uintptr_t)x) & 15) == 0 && K % 8 == 0) ? 1 : 0;
     constexpr int RPW = FMV_WAVES * FMV_RW;  // rows per workgroup
     const dim3 grid((unsigned)((N + RPW - 1) / RPW), (unsigned)((T + FMV_NT - 1) / FMV_NT));
-    hipLaunchKernelGGL((k_mv_float<TYPE, ROUND>), grid, dim3(64 * FMV_WAVES), 0, s, W, rb, x, y, N, K, T, vec);
+    // one token of 16-bit weights: its activation in LDS when it takes at most 48 KiB (K <= 12288; three such
+    // workgroups a CU). Measured (one box, A/B): BF16 9728 x 2560 13.5 -> 10.6 us, 2560 x 9728 16.4 -> 12.5 us,
+    // 151936 x 2560 160 -> 129 us, F16 4096 x 4096 7.0 -> 6.0 us; F32 (twice the weight bytes per value) 12.7 ->
+    // 13.1 us and four tokens (four LDS reads per weight chunk) 23.5 -> 37.5 us, so those read x from global memory
+    const long long lds = (long long)K * 4;
+    const int stage = vec && T == 1 && TYPE != QT_F32_ && lds <= 49152 ? 1 : 0;
+    hipLaunchKernelGGL((k_mv_float<TYPE, ROUND>), grid, dim3(64 * FMV_WAVES), stage ? (size_t)lds : 0, s, W, rb, x, y, N,
+                       K, T, vec, stage);
     return hipGetLastError();
 }
 
