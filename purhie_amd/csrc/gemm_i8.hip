@@ -92,15 +92,18 @@ struct I8StageK {
     static constexpr int BB = Q5 ? 176 : 144, QS = Q5 ? 48 : 16;
     static constexpr bool MINS = true;
     static constexpr int SHIFT = Q5 ? 7 : 3;  // isum = (H << SHIFT) + L
+    // the super-block's 16 header bytes (d, dmin, the 12 scale bytes), loaded once for its four stages (hdr) and
+    // kept apart from the stage's loads: loaded again at every stage they were two fifths of a stage's bytes
+    static constexpr bool HDR = true;
+    __device__ static uint4 hdr(const uint8_t *row, int s) { return *(const uint4 *)(row + s * BB); }
     struct Raw {
-        uint4 h;
+        uint4 h;    // (set from the kept header at the commit)
         uint2 q;
         uint2 qh;  // (Q5_K only)
     };
     __device__ static void load(const uint8_t *row, int s, int c, Raw &r) {
         const int p = threadIdx.x & 3;
         const uint8_t *b = row + s * BB;
-        r.h = *(const uint4 *)b;
         r.q = *(const uint2 *)(b + QS + 32 * c + 8 * p);
         if constexpr (Q5) r.qh = *(const uint2 *)(b + 16 + 8 * p);
         else r.qh = make_uint2(0u, 0u);
@@ -166,7 +169,7 @@ struct I8Stage<TY_Q5_K> : I8StageK<true> {};
 template <>
 struct I8Stage<TY_Q6_K> {
     static constexpr int BB = 210;
-    static constexpr bool MINS = false;
+    static constexpr bool MINS = false, HDR = false;
     static constexpr int SHIFT = 7;
     struct Raw {
         uint32_t a[3], b[3], h[3];
@@ -216,7 +219,7 @@ struct I8Stage<TY_Q6_K> {
 template <>
 struct I8Stage<TY_IQ4_XS> {
     static constexpr int BB = 136;
-    static constexpr bool MINS = false;
+    static constexpr bool MINS = false, HDR = false;
     static constexpr int SHIFT = 7;
     struct Raw {
         uint2 h, q;
@@ -251,6 +254,23 @@ struct I8Stage<TY_IQ4_XS> {
 // ---------------------------------------------------------------- the GEMM
 // WI x 1 tiles of 32 x 32 per wave (tokens x rows); 4 waves, WT along the tokens and 4 / WT along the rows:
 // BT = 32 WI WT tokens and I8_N = 32 (4 / WT) weight rows a workgroup.
+// a stage type's super-block header, loaded once for its four stages (HDR), and its store with that header
+template <class S>
+__device__ __forceinline__ uint4 stage_hdr(const uint8_t *row, int s) {
+    if constexpr (S::HDR) return S::hdr(row, s);
+    else return make_uint4(0u, 0u, 0u, 0u);
+}
+template <class S>
+__device__ __forceinline__ void stage_store(const typename S::Raw &raw, uint4 h, int c, const WDst &o) {
+    if constexpr (S::HDR) {
+        typename S::Raw r = raw;
+        r.h = h;
+        S::store(r, c, o);
+    } else {
+        S::store(raw, c, o);
+    }
+}
+
 template <int WI, int WT>
 struct I8Geo {
     static_assert(32 * (4 / WT) == I8_N, "4 waves cover the workgroup's rows");
@@ -335,8 +355,12 @@ __global__ void __launch_bounds__(I8_THREADS, 2) k_gemm_i8kq(GemmArgs a) {
         float kv;
     };
     Pre P0, P1;
+    // (HDR) the header of the super-block being committed (Hc) and of the next one (Hn: loaded with its stage 0,
+    // which its commit reads; Hc takes it when that super-block's steps begin)
+    uint4 Hc = make_uint4(0u, 0u, 0u, 0u), Hn = Hc;
     auto issue = [&](auto cc, Pre &p, int s) {
         constexpr int c = decltype(cc)::value;
+        if constexpr (c == 0) Hn = stage_hdr<S>(wrow, s);
         S::load(wrow, s, c, p.raw);
 #pragma unroll
         for (int i = 0; i < XR; ++i) p.xv[i] = *(const uint4 *)(xsrc[i] + 256 * s + 64 * c);
@@ -361,7 +385,7 @@ __global__ void __launch_bounds__(I8_THREADS, 2) k_gemm_i8kq(GemmArgs a) {
         o.lo = o.hi + G::WB;
         o.dd = (float2 *)(smem + G::OFF_DD) + sb * I8_N;
         o.mn = (_Float16 *)(smem + G::OFF_MN) + sb * I8_N * 8;
-        S::store(p.raw, c, o);
+        stage_store<S>(p.raw, c == 0 ? Hn : Hc, c, o);
         if constexpr (c == 0) {
             if (son) {
                 if constexpr (MINS) {  // the 32-value sums of sub-blocks 4 (tid & 1) .. + 3
@@ -481,6 +505,7 @@ __global__ void __launch_bounds__(I8_THREADS, 2) k_gemm_i8kq(GemmArgs a) {
     commit(IC<0>{}, P0, 0);
     __syncthreads();
     for (int s = 0; s < nsb; ++s) {
+        Hc = Hn;  // (HDR only; otherwise dead)
         step(IC<0>{}, s);
         step(IC<1>{}, s);
         step(IC<2>{}, s);
