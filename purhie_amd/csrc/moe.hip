@@ -64,16 +64,14 @@ __global__ void __launch_bounds__(256) k_swiglu4(const float4 *__restrict__ g, c
     const int lane = threadIdx.x & 63;
     const int b0 = ((blockIdx.x * blockDim.x + threadIdx.x) >> 6) * BW, nb = (n + 255) / 256;
     float4 ga[BW], ua[BW];
+    // every lane loads (past the end: the last four values again, never used), so the loads have no branch around
+    // them and the waits count them exactly
+    const long long last4 = n / 4 - 1;
 #pragma unroll
     for (int k = 0; k < BW; ++k) {
         const long long i4 = (long long)(b0 + k) * 64 + lane;
-        if (b0 + k < nb && 4 * i4 < n) {
-            ga[k] = g[i4];
-            ua[k] = u[i4];
-        } else {
-            ga[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            ua[k] = ga[k];
-        }
+        ga[k] = g[i4 < last4 ? i4 : last4];
+        ua[k] = u[i4 < last4 ? i4 : last4];
     }
 #pragma unroll
     for (int k = 0; k < BW; ++k) {
