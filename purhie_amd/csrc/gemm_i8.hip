@@ -252,8 +252,6 @@ struct I8Stage<TY_IQ4_XS> {
 };
 
 // ---------------------------------------------------------------- the GEMM
-// WI x 1 tiles of 32 x 32 per wave (tokens x rows); 4 waves, WT along the tokens and 4 / WT along the rows:
-// BT = 32 WI WT tokens and I8_N = 32 (4 / WT) weight rows a workgroup.
 // a stage type's super-block header, loaded once for its four stages (HDR), and its store with that header
 template <class S>
 __device__ __forceinline__ uint4 stage_hdr(const uint8_t *row, int s) {
@@ -271,6 +269,8 @@ __device__ __forceinline__ void stage_store(const typename S::Raw &raw, uint4 h,
     }
 }
 
+// WI x 1 tiles of 32 x 32 per wave (tokens x rows); 4 waves, WT along the tokens and 4 / WT along the rows:
+// BT = 32 WI WT tokens and I8_N = 32 (4 / WT) weight rows a workgroup.
 template <int WI, int WT>
 struct I8Geo {
     static_assert(32 * (4 / WT) == I8_N, "4 waves cover the workgroup's rows");
